@@ -1,0 +1,168 @@
+"""Benchmark: coded-weight GB/s of the fused Huffman decode + Q4_K dequant + GEMV on Mistral-7B-shaped layers.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--m 1]
+
+Workload: per layer the matrices q 4096x4096, k, v 1024x4096, o 4096x4096, gate, up
+14336x4096, down 4096x14336, Q4_K coded (huf4p, one Huffman table per matrix, entropy 2.3 bits per code), fp16
+activations x ~ N(0, 1) resident in HBM, batch 1. L distinct layers (default 8, > 600 MB of coded weights, beyond
+the 256 MB Infinity Cache) are generated with their own seeds. A step = one pass over all L layers, each layer's
+seven GEMVs launched back to back (grouped per layer). value = algorithmic coded bytes per step / step time, where
+the algorithmic bytes of a GEMV are blob + side tensor + 2 K (x) + 4 m N (y) (the reference's own size
+accounting; device-layout padding is not credited).
+
+roofline: the dominant kernel (k_fused) timed with HIP events around each launch on its stream; achieved = the same
+algorithmic bytes / mean launch duration, peak = 8 TB/s. cpu_baseline: the oracle's restatement of the reference CPU
+path (cpu_decode, kernels/llmrt.cu:2513-2541, then dequant + fp32 GEMV) on layer 0, timed on this host.
+One JSON line on stdout.
+"""
+import argparse
+import json
+import os
+import shutil
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "coded-weight GB/s and % HBM roofline, fused decode+GEMV, Mistral-7B-shaped Q4_K"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=8)
+    ap.add_argument("--m", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--workdir", default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the path has no multi-GPU leg); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from lazyweights_amd import Runtime, bundle, load_library
+    from lazyweights_amd.configs import config2_layer
+
+    lib = load_library()
+    work = a.workdir or tempfile.mkdtemp(prefix="lw_bench_")
+    os.makedirs(work, exist_ok=True)
+    try:
+        t0 = time.time()
+        mats = [m for l in range(a.layers) for m in config2_layer(l)]
+        bundle.write_synthetic_bundle(work, mats, threads=16)
+        log("bench: generated %d layers in %.1f s" % (a.layers, time.time() - t0))
+        t0 = time.time()
+        rt = Runtime(work)
+        log("bench: opened (device layout built) in %.1f s; coded %.1f MB, device layout %.1f MB"
+            % (time.time() - t0, rt.stat("coded_bytes") / 1e6, rt.stat("device_bytes") / 1e6))
+        m = a.m
+        infos = [rt.info(mt[0]) for mt in mats]
+        algo = [inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m + 4 * m * inf["N"] for inf in infos]
+        bytes_per_step = float(sum(algo))
+        g = torch.Generator().manual_seed(0)
+        X = [torch.randn(m, inf["K"], generator=g).half().cuda() for inf in infos]
+        Y = [torch.zeros(m, inf["N"], device="cuda") for inf in infos]
+        import ctypes
+        n = len(mats)
+        names = (ctypes.c_char_p * n)(*[mt[0].encode() for mt in mats])
+        xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in X])
+        yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in Y])
+        stream = torch.cuda.current_stream().cuda_stream
+
+        per_layer = []
+        for l in range(a.layers):
+            sl = slice(7 * l, 7 * l + 7)
+            per_layer.append(((ctypes.c_char_p * 7)(*names[sl]), (ctypes.c_void_p * 7)(*xp[sl]),
+                              (ctypes.c_void_p * 7)(*yp[sl])))
+
+        def step():
+            for nm, xx, yy in per_layer:
+                if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, m, yy, stream) != 0:
+                    raise RuntimeError(lib.lw_last_error().decode())
+
+        for _ in range(a.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            step()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
+        value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+        log("bench: %.3f ms per step (%d GEMVs), %.1f GB/s coded" % (ms_per_step, n, value))
+
+        # dominant kernel: HIP events around each fused launch, on the library's stream
+        sizes = (ctypes.c_int * a.layers)(*([7] * a.layers))
+        out = (ctypes.c_double * 3)()
+        rc = lib.lw_bench_groups(rt.h, a.layers, sizes, names, xp, m, yp, 1, max(3, a.steps // 2), out)
+        if rc != 0:
+            raise RuntimeError(lib.lw_last_error().decode())
+        kernel_ms_per_pass = out[1]
+        launches = int(out[2])
+        kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
+        achieved = kbytes / (kernel_ms_per_pass * 1e-3) / 1e9
+        log("bench: fused kernels %.3f ms per pass (%d launches, mean %.1f us), %.1f GB/s"
+            % (kernel_ms_per_pass, launches, kernel_ms_per_pass * 1e3 / launches, achieved))
+        ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
+        log("bench: streaming-read control %.1f GB/s" % ctrl)
+
+        cpu = None
+        if not a.no_cpu:
+            from oracle import oracle as orc
+            threads = min(16, len(os.sched_getaffinity(0)))
+            cfg, ts = bundle.read_manifest(work)
+            by = {t["name"]: t for t in ts}
+            layer0 = config2_layer(0)
+            blobs = [(bundle.read_tensor(work, by[nm]), bundle.read_tensor(work, by[nm + ".kqs"]), N, K)
+                     for nm, _, N, K, _, _ in layer0]
+            xs = [X[i][0].float().cpu().numpy() for i in range(7)]
+            sample_bytes = sum(len(b) + len(s) + 2 * K + 4 * N for b, s, N, K in blobs)
+            reps, t_cpu = 0, 0.0
+            while t_cpu < a.cpu_seconds and reps < 1000:
+                t0 = time.perf_counter()
+                for (b, s, N, K), x in zip(blobs, xs):
+                    orc.decode_gemv(1, b, s, N, K, x, threads)
+                t_cpu += time.perf_counter() - t0
+                reps += 1
+            cpu_gbs = sample_bytes * reps / t_cpu / 1e9
+            cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+                   "sample": "layer 0 of the workload (7 matrices, %.1f MB coded), %d passes, %.1f s; "
+                             "oracle cpu_decode + dequant + fp32 GEMV" % (sample_bytes / 1e6, reps, t_cpu)}
+            log("bench: cpu baseline %.2f GB/s on %d threads" % (cpu_gbs, threads))
+
+        res = {
+            "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp16*fp16->fp32", "data": "synthetic",
+            "config": {"workload": "config2: Mistral-7B-shaped Q4_K layers (q,k,v,o,gate,up,down), H=2.3 bits/code, "
+                                   "fp16 x, batch %d, %d distinct layers per step, grouped per layer" % (m, a.layers),
+                       "layers": a.layers, "m": m, "coded_bytes_per_step": int(bytes_per_step),
+                       "hbm_fraction": round(value / HBM_PEAK_GBS, 4)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "k_fused", "mean_launch_us": round(kernel_ms_per_pass * 1e3 / launches, 2)},
+            "cpu_baseline": cpu,
+            "control_stream_read_GBps": round(ctrl, 1),
+        }
+        print(json.dumps(res), flush=True)
+        rt.close()
+    finally:
+        if not a.workdir:
+            shutil.rmtree(work, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    main()

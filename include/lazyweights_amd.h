@@ -1,0 +1,125 @@
+/* lazyweights_amd — C-ABI of the MI355X-native decode-on-demand weight path.
+ *
+ * Drop-in for the reference runtime's matmul/decode exports (kernels/llmrt.cu extern "C" block, lines 1916-2575):
+ * same names, argument meaning and return codes. Host buffers are caller-owned; the handle is opaque and owned
+ * by the library until rt_close. Not thread-safe per handle (as the reference).
+ *
+ * Accepted bundles: a directory with manifest.txt + weights.bin (lazyweights/bundle.py:10-21). Coded matrices
+ * enc huf8 / huf4p (and the reference's pre-interleaved huf8_il / huf8_ilc / huf4p_il / huf4p_ilc exports), each
+ * with a K-quant side tensor <name>.kqs (enc kq_Q4_K | kq_Q5_K | kq_Q6_K | kq_IQ4_XS) for the fused GEMV.
+ * Matrix-only bundles (no model cfg keys) open. Errors never exit the process: functions return nullptr / -1 and
+ * lw_last_error() describes the failure.
+ */
+#ifndef LAZYWEIGHTS_AMD_H
+#define LAZYWEIGHTS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── reference-compatible entry points ─────────────────────────────────────────────────────────────────── */
+
+/* Replaces rt_open (kernels/llmrt.cu:1921). Opens a bundle; coded matrices are re-laid out for the GPU and made
+ * resident while budget_mb (< 0: unlimited) and the host MemAvailable floor (floor_mb) allow. budget_mb == 0 keeps
+ * everything on the host: no GPU is touched, CPU entry points still work. max_ctx / max_batch are accepted and
+ * ignored (no model runtime). Returns nullptr on a missing or malformed manifest / weights.bin. */
+void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, int floor_mb, int verbose);
+
+/* Replaces rt_close (kernels/llmrt.cu:2239). */
+void rt_close(void* h);
+
+/* Replaces rt_test_matmul (kernels/llmrt.cu:2441): Y[m, N] = X[m, K] @ dequant(W)^T for tensor `name`, host X (fp32)
+ * and host Y. path 0 = auto (fused if m <= 8), 1 = fused, 2 = decode into scratch + GEMM. Returns 0, or -1 when the
+ * tensor is missing, not resident or not a K-quant coded matrix. */
+int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, int path);
+
+/* Replaces rt_test_decode (kernels/llmrt.cu:2461): GPU decode to host codes [N, K] (one byte per weight, pair
+ * symbols unpacked low nibble first, no add for K-quants); raw8 tensors are copied. -1 if not resident. */
+int rt_test_decode(void* h, const char* name, uint8_t* out);
+
+/* Replaces rt_gpu_decode_all (kernels/llmrt.cu:2482): GPU decode of every resident coded matrix; median seconds of
+ * `reps` event-timed passes. */
+double rt_gpu_decode_all(void* h, int reps);
+
+/* Replaces rt_test_cpu_decode (kernels/llmrt.cu:2543): CPU decode of the raw blob to symbols [N, KS]
+ * (KS = K / 2 for huf4p), `threads` workers. -1 for pre-interleaved or non-coded tensors. */
+int rt_test_cpu_decode(void* h, const char* name, int threads, uint8_t* out);
+
+/* Replaces rt_cpu_decode_all (kernels/llmrt.cu:2558): CPU decode of every coded matrix, blobs read first (untimed);
+ * returns decode seconds, *symbols = symbols decoded. */
+double rt_cpu_decode_all(void* h, int threads, long long* symbols);
+
+/* Replaces rt_stat (kernels/llmrt.cu:2276). Keys of the reference: resident_bytes, streamed_bytes, stream_wait_s,
+ * stream_bytes_moved, mem_available_mb, n_streamed, graph_launches, graph_captures; plus coded_bytes (algorithmic
+ * bytes of the resident coded matrices: blob + side tensor), device_bytes (their device layout), pad_bytes
+ * (device layout bytes beyond the blob payload). Unknown keys: -1. */
+double rt_stat(void* h, const char* key);
+
+/* Model-runtime entries of the reference (kernels/llmrt.cu:2269-2291). This library holds matrices, not a model:
+ * rt_forward returns -1; rt_vocab returns 0; the others keep a position counter only. */
+int rt_forward(void* h, const int* ids, int n, float* logits, int all_logits);
+void rt_reset(void* h);
+void rt_set_window(void* h, int w);
+void rt_set_pos(void* h, int p);
+int rt_pos(void* h);
+int rt_vocab(void* h);
+
+/* ── extensions (no counterpart in the reference) ──────────────────────────────────────────────────────── */
+
+/* Last error message of the calling thread ("" if none). */
+const char* lw_last_error(void);
+
+/* Shape and byte counts of a tensor: out[0] N, out[1] K, out[2] kqt (0 none, 1 Q4_K, 2 Q5_K, 3 Q6_K, 4 IQ4_XS),
+ * out[3] symbol bits (4 or 8), out[4] blob bytes, out[5] side bytes, out[6] device layout bytes, out[7] tiles,
+ * out[8] resident (0/1). Returns -1 if absent. */
+int lw_tensor_info(void* h, const char* name, int64_t* out);
+
+/* Device-pointer GEMV / skinny GEMM on `stream` (a hipStream_t; NULL = the null stream), no host copies, no
+ * synchronisation: Y[m, N] (row stride ldy) = X[m, K] @ dequant(W)^T. X is fp16 (x_f16 = 1, the headline path) or
+ * fp32 (x_f16 = 0: split into fp16 hi + lo). m <= 8 (fp32) or <= 16 (fp16). Returns 0 or -1. */
+int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy, void* stream);
+
+/* Several independent matmuls (e.g. the matrices of one decoder layer), each with its own fp16 activations X[i]
+ * [m, K_i] and output Y[i] [m, N_i], launched back to back on `stream`. Returns 0 or -1. */
+int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
+                        float* const* Y, void* stream);
+
+/* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in
+ * names/X/Y (group g has sizes[g] matrices), cycling through the groups, with HIP events on the launch stream.
+ * out[0] = mean ms per pass over all groups, out[1] = mean ms per fused-kernel launch set (decode + GEMV kernels
+ * only, events around each group's fused launches), out[2] = number of fused launches per pass. */
+int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* names, const void* const* X, int m,
+                    float* const* Y, int warmup, int iters, double* out);
+
+/* Achievable HBM read bandwidth (GB/s): streaming 16-byte reads over `bytes` of device memory, median of reps. */
+double lw_stream_read_gbps(long long bytes, int reps);
+
+/* Synthetic data and bundles (test / bench inputs). */
+/* codes [N, K] (one byte per weight) and side bytes [N, K / 256 * SB]; seeded; independent of `threads`. */
+int lw_synth_matrix(int kqt, int N, int K, double entropy, uint64_t seed, uint8_t* codes, uint8_t* side, int threads);
+/* codes -> symbols [N, KS] (pairs for Q4_K / IQ4_XS). */
+int lw_form_symbols(int kqt, const uint8_t* codes, int N, int K, uint8_t* sym);
+/* Encode symbols [N, KS] as a huf8/huf4p blob (lazyweights/bundle.py:57-85). Returns the blob size; writes it
+ * to `blob` when cap is large enough; *bits = payload bits. -1 on bad shapes. */
+long long lw_encode(const uint8_t* sym, int N, int KS, uint8_t* blob, long long cap, uint64_t* bits);
+/* Write a bundle directory of `count` synthetic K-quant matrices (each with its .kqs side tensor). */
+int lw_write_bundle(const char* dir, int count, const char* const* names, const int* kqts, const int* Ns,
+                    const int* Ks, const double* entropies, const uint64_t* seeds, int threads);
+
+/* Huffman code lengths of a histogram (n <= 256 symbols): lmax > 0 gives the length-limited lengths of
+ * lazyweights/lanecodecs.py:28-38, lmax <= 0 the plain heap lengths of lazyweights/huffman.py:8-26. */
+int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L);
+
+/* The device layout this library builds from a blob at load time (host-side, for inspection and tests): fills tbase
+ * [T], mid [T * 32], rows [T] and, when words_cap is large enough, words; returns the word count (-1 on a bad or
+ * corrupt blob). pre_il / compact select the reference's pre-interleaved export formats (_il / _ilc). */
+long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,
+                          uint16_t* mid, uint16_t* rows, uint32_t* words, long long words_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAZYWEIGHTS_AMD_H */

@@ -1,0 +1,116 @@
+"""Bundle directories and coded blobs, with the reference's Python names (lazyweights/bundle.py).
+
+Writer / read_manifest follow lazyweights/bundle.py:114-148 (manifest.txt + weights.bin, every blob 256-byte
+aligned). encode_huf8 produces the same blob bytes as lazyweights/bundle.py:57-85 (checked byte for byte against
+fixtures written by the reference encoder), computed by the C++ codec of this library.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from ._lib import last_error, load_library
+
+TN, TK, LMAX, LANES = 64, 256, 11, 32
+ALIGN = 256
+KQ = {"Q4_K": 1, "Q5_K": 2, "Q6_K": 3, "IQ4_XS": 4}
+KQ_NAME = {v: k for k, v in KQ.items()}
+SIDE_BYTES = {1: 16, 2: 16, 3: 18, 4: 8}       # per 256-weight super-block
+SYMBITS = {1: 4, 2: 8, 3: 8, 4: 4}             # 4: two codes per symbol (huf4p), 8: one (huf8)
+
+
+def encode_huf8(sym):
+    """uint8 symbols [N, KS] -> (blob bytes, payload bits)."""
+    sym = np.ascontiguousarray(sym, np.uint8)
+    N, KS = sym.shape
+    lib = load_library()
+    bits = ctypes.c_uint64(0)
+    n = lib.lw_encode(sym.ctypes.data, N, KS, None, 0, ctypes.byref(bits))
+    if n < 0:
+        raise ValueError("encode_huf8: shape %s is not a whole number of 64 x 256 tiles" % (sym.shape,))
+    out = np.zeros(n, np.uint8)
+    lib.lw_encode(sym.ctypes.data, N, KS, out.ctypes.data, n, ctypes.byref(bits))
+    return out.tobytes(), int(bits.value)
+
+
+def synth_matrix(kqt, N, K, entropy, seed, threads=8):
+    """Seeded synthetic K-quant matrix: (codes [N, K] uint8, side bytes [N, K / 256 * SB] uint8)."""
+    codes = np.zeros((N, K), np.uint8)
+    side = np.zeros((N, K // 256 * SIDE_BYTES[kqt]), np.uint8)
+    if load_library().lw_synth_matrix(kqt, N, K, float(entropy), int(seed), codes.ctypes.data, side.ctypes.data,
+                                      threads) != 0:
+        raise ValueError("synth_matrix: bad arguments")
+    return codes, side
+
+
+def form_symbols(kqt, codes):
+    """codes [N, K] -> symbols [N, KS] (scripts/a2_kq_bundle.py:108: pair = q[2c] | q[2c + 1] << 4)."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    if SYMBITS[kqt] == 8:
+        return codes.copy()
+    return (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+
+
+class Writer:
+    def __init__(self, path):
+        os.makedirs(path, exist_ok=True)
+        self.path = path
+        self.f = open(os.path.join(path, "weights.bin"), "wb")
+        self.lines = []
+        self.off = 0
+
+    def cfg(self, k, v):
+        self.lines.append("cfg %s %s" % (k, v))
+
+    def add(self, name, enc, N, K, scale, zp, blob):
+        pad = (-self.off) % ALIGN
+        self.f.write(b"\0" * pad)
+        self.off += pad
+        self.f.write(blob)
+        self.lines.append("t %s %s %d %d %.9g %d %d %d" % (name, enc, N, K, scale, zp, self.off, len(blob)))
+        self.off += len(blob)
+
+    def add_kquant(self, name, kqt, codes, side):
+        """A K-quant matrix as the reference bundler writes it (scripts/a2_kq_bundle.py:216-218)."""
+        N, K = codes.shape
+        blob, _ = encode_huf8(form_symbols(kqt, codes))
+        self.add(name, "huf4p" if SYMBITS[kqt] == 4 else "huf8", N, K, 1.0, 0, blob)
+        self.add(name + ".kqs", "kq_" + KQ_NAME[kqt], N, side.shape[1], 1.0, 0, np.ascontiguousarray(side).tobytes())
+
+    def close(self):
+        self.f.close()
+        with open(os.path.join(self.path, "manifest.txt"), "w") as f:
+            f.write("\n".join(self.lines) + "\n")
+
+
+def read_manifest(path):
+    cfg, ts = {}, []
+    for line in open(os.path.join(path, "manifest.txt")):
+        p = line.split()
+        if p and p[0] == "cfg":
+            cfg[p[1]] = p[2]
+        elif p and p[0] == "t":
+            ts.append(dict(name=p[1], enc=p[2], N=int(p[3]), K=int(p[4]), scale=float(p[5]), zp=int(p[6]),
+                           offset=int(p[7]), nbytes=int(p[8])))
+    return cfg, ts
+
+
+def read_tensor(path, t):
+    with open(os.path.join(path, "weights.bin"), "rb") as f:
+        f.seek(t["offset"])
+        return np.frombuffer(f.read(t["nbytes"]), np.uint8)
+
+
+def write_synthetic_bundle(path, mats, threads=16):
+    """Fast all-C++ writer: mats = [(name, kqt, N, K, entropy, seed), ...]."""
+    n = len(mats)
+    names = (ctypes.c_char_p * n)(*[m[0].encode() for m in mats])
+    kq = (ctypes.c_int * n)(*[m[1] for m in mats])
+    Ns = (ctypes.c_int * n)(*[m[2] for m in mats])
+    Ks = (ctypes.c_int * n)(*[m[3] for m in mats])
+    Hs = (ctypes.c_double * n)(*[float(m[4]) for m in mats])
+    seeds = (ctypes.c_uint64 * n)(*[int(m[5]) for m in mats])
+    rc = load_library().lw_write_bundle(str(path).encode(), n, names, kq, Ns, Ks, Hs, seeds, threads)
+    if rc != 0:
+        raise RuntimeError("lw_write_bundle failed: " + last_error())
+    return path

@@ -1,0 +1,45 @@
+// Device-side matrix descriptor and kernel launchers (host interface of lw_kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lw {
+
+// One coded matrix resident in HBM, in the device layout built by the runtime at load time:
+//   lut   u16[2048]            the bundle's decode table (sym | len << 8)
+//   tbase u32[T]               word index (into words) of tile t's first word row
+//   mid   u16[T][32]           bit offset, within lane l's stream, of the lane's second row (symbol 256)
+//   words u32[...]             tile t: word i of lane l at tbase[t] + 32 i + l, i < rows[t]; every lane starts at
+//                              bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
+//   side  u8[N][K/256][SB]     K-quant side bytes as in the bundle's <name>.kqs
+struct DevMat {
+  const uint16_t* lut;
+  const uint32_t* tbase;
+  const uint16_t* mid;
+  const uint16_t* rows;
+  const uint32_t* words;
+  const uint8_t* side;
+  int N, K;         // weights
+  int kqt;          // 1 Q4_K, 2 Q5_K, 3 Q6_K, 4 IQ4_XS (0: none -> decode only)
+  int symbits;      // 4 (huf4p) or 8 (huf8)
+  int KT, NT;       // tile columns, tile rows
+  int max_rows;     // max over tiles of rows[t]
+};
+
+// X16 [mt][K] fp16 (mt pseudo-tokens); P [KT][mt][N] fp32 per-tile-column partials.
+hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
+// Y[j][n] (row stride ldy) = sum over tile columns tc (in order) of P[tc][jj][n], jj over `per` pseudo-tokens of
+// token j (per = 1: fp16 activations; per = 2: fp32 activations split into fp16 hi + lo).
+hipError_t launch_reduce(const float* P, float* Y, int m, int per, int N, int ldy, int KT, hipStream_t s);
+// fp32 X [m][K] -> fp16 X16 [2m][K] (row 2j = hi, 2j + 1 = lo = x - hi)
+hipError_t launch_split_x(const float* X, void* X16, int m, int K, hipStream_t s);
+// codes [N][K] (one byte per weight) for tile rows [tr0, tr1)
+hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s);
+// simple K-quant GEMM from decoded codes (m > 8 or path 2): Y[m][N] = X[m][K] dequant(codes, side)^T
+hipError_t launch_gemm_codes(const DevMat& M, const uint8_t* codes, int row0, int nrows, const float* X, int m,
+                             float* Y, int ldy, hipStream_t s);
+// streaming read of n16 16-byte words (achievable HBM bandwidth control); out gets one value per block
+hipError_t launch_stream_read(const void* src, size_t n16, float* out, int blocks, hipStream_t s);
+
+}  // namespace lw

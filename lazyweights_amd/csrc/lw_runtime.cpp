@@ -1,0 +1,747 @@
+// Runtime and C-ABI of the decode-on-demand weight path (include/lazyweights_amd.h).
+//
+// Reference counterparts (kernels/llmrt.cu): rt_open 1921-2237 (manifest, residency, interleave at load, .kqs side
+// tensors), matmul() K-quant branch 1806-1842, rt_test_matmul 2441, rt_test_decode 2461, rt_gpu_decode_all 2482,
+// cpu_decode / rt_test_cpu_decode / rt_cpu_decode_all 2513-2573, rt_stat 2276. Differences by design: no exit() on
+// bad input (error codes + lw_last_error), matrix-only bundles open, the device layout is this library's own
+// (lw_kernels.h), and there is no model runtime or weight streaming.
+#include <fcntl.h>
+#include <hip/hip_runtime.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/lazyweights_amd.h"
+#include "lw_codec.h"
+#include "lw_format.h"
+#include "lw_kernels.h"
+#include "lw_layout.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+bool fail(const std::string& m) {
+  g_err = m;
+  return false;
+}
+
+#define HIPCHECK(x)                                                                                  \
+  do {                                                                                               \
+    hipError_t e_ = (x);                                                                             \
+    if (e_ != hipSuccess) {                                                                          \
+      g_err = std::string("HIP error ") + hipGetErrorString(e_) + " at " + __FILE__ + ":" + std::to_string(__LINE__); \
+      return -1;                                                                                     \
+    }                                                                                                \
+  } while (0)
+
+long long meminfo_kb(const char* key) {
+  FILE* f = fopen("/proc/meminfo", "r");
+  if (!f) return -1;
+  char k[64];
+  long long v = -1, x;
+  while (fscanf(f, "%63s %lld kB", k, &x) == 2)
+    if (!strncmp(k, key, strlen(key)) && k[strlen(key)] == ':') {
+      v = x;
+      break;
+    }
+  fclose(f);
+  return v;
+}
+
+bool pread_all(int fd, void* buf, size_t n, uint64_t off) {
+  uint8_t* p = static_cast<uint8_t*>(buf);
+  while (n) {
+    const ssize_t r = pread(fd, p, n, (off_t)off);
+    if (r <= 0) return false;
+    p += r;
+    n -= (size_t)r;
+    off += (uint64_t)r;
+  }
+  return true;
+}
+
+struct Tensor {
+  std::string name, enc;
+  long long N = 0, K = 0;
+  double scale = 1.0;
+  long long zp = 0;
+  uint64_t off = 0, nbytes = 0;
+  bool pre_il = false, compact = false;
+  int symbits = 8, kqt = 0;
+  int side_idx = -1;
+  bool resident = false;
+  void* dev = nullptr;  // device layout (one allocation)
+  size_t dev_bytes = 0;
+  uint8_t* dside = nullptr;
+  size_t side_bytes = 0;
+  uint64_t payload_bits = 0;
+  lw::DevMat dm{};
+  bool coded() const { return enc == "huf8" || enc == "huf4p"; }
+  int KS() const { return (int)(symbits == 4 ? K / 2 : K); }
+  int T() const { return (int)((N / lw::TN) * (KS() / lw::TK)); }
+};
+
+struct Model {
+  std::string dir;
+  std::map<std::string, std::string> cfg;
+  std::vector<Tensor> ts;
+  std::map<std::string, int> by_name;
+  int fd = -1;
+  uint64_t file_size = 0;
+  bool gpu = false;
+  hipStream_t stream = nullptr;
+  size_t resident_bytes = 0, coded_bytes = 0, device_bytes = 0, pad_bytes = 0;
+  long long avail_after_kb = -1;
+  int pos = 0, window = 0;
+  // device scratch, grown on demand
+  float* P = nullptr;
+  size_t P_cap = 0;
+  uint16_t* X16 = nullptr;
+  size_t X16_cap = 0;
+  uint8_t* codes = nullptr;
+  size_t codes_cap = 0;
+  int verbose = 0;
+  Tensor* find(const char* name) {
+    if (!name) return nullptr;
+    auto it = by_name.find(name);
+    return it == by_name.end() ? nullptr : &ts[it->second];
+  }
+};
+
+bool ends_with(const std::string& s, const std::string& x) {
+  return s.size() > x.size() && !s.compare(s.size() - x.size(), x.size(), x);
+}
+
+template <class T>
+int grow(T*& p, size_t& cap, size_t bytes) {
+  if (bytes <= cap) return 0;
+  if (p) (void)hipFree(p);
+  p = nullptr;
+  cap = 0;
+  HIPCHECK(hipMalloc(reinterpret_cast<void**>(&p), bytes));
+  cap = bytes;
+  return 0;
+}
+
+// ── load ─────────────────────────────────────────────────────────────────────────────────────────────────
+
+bool parse_manifest(Model& M) {
+  std::ifstream mf(M.dir + "/manifest.txt");
+  if (!mf) return fail("cannot open " + M.dir + "/manifest.txt");
+  std::string line;
+  int ln = 0;
+  while (std::getline(mf, line)) {
+    ++ln;
+    std::istringstream is(line);
+    std::string tag;
+    if (!(is >> tag)) continue;
+    if (tag == "cfg") {
+      std::string k, v;
+      if (!(is >> k >> v)) return fail("manifest line " + std::to_string(ln) + ": bad cfg line");
+      M.cfg[k] = v;
+    } else if (tag == "t") {
+      Tensor t;
+      if (!(is >> t.name >> t.enc >> t.N >> t.K >> t.scale >> t.zp >> t.off >> t.nbytes))
+        return fail("manifest line " + std::to_string(ln) + ": bad tensor line");
+      for (const char* x : {"_ilc", "_il"}) {  // pre-interleaved export (kernels/llmrt.cu:1938-1947)
+        if (ends_with(t.enc, x)) {
+          t.enc.resize(t.enc.size() - strlen(x));
+          t.pre_il = true;
+          t.compact = x[3] == 'c';
+          break;
+        }
+      }
+      if (t.N <= 0 || t.K <= 0) return fail("manifest line " + std::to_string(ln) + ": non-positive shape");
+      t.symbits = t.enc == "huf4p" || t.enc == "pk4" ? 4 : 8;
+      if (M.by_name.count(t.name)) return fail("manifest: duplicate tensor " + t.name);
+      M.by_name[t.name] = (int)M.ts.size();
+      M.ts.push_back(t);
+    }
+  }
+  return true;
+}
+
+bool validate(Model& M) {
+  static const char* kn[] = {"", "kq_Q4_K", "kq_Q5_K", "kq_Q6_K", "kq_IQ4_XS"};
+  for (auto& t : M.ts) {
+    if (t.off + t.nbytes > M.file_size)
+      return fail(t.name + ": extends past the end of weights.bin");
+    if (!t.coded()) continue;
+    if (t.N % lw::TN || t.K % (t.symbits == 4 ? 2 * lw::TK : lw::TK))
+      return fail(t.name + ": shape " + std::to_string(t.N) + "x" + std::to_string(t.K) +
+                  " is not a whole number of 64 x 256-symbol tiles");
+    if (t.K >= (1ll << 31) || t.N >= (1ll << 31)) return fail(t.name + ": shape too large");
+    auto it = M.by_name.find(t.name + ".kqs");
+    if (it == M.by_name.end()) continue;  // decode-only matrix (no K-quant side bytes)
+    const Tensor& x = M.ts[it->second];
+    int kqt = 0;
+    for (int i = 1; i <= 4; ++i)
+      if (x.enc == kn[i]) kqt = i;
+    if (!kqt) return fail(t.name + ": side tensor " + x.name + " has unknown enc " + x.enc);
+    if (x.N != t.N || x.K != (t.K / 256) * lw::kq_sbytes(kqt) || x.nbytes < (uint64_t)x.N * x.K)
+      return fail(t.name + ": side tensor " + x.name + " shape does not match the matrix");
+    if (t.symbits != lw::kq_symbits(kqt))
+      return fail(t.name + ": " + x.enc + " needs enc " + (lw::kq_symbits(kqt) == 4 ? "huf4p" : "huf8"));
+    t.kqt = kqt;
+    t.side_idx = it->second;
+  }
+  return true;
+}
+
+// Build and upload the device layout (and side bytes) of a coded tensor.
+bool make_resident(Model& M, Tensor& t, int threads) {
+  std::vector<uint8_t> blob(t.nbytes + 16, 0);
+  if (!pread_all(M.fd, blob.data(), t.nbytes, t.off)) return fail(t.name + ": read error");
+  lw::Layout L;
+  std::string err;
+  const bool ok = t.pre_il ? lw::build_layout_il(blob.data(), t.nbytes, (int)t.N, t.KS(), t.compact, threads, L, err)
+                           : lw::build_layout_raw(blob.data(), t.nbytes, (int)t.N, t.KS(), threads, L, err);
+  if (!ok) return fail(t.name + ": " + err);
+  std::vector<uint8_t>().swap(blob);
+  const int T = t.T();
+  // [lut 4096 B][tbase 4T][mid 64T][rows 2T] padded to 256 B, then the words
+  const size_t o_tb = 2 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
+  const size_t o_words = (o_rows + 2ull * T + 255) & ~(size_t)255;
+  const size_t bytes = o_words + 4 * L.words.size();
+  std::vector<uint8_t> host(o_words, 0);
+  memcpy(host.data(), L.lut, 2 * lw::LUTN);
+  memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
+  memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
+  memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
+  void* d = nullptr;
+  if (hipMalloc(&d, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(t.name + ": device allocation failed");
+  }
+  if (hipMemcpy(d, host.data(), o_words, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(static_cast<uint8_t*>(d) + o_words, L.words.data(), 4 * L.words.size(), hipMemcpyHostToDevice) !=
+          hipSuccess) {
+    (void)hipFree(d);
+    return fail(t.name + ": upload failed");
+  }
+  t.dev = d;
+  t.dev_bytes = bytes;
+  t.payload_bits = L.payload_bits;
+  lw::DevMat& dm = t.dm;
+  uint8_t* b = static_cast<uint8_t*>(d);
+  dm.lut = reinterpret_cast<const uint16_t*>(b);
+  dm.tbase = reinterpret_cast<const uint32_t*>(b + o_tb);
+  dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
+  dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
+  dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
+  dm.side = nullptr;
+  dm.N = (int)t.N;
+  dm.K = (int)t.K;
+  dm.kqt = t.kqt;
+  dm.symbits = t.symbits;
+  dm.KT = t.KS() / lw::TK;
+  dm.NT = (int)(t.N / lw::TN);
+  dm.max_rows = L.max_rows;
+  if (t.kqt) {
+    const Tensor& x = M.ts[t.side_idx];
+    t.side_bytes = (size_t)x.N * x.K;
+    std::vector<uint8_t> sb(t.side_bytes);
+    if (!pread_all(M.fd, sb.data(), t.side_bytes, x.off)) return fail(t.name + ": side read error");
+    if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(t.name + ": device allocation failed (side)");
+    }
+    if (hipMemcpy(t.dside, sb.data(), t.side_bytes, hipMemcpyHostToDevice) != hipSuccess)
+      return fail(t.name + ": upload failed (side)");
+    dm.side = t.dside;
+  }
+  t.resident = true;
+  M.resident_bytes += bytes + t.side_bytes;
+  M.device_bytes += bytes;
+  M.coded_bytes += t.nbytes + t.side_bytes;
+  const size_t blob_pay = (size_t)((t.payload_bits + 31) / 32) * 4;
+  M.pad_bytes += bytes > blob_pay ? bytes - blob_pay : 0;
+  return true;
+}
+
+void release(Model* M) {
+  if (!M) return;
+  for (auto& t : M->ts) {
+    if (t.dev) (void)hipFree(t.dev);
+    if (t.dside) (void)hipFree(t.dside);
+  }
+  if (M->P) (void)hipFree(M->P);
+  if (M->X16) (void)hipFree(M->X16);
+  if (M->codes) (void)hipFree(M->codes);
+  if (M->stream) (void)hipStreamDestroy(M->stream);
+  if (M->fd >= 0) close(M->fd);
+  delete M;
+}
+
+// ── matmul ───────────────────────────────────────────────────────────────────────────────────────────────
+
+int check_matmul(Tensor* t, const char* name) {
+  if (!t) {
+    g_err = std::string("no tensor ") + (name ? name : "(null)");
+    return -1;
+  }
+  if (!t->resident) {
+    g_err = t->name + ": not resident";
+    return -1;
+  }
+  if (!t->kqt) {
+    g_err = t->name + ": not a K-quant coded matrix (no .kqs side tensor)";
+    return -1;
+  }
+  return 0;
+}
+
+// fused path on device buffers: X16 [mt][K] fp16 pseudo-tokens, per = pseudo-tokens per output token
+int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, int ldy, hipStream_t s) {
+  const int mt = m * per;
+  if (grow(M.P, M.P_cap, (size_t)t.dm.KT * mt * t.N * sizeof(float))) return -1;
+  HIPCHECK(lw::launch_fused(t.dm, X16, mt, M.P, s));
+  HIPCHECK(lw::launch_reduce(M.P, Y, m, per, (int)t.N, ldy, t.dm.KT, s));
+  return 0;
+}
+
+// decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
+int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
+  const size_t row_bytes = (size_t)lw::TN * t.K;
+  const size_t cap = std::max(row_bytes, std::min<size_t>((size_t)t.N * t.K, (size_t)64 << 20));
+  if (grow(M.codes, M.codes_cap, cap)) return -1;
+  const int rows_fit = (int)std::max<size_t>(1, M.codes_cap / row_bytes);
+  for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit) {
+    const int tr1 = std::min(t.dm.NT, tr0 + rows_fit);
+    HIPCHECK(lw::launch_decode(t.dm, M.codes, tr0, tr1, s));
+    HIPCHECK(lw::launch_gemm_codes(t.dm, M.codes, tr0 * lw::TN, (tr1 - tr0) * lw::TN, X, m, Y, ldy, s));
+  }
+  return 0;
+}
+
+}  // namespace
+
+// ── C-ABI ────────────────────────────────────────────────────────────────────────────────────────────────
+
+extern "C" {
+
+const char* lw_last_error(void) { return g_err.c_str(); }
+
+void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, int floor_mb, int verbose) {
+  (void)max_ctx;
+  (void)max_batch;
+  g_err.clear();
+  if (!dir) {
+    fail("rt_open: null directory");
+    return nullptr;
+  }
+  std::unique_ptr<Model> M(new Model());
+  M->dir = dir;
+  M->verbose = verbose;
+  if (!parse_manifest(*M)) return nullptr;
+  M->fd = open((M->dir + "/weights.bin").c_str(), O_RDONLY);
+  if (M->fd < 0) {
+    fail("cannot open " + M->dir + "/weights.bin");
+    return nullptr;
+  }
+  struct stat st;
+  if (fstat(M->fd, &st)) {
+    fail("cannot stat weights.bin");
+    release(M.release());
+    return nullptr;
+  }
+  M->file_size = (uint64_t)st.st_size;
+  if (!validate(*M)) {
+    release(M.release());
+    return nullptr;
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+  if (budget_mb != 0) {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) {
+      (void)hipGetLastError();
+      fail("rt_open: no GPU (open with budget_mb = 0 for CPU-only use)");
+      release(M.release());
+      return nullptr;
+    }
+    if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess) {
+      fail("rt_open: stream creation failed");
+      release(M.release());
+      return nullptr;
+    }
+    M->gpu = true;
+    const int threads = lw::default_threads();
+    const long long floor_kb = (long long)floor_mb * 1024;
+    size_t used = 0;
+    for (auto& t : M->ts) {
+      if (!t.coded()) continue;
+      if (budget_mb > 0 && used + t.nbytes > (size_t)budget_mb * 1048576ull) break;  // forward order: stop
+      if (floor_mb > 0 && meminfo_kb("MemAvailable") - (long long)(t.nbytes >> 10) < floor_kb) break;
+      if (!make_resident(*M, t, threads)) {
+        release(M.release());
+        return nullptr;
+      }
+      used += t.dev_bytes + t.side_bytes;
+    }
+  }
+  M->avail_after_kb = meminfo_kb("MemAvailable");
+  if (verbose)
+    fprintf(stderr, "[lazyweights_amd] %s: %zu tensors, resident %.1f MB (coded %.1f MB, layout padding %.1f MB), "
+                    "load %.2f s\n",
+            dir, M->ts.size(), M->resident_bytes / 1e6, M->coded_bytes / 1e6, M->pad_bytes / 1e6,
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+  return M.release();
+}
+
+void rt_close(void* h) { release(static_cast<Model*>(h)); }
+
+int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, int path) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !X || !Y || m < 1) {
+    g_err = "rt_test_matmul: bad arguments";
+    return -1;
+  }
+  Tensor* t = M->find(name);
+  if (check_matmul(t, name)) return -1;
+  const size_t K = (size_t)t->K, N = (size_t)t->N;
+  float *dx = nullptr, *dy = nullptr;
+  void* dx16 = nullptr;
+  int rc = 0;
+  auto cleanup = [&]() {
+    if (dx) (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (dx16) (void)hipFree(dx16);
+  };
+  if (hipMalloc(reinterpret_cast<void**>(&dy), (size_t)m * N * 4) != hipSuccess) {
+    cleanup();
+    g_err = "rt_test_matmul: device allocation failed";
+    return -1;
+  }
+  if (m <= 8 && path != 2) {
+    // fp32 activations as fp16 hi + lo pseudo-tokens (x = hi + lo to 2^-22 relative)
+    std::vector<uint16_t> x16((size_t)2 * m * K);
+    for (int j = 0; j < m; ++j)
+      for (size_t k = 0; k < K; ++k) {
+        const float x = X[(size_t)j * K + k];
+        const uint16_t hi = lw::f32_to_f16(x);
+        x16[(2 * j) * K + k] = hi;
+        x16[(2 * j + 1) * K + k] = lw::f32_to_f16(x - lw::f16_to_f32(hi));
+      }
+    if (hipMalloc(&dx16, x16.size() * 2) != hipSuccess ||
+        hipMemcpy(dx16, x16.data(), x16.size() * 2, hipMemcpyHostToDevice) != hipSuccess) {
+      cleanup();
+      g_err = "rt_test_matmul: upload failed";
+      return -1;
+    }
+    rc = fused_dev(*M, *t, dx16, m, 2, dy, (int)N, M->stream);
+  } else {
+    if (hipMalloc(reinterpret_cast<void**>(&dx), (size_t)m * K * 4) != hipSuccess ||
+        hipMemcpy(dx, X, (size_t)m * K * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      cleanup();
+      g_err = "rt_test_matmul: upload failed";
+      return -1;
+    }
+    rc = decode_gemm_dev(*M, *t, dx, m, dy, (int)N, M->stream);
+  }
+  if (rc == 0) {
+    if (hipStreamSynchronize(M->stream) != hipSuccess ||
+        hipMemcpy(Y, dy, (size_t)m * N * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+      g_err = std::string("rt_test_matmul: ") + hipGetErrorString(hipGetLastError());
+      rc = -1;
+    }
+  }
+  cleanup();
+  return rc;
+}
+
+int rt_test_decode(void* h, const char* name, uint8_t* out) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !out) {
+    g_err = "rt_test_decode: bad arguments";
+    return -1;
+  }
+  Tensor* t = M->find(name);
+  if (!t) {
+    g_err = std::string("no tensor ") + (name ? name : "(null)");
+    return -1;
+  }
+  if (t->enc == "raw8") return pread_all(M->fd, out, t->nbytes, t->off) ? 0 : -1;
+  if (!t->resident) {
+    g_err = t->name + ": not resident";
+    return -1;
+  }
+  uint8_t* d = nullptr;
+  const size_t n = (size_t)t->N * t->K;
+  HIPCHECK(hipMalloc(reinterpret_cast<void**>(&d), n));
+  hipError_t e = lw::launch_decode(t->dm, d, 0, t->dm.NT, M->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(M->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, d, n, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) {
+    g_err = std::string("rt_test_decode: ") + hipGetErrorString(e);
+    return -1;
+  }
+  return 0;
+}
+
+double rt_gpu_decode_all(void* h, int reps) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !M->gpu || reps < 1) return -1;
+  size_t need = 0;
+  for (auto& t : M->ts)
+    if (t.resident) need = std::max(need, std::min<size_t>((size_t)t.N * t.K, (size_t)256 << 20));
+  if (!need || grow(M->codes, M->codes_cap, need)) return -1;
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1;
+  std::vector<double> ts;
+  for (int r = 0; r < reps; ++r) {
+    (void)hipEventRecord(e0, M->stream);
+    for (auto& t : M->ts) {
+      if (!t.resident) continue;
+      const size_t row_bytes = (size_t)lw::TN * t.K;
+      const int rows_fit = (int)std::max<size_t>(1, M->codes_cap / row_bytes);
+      for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit)
+        (void)lw::launch_decode(t.dm, M->codes, tr0, std::min(t.dm.NT, tr0 + rows_fit), M->stream);
+    }
+    (void)hipEventRecord(e1, M->stream);
+    (void)hipEventSynchronize(e1);
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    ts.push_back(ms / 1e3);
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  std::sort(ts.begin(), ts.end());
+  return ts[ts.size() / 2];
+}
+
+int rt_test_cpu_decode(void* h, const char* name, int threads, uint8_t* out) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !out) return -1;
+  Tensor* t = M->find(name);
+  if (!t || !t->coded() || t->pre_il) {
+    g_err = std::string(name ? name : "(null)") + ": not a raw coded tensor";
+    return -1;
+  }
+  std::vector<uint8_t> blob(t->nbytes + 16, 0);
+  if (!pread_all(M->fd, blob.data(), t->nbytes, t->off)) return -1;
+  lw::cpu_decode(blob.data(), (int)t->N, t->KS(), std::max(1, threads), out);
+  return 0;
+}
+
+double rt_cpu_decode_all(void* h, int threads, long long* symbols) {
+  Model* M = static_cast<Model*>(h);
+  if (!M) return -1;
+  double total = 0;
+  long long nsym = 0;
+  std::vector<uint8_t> blob, out;
+  for (auto& t : M->ts) {
+    if (!t.coded() || t.pre_il) continue;
+    blob.assign(t.nbytes + 16, 0);
+    if (!pread_all(M->fd, blob.data(), t.nbytes, t.off)) return -1;
+    out.resize((size_t)t.N * t.KS());
+    total += lw::cpu_decode(blob.data(), (int)t.N, t.KS(), std::max(1, threads), out.data());
+    nsym += (long long)t.N * t.KS();
+  }
+  if (symbols) *symbols = nsym;
+  return total;
+}
+
+double rt_stat(void* h, const char* key) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !key) return -1;
+  const std::string s(key);
+  if (s == "resident_bytes") return (double)M->resident_bytes;
+  if (s == "streamed_bytes" || s == "stream_wait_s" || s == "stream_bytes_moved" || s == "n_streamed" ||
+      s == "graph_launches" || s == "graph_captures")
+    return 0;
+  if (s == "mem_available_mb") return M->avail_after_kb / 1024.0;
+  if (s == "coded_bytes") return (double)M->coded_bytes;
+  if (s == "device_bytes") return (double)M->device_bytes;
+  if (s == "pad_bytes") return (double)M->pad_bytes;
+  return -1;
+}
+
+int rt_forward(void* h, const int* ids, int n, float* logits, int all_logits) {
+  (void)h;
+  (void)ids;
+  (void)n;
+  (void)logits;
+  (void)all_logits;
+  g_err = "rt_forward: this library holds coded matrices only (no model runtime)";
+  return -1;
+}
+void rt_reset(void* h) {
+  if (h) static_cast<Model*>(h)->pos = 0;
+}
+void rt_set_window(void* h, int w) {
+  if (h) static_cast<Model*>(h)->window = std::max(0, w);
+}
+void rt_set_pos(void* h, int p) {
+  if (h) static_cast<Model*>(h)->pos = std::max(0, std::min(p, static_cast<Model*>(h)->pos));
+}
+int rt_pos(void* h) { return h ? static_cast<Model*>(h)->pos : 0; }
+int rt_vocab(void* h) {
+  (void)h;
+  return 0;
+}
+
+int lw_tensor_info(void* h, const char* name, int64_t* out) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !out) return -1;
+  Tensor* t = M->find(name);
+  if (!t) {
+    g_err = std::string("no tensor ") + (name ? name : "(null)");
+    return -1;
+  }
+  out[0] = t->N;
+  out[1] = t->K;
+  out[2] = t->kqt;
+  out[3] = t->symbits;
+  out[4] = (int64_t)t->nbytes;
+  out[5] = t->kqt ? (int64_t)M->ts[t->side_idx].nbytes : 0;
+  out[6] = (int64_t)t->dev_bytes;
+  out[7] = t->coded() ? t->T() : 0;
+  out[8] = t->resident ? 1 : 0;
+  return 0;
+}
+
+int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy, void* stream) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !X || !Y) {
+    g_err = "lw_matmul_dev: bad arguments";
+    return -1;
+  }
+  Tensor* t = M->find(name);
+  if (check_matmul(t, name)) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_f16) {
+    if (m < 1 || m > 16) {
+      g_err = "lw_matmul_dev: fp16 activations need 1 <= m <= 16";
+      return -1;
+    }
+    return fused_dev(*M, *t, X, m, 1, Y, ldy, s);
+  }
+  if (m < 1 || m > 8) {
+    g_err = "lw_matmul_dev: fp32 activations need 1 <= m <= 8";
+    return -1;
+  }
+  if (grow(M->X16, M->X16_cap, (size_t)2 * m * t->K * 2)) return -1;
+  HIPCHECK(lw::launch_split_x(static_cast<const float*>(X), M->X16, m, (int)t->K, s));
+  return fused_dev(*M, *t, M->X16, m, 2, Y, ldy, s);
+}
+
+int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
+                        float* const* Y, void* stream) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || count < 1 || !names || !X || !Y) {
+    g_err = "lw_group_matmul_dev: bad arguments";
+    return -1;
+  }
+  for (int i = 0; i < count; ++i) {
+    Tensor* t = M->find(names[i]);
+    if (check_matmul(t, names[i])) return -1;
+    if (lw_matmul_dev(h, names[i], X[i], 1, m, Y[i], (int)t->N, stream)) return -1;
+  }
+  return 0;
+}
+
+int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* names, const void* const* X, int m,
+                    float* const* Y, int warmup, int iters, double* out) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || ngroups < 1 || !sizes || !out || iters < 1) {
+    g_err = "lw_bench_groups: bad arguments";
+    return -1;
+  }
+  std::vector<int> first(ngroups + 1, 0);
+  for (int g = 0; g < ngroups; ++g) first[g + 1] = first[g] + sizes[g];
+  hipStream_t s = M->stream;
+  for (int w = 0; w < warmup; ++w)
+    for (int g = 0; g < ngroups; ++g)
+      if (lw_group_matmul_dev(h, sizes[g], names + first[g], X + first[g], m, Y + first[g], s)) return -1;
+  HIPCHECK(hipStreamSynchronize(s));
+  hipEvent_t a, b;
+  HIPCHECK(hipEventCreate(&a));
+  HIPCHECK(hipEventCreate(&b));
+  HIPCHECK(hipEventRecord(a, s));
+  for (int it = 0; it < iters; ++it)
+    for (int g = 0; g < ngroups; ++g)
+      if (lw_group_matmul_dev(h, sizes[g], names + first[g], X + first[g], m, Y + first[g], s)) return -1;
+  HIPCHECK(hipEventRecord(b, s));
+  HIPCHECK(hipEventSynchronize(b));
+  float ms = 0;
+  HIPCHECK(hipEventElapsedTime(&ms, a, b));
+  // fused kernels alone: events around each fused launch (partials only; the ordered reduction excluded)
+  std::vector<hipEvent_t> ev(2 * (size_t)first[ngroups]);
+  for (auto& e : ev) HIPCHECK(hipEventCreate(&e));
+  double kms = 0;
+  const int kit = std::max(1, std::min(iters, 20));
+  for (int it = 0; it < kit; ++it) {
+    int idx = 0;
+    for (int g = 0; g < ngroups; ++g)
+      for (int i = first[g]; i < first[g + 1]; ++i, ++idx) {
+        Tensor* t = M->find(names[i]);
+        if (grow(M->P, M->P_cap, (size_t)t->dm.KT * m * t->N * sizeof(float))) return -1;
+        HIPCHECK(hipEventRecord(ev[2 * idx], s));
+        HIPCHECK(lw::launch_fused(t->dm, X[i], m, M->P, s));
+        HIPCHECK(hipEventRecord(ev[2 * idx + 1], s));
+      }
+    HIPCHECK(hipEventSynchronize(ev.back()));
+    for (int i = 0; i < idx; ++i) {
+      float k = 0;
+      HIPCHECK(hipEventElapsedTime(&k, ev[2 * i], ev[2 * i + 1]));
+      kms += k;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  out[0] = ms / iters;
+  out[1] = kms / kit;
+  out[2] = first[ngroups];
+  return 0;
+}
+
+double lw_stream_read_gbps(long long bytes, int reps) {
+  if (bytes < (1 << 20) || reps < 1) return -1;
+  void* buf = nullptr;
+  float* out = nullptr;
+  const int blocks = 256 * 16;
+  if (hipMalloc(&buf, (size_t)bytes) != hipSuccess) return -1;
+  if (hipMalloc(reinterpret_cast<void**>(&out), (size_t)blocks * 256 * 4) != hipSuccess) {
+    (void)hipFree(buf);
+    return -1;
+  }
+  (void)hipMemset(buf, 1, (size_t)bytes);
+  hipEvent_t a, b;
+  (void)hipEventCreate(&a);
+  (void)hipEventCreate(&b);
+  std::vector<double> r;
+  const size_t n16 = (size_t)bytes / 16;
+  (void)lw::launch_stream_read(buf, n16, out, blocks, nullptr);
+  for (int i = 0; i < reps; ++i) {
+    (void)hipEventRecord(a, nullptr);
+    (void)lw::launch_stream_read(buf, n16, out, blocks, nullptr);
+    (void)hipEventRecord(b, nullptr);
+    (void)hipEventSynchronize(b);
+    float ms = 0;
+    (void)hipEventElapsedTime(&ms, a, b);
+    r.push_back(n16 * 16.0 / (ms * 1e-3) / 1e9);
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipFree(buf);
+  (void)hipFree(out);
+  std::sort(r.begin(), r.end());
+  return r[r.size() / 2];
+}
+
+}  // extern "C"

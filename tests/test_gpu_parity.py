@@ -1,0 +1,207 @@
+"""GPU parity of the HIP path through the C-ABI, against the oracle.
+
+Bars: decoded codes bit-exact; GEMV / skinny GEMM max|y - y64| / max|y64| <= 1e-3 against the fp64
+dequantize-then-matmul (the contract tolerance; the kernels accumulate in fp32 and land near 1e-6, so a tighter
+internal bar of 2e-5 is also asserted to catch partial mistakes such as one wrong sub-block scale).
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import golden_cases, load_golden
+
+pytestmark = pytest.mark.gpu
+TOL_CONTRACT, TOL_TIGHT = 1e-3, 2e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def check_err(y, y64, what):
+    from oracle.oracle import rel_err
+    e = rel_err(y, y64)
+    say("  %s rel err %.3g" % (what, e))
+    assert e <= TOL_CONTRACT and e <= TOL_TIGHT, (what, e)
+    return e
+
+
+@pytest.fixture(scope="module")
+def golden_rt(gpu, tmp_path_factory, lib):
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer, encode_huf8
+    d = tmp_path_factory.mktemp("golden")
+    w = Writer(str(d))
+    for case in golden_cases():
+        g = load_golden(case)
+        N, KS = g["sym"].shape
+        four = case.startswith("huf4p")
+        blob, _ = encode_huf8(g["sym"])
+        w.add(case, "huf4p" if four else "huf8", N, 2 * KS if four else KS, 1.0, 0, blob)
+    w.close()
+    rt = Runtime(d)
+    yield rt
+    rt.close()
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_gpu_decode_golden(golden_rt, orc, case):
+    say("decode golden", case)
+    g = load_golden(case)
+    four = case.startswith("huf4p")
+    want = orc.unpack_symbols(4 if four else 8, g["decoded"])
+    assert np.array_equal(golden_rt.test_decode(case), want)
+
+
+FORMATS = [(1, "Q4_K", 2.3), (2, "Q5_K", 3.4), (3, "Q6_K", 4.3), (4, "IQ4_XS", 2.6)]
+
+
+@pytest.fixture(scope="module")
+def fmt_rt(gpu, tmp_path_factory, lib):
+    from lazyweights_amd import Runtime, bundle
+    d = tmp_path_factory.mktemp("fmt")
+    mats = []
+    for kqt, name, H in FORMATS:
+        mats.append((name, kqt, 320, 3072, H, 50 + kqt))          # 5 tile rows: a partially filled block
+        mats.append((name + "_small", kqt, 64, 512, H, 60 + kqt))  # one tile column
+    bundle.write_synthetic_bundle(str(d), mats, threads=8)
+    rt = Runtime(d)
+    yield rt, {m[0]: m for m in mats}
+    rt.close()
+
+
+def reference_y(orc, mat, X64):
+    from lazyweights_amd import bundle
+    name, kqt, N, K, H, seed = mat
+    codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
+    return codes, orc.gemv_f64(orc.dequant(kqt, codes, side), X64)
+
+
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_decode_formats(fmt_rt, kqt, fmt, H):
+    from lazyweights_amd import bundle
+    rt, mats = fmt_rt
+    for nm in (fmt, fmt + "_small"):
+        say("decode", nm)
+        name, kqt_, N, K, H_, seed = mats[nm]
+        codes, _ = bundle.synth_matrix(kqt_, N, K, H_, seed)
+        assert np.array_equal(rt.test_decode(nm), codes)
+
+
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_fused_fp32_x(fmt_rt, orc, kqt, fmt, H):
+    """rt_test_matmul (fp32 host X, fused path) for m = 1..8 against fp64."""
+    rt, mats = fmt_rt
+    rng = np.random.default_rng(kqt)
+    for nm in (fmt, fmt + "_small"):
+        mat = mats[nm]
+        X = rng.standard_normal((8, mat[3])).astype(np.float32)
+        _, y64 = reference_y(orc, mat, X.astype(np.float64))
+        for m in (1, 2, 3, 5, 8):
+            say("fused fp32", nm, "m", m)
+            Y = rt.test_matmul(nm, X[:m], path=0)
+            check_err(Y, y64[:m], "%s m=%d" % (nm, m))
+
+
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
+    """path 2 (decode to scratch + GEMM) and m > 8 (auto) against fp64."""
+    rt, mats = fmt_rt
+    mat = mats[fmt]
+    rng = np.random.default_rng(10 + kqt)
+    X = rng.uniform(-0.5, 0.5, (12, mat[3])).astype(np.float32)
+    _, y64 = reference_y(orc, mat, X.astype(np.float64))
+    say("path2", fmt)
+    check_err(rt.test_matmul(fmt, X[:3], path=2), y64[:3], fmt + " path2 m=3")
+    say("auto m=12", fmt)
+    check_err(rt.test_matmul(fmt, X, path=0), y64, fmt + " auto m=12")
+
+
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_fused_fp16_x_device(fmt_rt, orc, kqt, fmt, H):
+    """lw_matmul_dev with fp16 activations resident on the GPU (the bench path), m up to 16."""
+    import torch
+    rt, mats = fmt_rt
+    mat = mats[fmt]
+    N, K = mat[2], mat[3]
+    g = torch.Generator().manual_seed(kqt)
+    X = torch.randn(16, K, generator=g).half()
+    _, y64 = reference_y(orc, mat, X.double().numpy())
+    Xd = X.cuda()
+    for m in (1, 2, 4, 5, 8, 16):
+        say("fused fp16", fmt, "m", m)
+        Y = torch.full((m, N), float("nan"), dtype=torch.float32, device="cuda")
+        rt.matmul_dev(fmt, Xd[:m], Y, x_f16=True, stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        check_err(Y.cpu().numpy(), y64[:m], "%s fp16 m=%d" % (fmt, m))
+
+
+def test_gpu_verify_gemm_equals_repeated_gemv(fmt_rt):
+    """One m = 5 launch gives the same bits as five m = 1 launches (tokens accumulate independently)."""
+    import torch
+    rt, mats = fmt_rt
+    for fmt in ("Q4_K", "Q5_K"):
+        N, K = mats[fmt][2], mats[fmt][3]
+        X = torch.randn(5, K).half().cuda()
+        Y5 = torch.zeros(5, N, device="cuda")
+        rt.matmul_dev(fmt, X, Y5)
+        Y1 = torch.zeros(5, N, device="cuda")
+        for j in range(5):
+            rt.matmul_dev(fmt, X[j:j + 1], Y1[j:j + 1])
+        torch.cuda.synchronize()
+        say("verify == 5 x gemv", fmt)
+        assert torch.equal(Y5, Y1)
+
+
+def test_gpu_decode_all_timing(fmt_rt):
+    rt, _ = fmt_rt
+    s = rt.gpu_decode_all(3)
+    say("gpu_decode_all", s)
+    assert s > 0
+
+
+# ── full BASELINE shapes ─────────────────────────────────────────────────────────────────────────────────
+
+def full_size_check(tmp_path, mats, m_list=(1,)):
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from oracle import oracle as orc
+    bundle.write_synthetic_bundle(str(tmp_path), mats, threads=16)
+    with Runtime(tmp_path) as rt:
+        for mat in mats:
+            name, kqt, N, K, H, seed = mat
+            say("full-size", name, N, K)
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            assert np.array_equal(rt.test_decode(name), codes)
+            X = torch.randn(max(m_list), K).half()
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X.double().numpy())
+            Xd = X.cuda()
+            for m in m_list:
+                Y = torch.zeros(m, N, device="cuda")
+                rt.matmul_dev(name, Xd[:m], Y)
+                torch.cuda.synchronize()
+                check_err(Y.cpu().numpy(), y64[:m], "%s m=%d" % (name, m))
+            del codes, side
+
+
+def test_full_config0(gpu, tmp_path):
+    from lazyweights_amd.configs import CONFIG0
+    full_size_check(tmp_path, CONFIG0, (1, 5))
+
+
+def test_full_config2_layer(gpu, tmp_path):
+    from lazyweights_amd.configs import config2_layer
+    full_size_check(tmp_path, config2_layer(0), (1,))
+
+
+def test_full_config3_mixed(gpu, tmp_path):
+    from lazyweights_amd.configs import CONFIG3
+    full_size_check(tmp_path, CONFIG3, (1,))
+
+
+def test_full_config4_q5k_verify(gpu, tmp_path):
+    from lazyweights_amd.configs import CONFIG4
+    full_size_check(tmp_path, [m for m in CONFIG4 if m[0] in ("q5.gate", "q5.down")], (5,))

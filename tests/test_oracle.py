@@ -1,0 +1,163 @@
+"""Pins the oracle (oracle/lw_oracle.c) before it is trusted as the checker.
+
+- decoders: against decodes written by the reference's lazyweights/bundle.py (golden fixtures) and against the
+  reference's own C++ decoder (hw/huff/tb/csim_main.cpp) compiled under oracle/_ref;
+- comparator tables: against the LUT over all 2048 windows (brute force);
+- sub-scale extraction: against the reference's field *packing* (scripts/kq_quant.py:204-221), restated here as
+  the inverse function, and against hand-computed known answers;
+- GEMV: against numpy's fp64 matmul.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, golden_cases, load_golden
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_lockstep_decode_matches_reference(orc, case):
+    g = load_golden(case)
+    N, KS = g["sym"].shape
+    assert np.array_equal(orc.decode_lockstep(g["blob"], N, KS), g["decoded"])
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_cpu_decode_matches_reference(orc, case):
+    g = load_golden(case)
+    N, KS = g["sym"].shape
+    for th in (1, 3):
+        assert np.array_equal(orc.cpu_decode(g["blob"], N, KS, th), g["decoded"])
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_comparator_equals_lut(orc, case):
+    lut = load_golden(case)["lut"]
+    tabs = orc.canon_tables(lut)
+    for w in range(2048):
+        if lut[w] >> 8:       # entries a code reaches (the single-symbol table leaves odd windows empty)
+            assert orc.canon_lookup(tabs, w) == int(lut[w]), w
+
+
+def pack_q4k(d, dmin, sc, m):
+    """scripts/kq_quant.py:204-215 field packing of one Q4_K/Q5_K super-block (the inverse of extraction)."""
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = sc[j] | ((sc[4 + j] >> 4) << 6)
+        s[4 + j] = m[j] | ((m[4 + j] >> 4) << 6)
+        s[8 + j] = (sc[4 + j] & 15) | ((m[4 + j] & 15) << 4)
+    return np.concatenate([np.array([d], np.float16).view(np.uint8), np.array([dmin], np.float16).view(np.uint8), s])
+
+
+def pack_iq4xs(d, ls):
+    """scripts/kq_quant.py:218-221 (ls = stored 6-bit values)."""
+    hi = 0
+    for j in range(8):
+        hi |= (ls[j] >> 4) << (2 * j)
+    lo = [ls[j] & 15 for j in range(8)]
+    b = [lo[2 * j] | (lo[2 * j + 1] << 4) for j in range(4)]
+    return np.concatenate([np.array([d], np.float16).view(np.uint8), np.array([hi], np.uint16).view(np.uint8),
+                           np.array(b, np.uint8)])
+
+
+def test_sub_scales_invert_reference_packing(orc):
+    rng = np.random.default_rng(3)
+    for kqt in (1, 2):
+        for _ in range(50):
+            d, dmin = np.float16(rng.uniform(0.005, 0.02)), np.float16(rng.uniform(0.005, 0.02))
+            sc, m = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+            s, o = orc.sub_scales(kqt, pack_q4k(d, dmin, sc, m)[None])
+            assert np.array_equal(s[0], np.float32(d) * sc.astype(np.float32))
+            assert np.array_equal(o[0], np.float32(dmin) * m.astype(np.float32))
+    for _ in range(50):
+        d, ls = np.float16(rng.uniform(0.005, 0.02)), rng.integers(0, 64, 8)
+        s, o = orc.sub_scales(4, pack_iq4xs(d, ls)[None])
+        assert np.array_equal(s[0], np.float32(d) * (ls - 32).astype(np.float32)) and not o.any()
+    for _ in range(20):
+        d, sc = np.float16(rng.uniform(0.005, 0.02)), rng.integers(-128, 128, 16)
+        rec = np.concatenate([sc.astype(np.int8).view(np.uint8), np.array([d], np.float16).view(np.uint8)])
+        s, o = orc.sub_scales(3, rec[None])
+        assert np.array_equal(s[0], np.float32(d) * sc.astype(np.float32)) and not o.any()
+
+
+def test_sub_scales_known_answers(orc):
+    # Q4_K: d = 1, dmin = 0.5; scale bytes chosen by hand. Sub-block 5: sc = (b[9] & 15) | (b[1] >> 6) << 4
+    rec = np.zeros(16, np.uint8)
+    rec[0:2] = np.array([1.0], np.float16).view(np.uint8)
+    rec[2:4] = np.array([0.5], np.float16).view(np.uint8)
+    rec[4 + 1] = 0b11000011   # q[1]: sc[1] = 3, high bits of sc[5] = 3
+    rec[4 + 5] = 0b01000111   # q[5]: m[1] = 7, high bits of m[5] = 1
+    rec[4 + 9] = 0x2A         # q[9]: sc[5] low nibble 10, m[5] low nibble 2
+    s, o = orc.sub_scales(1, rec[None])
+    assert s[0, 1] == 3 and o[0, 1] == 3.5            # d*3, 0.5*7
+    assert s[0, 5] == 10 + 48 and o[0, 5] == 0.5 * (2 + 16)
+    # IQ4_XS: ls_j = ((b[4 + j/2] >> 4 (j & 1)) & 15) | ((hi >> 2j) & 3) << 4; s = d (ls - 32)
+    rec = np.zeros(8, np.uint8)
+    rec[0:2] = np.array([2.0], np.float16).view(np.uint8)
+    rec[2:4] = np.array([0b11 << 6], np.uint16).view(np.uint8)   # hi bits of ls_3 = 3
+    rec[4 + 1] = 0x70          # ls_3 low nibble = 7 (high nibble of byte 1), ls_2 low = 0
+    s, _ = orc.sub_scales(4, rec[None])
+    assert s[0, 3] == 2.0 * ((7 | 48) - 32) and s[0, 2] == 2.0 * (0 - 32)
+
+
+def test_dequant_known_grid(orc):
+    # IQ4_XS grid (llama.cpp kvalues_iq4nl) and Q6_K centring on a 1 x 256 matrix with unit scales
+    side = np.zeros((1, 8), np.uint8)
+    side[0, 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    side[0, 2:4] = np.array([0xAAAA], np.uint16).view(np.uint8)   # ls high bits 2 -> ls = 32 + low
+    side[0, 4:8] = 0x11                                           # ls low nibbles 1 -> ls = 33 -> s = 1
+    codes = np.tile(np.arange(16, dtype=np.uint8), 16)[None]
+    w = orc.dequant(4, codes, side)
+    assert list(w[0, :16]) == [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    side6 = np.zeros((1, 18), np.uint8)
+    side6[0, :16] = 1
+    side6[0, 16:18] = np.array([0.5], np.float16).view(np.uint8)
+    codes6 = np.arange(256, dtype=np.uint8)[None] % 64
+    w6 = orc.dequant(3, codes6, side6)
+    assert np.array_equal(w6[0], 0.5 * (codes6[0].astype(np.float32) - 32))
+
+
+def test_gemv_f64_matches_numpy(orc):
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((64, 512)).astype(np.float32)
+    x = rng.standard_normal((3, 512))
+    assert np.allclose(orc.gemv_f64(w, x), x @ w.astype(np.float64).T, rtol=1e-13, atol=1e-12)
+
+
+def test_decode_gemv_baseline_matches_dequant(orc):
+    from lazyweights_amd import bundle
+    rng = np.random.default_rng(1)
+    for kqt in (1, 2, 3, 4):
+        codes, side = bundle.synth_matrix(kqt, 128, 1024, 2.5, 11)
+        blob, _ = bundle.encode_huf8(bundle.form_symbols(kqt, codes))
+        x = rng.standard_normal(1024).astype(np.float32)
+        y = orc.decode_gemv(kqt, blob, side, 128, 1024, x, threads=2)
+        y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), x.astype(np.float64))[0]
+        assert orc.rel_err(y, y64) < 1e-5
+
+
+CSIM = os.path.join(ROOT, "oracle", "_ref", "huff_csim")
+
+
+@pytest.mark.skipif(not os.path.exists(CSIM), reason="reference C++ decoder not built (reference tree absent)")
+def test_reference_cpp_decoder_reads_our_bundles(tmp_path):
+    from lazyweights_amd.bundle import Writer
+    w = Writer(str(tmp_path))
+    names = []
+    for case in ("huf4p_q4k_128x1024", "huf8_q6k_64x512", "limited_64x768"):
+        g = load_golden(case)
+        N, KS = g["sym"].shape
+        from lazyweights_amd.bundle import encode_huf8
+        blob, _ = encode_huf8(g["sym"])
+        four = case.startswith("huf4p")
+        w.add(case, "huf4p" if four else "huf8", N, 2 * KS if four else KS, 1.0, 0, blob)
+        names.append((case, g["sym"]))
+    w.close()
+    for case, sym in names:
+        dump = tmp_path / (case + ".bin")
+        p = subprocess.run([CSIM, str(tmp_path), "--threads", "2", "--only", case, "--dump-ref", case, str(dump)],
+                           stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+        assert p.returncode == 0, p.stderr
+        assert '"mismatch": 0' in p.stdout and '"mismatch": 1' not in p.stdout
+        assert np.array_equal(np.fromfile(dump, np.uint8).reshape(sym.shape), sym)

@@ -1,0 +1,138 @@
+"""Runtime boundary on the CPU: exports, manifest validation and error returns, CPU decode entry points.
+
+Failure handling is forced from the host (bad manifests, mismatched side tensors, truncated blobs); no GPU is
+touched (budget_mb = 0 opens without residency)."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, load_golden
+
+
+def declared_functions():
+    src = open(os.path.join(ROOT, "include", "lazyweights_amd.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"\b([a-z_][a-z0-9_]*)\s*\(", src)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = [n for n in declared_functions() if n.startswith(("rt_", "lw_"))]
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def write_bundle(path, cases=("huf4p_q4k_128x1024", "huf8_q6k_64x512"), side=True):
+    from lazyweights_amd.bundle import Writer, encode_huf8
+    w = Writer(str(path))
+    for case in cases:
+        g = load_golden(case)
+        N, KS = g["sym"].shape
+        four = case.startswith("huf4p")
+        K = 2 * KS if four else KS
+        blob, _ = encode_huf8(g["sym"])
+        w.add(case, "huf4p" if four else "huf8", N, K, 1.0, 0, blob)
+        if side:
+            kqt, sb = (1, 16) if four else (3, 18)
+            w.add(case + ".kqs", "kq_Q4_K" if four else "kq_Q6_K", N, K // 256 * sb, 1.0, 0,
+                  np.zeros(N * (K // 256) * sb, np.uint8).tobytes())
+    w.close()
+    return path
+
+
+def test_open_missing_dir(lib):
+    from lazyweights_amd import Runtime
+    with pytest.raises(RuntimeError, match="manifest"):
+        Runtime("/nonexistent/bundle", budget_mb=0)
+
+
+def test_open_bad_manifest(lib, tmp_path):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path)
+    with open(tmp_path / "manifest.txt", "a") as f:
+        f.write("t broken huf8 64\n")
+    with pytest.raises(RuntimeError, match="bad tensor line"):
+        Runtime(tmp_path, budget_mb=0)
+
+
+def test_open_mismatched_side_tensor(lib, tmp_path):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path)
+    txt = open(tmp_path / "manifest.txt").read().replace("kq_Q6_K 64 36", "kq_Q6_K 64 32")
+    open(tmp_path / "manifest.txt", "w").write(txt)
+    with pytest.raises(RuntimeError, match="side tensor"):
+        Runtime(tmp_path, budget_mb=0)
+
+
+def test_open_wrong_symbol_layout(lib, tmp_path):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path)
+    txt = open(tmp_path / "manifest.txt").read().replace("kq_Q6_K", "kq_IQ4_XS")
+    open(tmp_path / "manifest.txt", "w").write(txt)
+    with pytest.raises(RuntimeError):
+        Runtime(tmp_path, budget_mb=0)
+
+
+def test_open_truncated_weights(lib, tmp_path):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path)
+    size = os.path.getsize(tmp_path / "weights.bin")
+    with open(tmp_path / "weights.bin", "r+b") as f:
+        f.truncate(size - 100)
+    with pytest.raises(RuntimeError, match="past the end"):
+        Runtime(tmp_path, budget_mb=0)
+
+
+def test_open_bad_tile_shape(lib, tmp_path):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path, side=False)
+    txt = open(tmp_path / "manifest.txt").read().replace("huf8 64 512", "huf8 64 500")
+    open(tmp_path / "manifest.txt", "w").write(txt)
+    with pytest.raises(RuntimeError, match="tiles"):
+        Runtime(tmp_path, budget_mb=0)
+
+
+def test_cpu_decode_entry_points(lib, tmp_path, orc):
+    from lazyweights_amd import Runtime
+    write_bundle(tmp_path)
+    with Runtime(tmp_path, budget_mb=0) as rt:
+        for case in ("huf4p_q4k_128x1024", "huf8_q6k_64x512"):
+            g = load_golden(case)
+            for th in (1, 4):
+                assert np.array_equal(rt.test_cpu_decode(case, th), g["decoded"])
+        s, n = rt.cpu_decode_all(2)
+        assert n == 128 * 512 + 64 * 512 and s >= 0
+        # not resident: GPU entry points refuse with -1 instead of exiting
+        X = np.zeros((1, 1024), np.float32)
+        with pytest.raises(RuntimeError, match="not resident"):
+            rt.test_matmul("huf4p_q4k_128x1024", X)
+        with pytest.raises(RuntimeError, match="not resident"):
+            rt.test_decode("huf4p_q4k_128x1024")
+        Y = np.zeros((1, 128), np.float32)
+        assert rt.lib.rt_test_matmul(rt.h, b"absent", X.ctypes.data, 1, Y.ctypes.data, 0) == -1
+        assert "no tensor" in rt.lib.lw_last_error().decode()
+        with pytest.raises(RuntimeError):
+            rt.test_cpu_decode("huf4p_q4k_128x1024.kqs")
+        assert rt.stat("resident_bytes") == 0 and rt.stat("no_such_key") == -1
+        assert rt.lib.rt_forward(rt.h, None, 0, None, 0) == -1
+
+
+def test_synthetic_bundle_writer(lib, tmp_path, orc):
+    """The all-C++ bundle writer produces blobs that the reference-faithful oracle decodes to the seeded codes."""
+    from lazyweights_amd import bundle
+    mats = [("a", 1, 128, 1024, 2.3, 7), ("b", 3, 64, 512, 4.3, 8), ("c", 4, 64, 1024, 2.6, 9), ("d", 2, 64, 512, 3.4, 10)]
+    bundle.write_synthetic_bundle(str(tmp_path), mats, threads=4)
+    cfg, ts = bundle.read_manifest(str(tmp_path))
+    by = {t["name"]: t for t in ts}
+    assert all(t["offset"] % 256 == 0 for t in ts)
+    for name, kqt, N, K, H, seed in mats:
+        codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
+        t = by[name]
+        assert t["enc"] == ("huf4p" if kqt in (1, 4) else "huf8") and (t["N"], t["K"]) == (N, K)
+        blob = bundle.read_tensor(str(tmp_path), t)
+        ks = K // 2 if kqt in (1, 4) else K
+        sym = orc.decode_lockstep(blob, N, ks)
+        assert np.array_equal(orc.unpack_symbols(8 if ks == K else 4, sym), codes)
+        assert np.array_equal(bundle.read_tensor(str(tmp_path), by[name + ".kqs"]).reshape(side.shape), side)
