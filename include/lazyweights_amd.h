@@ -86,6 +86,10 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
                         float* const* Y, void* stream);
 
+/* Fused-kernel selection for all handles: 0 (default) = the ring-staged kernel, grouped per layer, wherever a
+ * matrix has a ring schedule; 1 = the whole-tile kernel everywhere (the fallback path). Returns 0 or -1. */
+int lw_set_kernel_mode(int mode);
+
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in
  * names/X/Y (group g has sizes[g] matrices), cycling through the groups, with HIP events on the launch stream.
  * out[0] = mean ms per pass over all groups, out[1] = mean ms per fused-kernel launch set (decode + GEMV kernels
@@ -113,10 +117,12 @@ int lw_write_bundle(const char* dir, int count, const char* const* names, const 
 int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L);
 
 /* The device layout this library builds from a blob at load time (host-side, for inspection and tests): fills tbase
- * [T], mid [T * 32], rows [T] and, when words_cap is large enough, words; returns the word count (-1 on a bad or
- * corrupt blob). pre_il / compact select the reference's pre-interleaved export formats (_il / _ilc). */
+ * [T], mid [T * 32], rows [T], sched [2 T] (ring staging schedule), *ring_rows and, when words_cap is large enough,
+ * words; returns the word count (-1 on a bad or corrupt blob). Any output pointer may be NULL. pre_il / compact
+ * select the reference's pre-interleaved export formats (_il / _ilc). */
 long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,
-                          uint16_t* mid, uint16_t* rows, uint32_t* words, long long words_cap);
+                          uint16_t* mid, uint16_t* rows, uint64_t* sched, int* ring_rows, uint32_t* words,
+                          long long words_cap);
 
 #ifdef __cplusplus
 }

@@ -10,9 +10,11 @@ namespace lw {
 //   lut   u16[2048]            the bundle's decode table (sym | len << 8)
 //   tbase u32[T]               word index (into words) of tile t's first word row
 //   mid   u16[T][32]           bit offset, within lane l's stream, of the lane's second row (symbol 256)
-//   words u32[...]             tile t: word i of lane l at tbase[t] + 32 i + l, i < rows[t]; every lane starts at
-//                              bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
+//   words u32[...]             tile t: word i of lane l at tbase[t] + 32 i + l, i < rows[t]; every lane stream
+//                              starts at bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
 //   side  u8[N][K/256][SB]     K-quant side bytes as in the bundle's <name>.kqs
+//   sched u32x4[T]             ring staging schedule of each tile (lw_layout.h, Layout::sched)
+// Every lane stream starts with GUARD = 3 zero bits (symbol 0 at stream bit 3).
 struct DevMat {
   const uint16_t* lut;
   const uint32_t* tbase;
@@ -20,12 +22,46 @@ struct DevMat {
   const uint16_t* rows;
   const uint32_t* words;
   const uint8_t* side;
+  const uint4* sched;
   int N, K;         // weights
   int kqt;          // 1 Q4_K, 2 Q5_K, 3 Q6_K, 4 IQ4_XS (0: none -> decode only)
   int symbits;      // 4 (huf4p) or 8 (huf8)
   int KT, NT;       // tile columns, tile rows
   int max_rows;     // max over tiles of rows[t]
+  int ring_rows;    // 16 / 32: ring kernel usable with that ring; 0: whole-tile kernel only
 };
+
+// Matrices of one grouped launch of the ring kernel (same K-quant type and ring size). Matrix i owns blocks
+// [block0, block0 + KT * ceil(NT / WPB)); X2 = its fp16 activations [mt][K] as pairs, P its partials [KT][mt][N].
+constexpr int MAX_GROUP = 8;
+struct GroupEntry {
+  DevMat M;
+  const uint32_t* X2;
+  float* P;
+  int block0;
+};
+struct GroupPlan {
+  GroupEntry e[MAX_GROUP];
+  int n;
+  int mt;
+  int blocks;
+};
+// One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
+// K-quant types or ring sizes, or a matrix has no ring schedule).
+hipError_t launch_fused_group(const GroupPlan& plan, hipStream_t s);
+int group_waves_per_block(int ring_rows);
+
+// Ordered reduction of several matrices in one launch: Y_i[j][n] = sum_tc P_i[tc][jj][n] (as launch_reduce).
+struct ReduceEntry {
+  const float* P;
+  float* Y;
+  int N, KT, ldy, out0;  // out0 = first output index of this matrix in the flattened launch (m * N each)
+};
+struct ReducePlan {
+  ReduceEntry e[MAX_GROUP];
+  int n, m, per, total;
+};
+hipError_t launch_reduce_group(const ReducePlan& plan, hipStream_t s);
 
 // X16 [mt][K] fp16 (mt pseudo-tokens); P [KT][mt][N] fp32 per-tile-column partials.
 hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);

@@ -23,6 +23,9 @@ namespace lw {
 
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
+// leading zero bits of every device lane stream (lw_layout.h GUARD)
+constexpr int GUARD_BITS = 3;
+
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
 }
@@ -82,6 +85,48 @@ __device__ __forceinline__ void side_scale(const uint32_t* w, int j, float& s, f
     const uint32_t ls = ((side_byte(w, 4 + j / 2) >> (4 * (j & 1))) & 15) | (((w[0] >> (16 + 2 * j)) & 3) << 4);
     s = h2f(w[0]) * (float)((int)ls - 32);
     o = 0.f;
+  }
+}
+
+// Sub-block scales of one super-block packed as bytes, consumed low byte first (reference llmrt.cu:125-149; Q4_K /
+// Q5_K fields per llama.cpp get_scale_min_k4, four at a time): s_j = dA * byte_j (Q6_K: signed bytes, 16 of them in
+// scq then scq2; IQ4_XS: ls_j - 32 as a signed byte), o_j = dB * m_j (side_mins).
+template <int KQ>
+__device__ __forceinline__ void side_packed(const uint32_t* w, uint64_t& scq, uint64_t& scq2, float& dA, float& dB) {
+  if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
+    const uint32_t sc_lo = w[1] & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (w[3] & 0x0F0F0F0Fu) | ((w[1] >> 2) & 0x30303030u);
+    scq = (uint64_t)sc_lo | (uint64_t)sc_hi << 32;
+    scq2 = 0;
+    dA = h2f(w[0]);
+    dB = h2f(w[0] >> 16);
+  } else if (KQ == KQ_Q6_K) {
+    scq = (uint64_t)w[0] | (uint64_t)w[1] << 32;
+    scq2 = (uint64_t)w[2] | (uint64_t)w[3] << 32;
+    dA = h2f(w[4]);
+    dB = 0.f;
+  } else {
+    const uint32_t hi = w[0] >> 16, lo = w[1];
+    uint64_t q = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t ls = ((lo >> (4 * i)) & 15u) | (((hi >> (2 * i)) & 3u) << 4);
+      q |= (uint64_t)((ls - 32u) & 255u) << (8 * i);
+    }
+    scq = q;
+    scq2 = 0;
+    dA = h2f(w[0]);
+    dB = 0.f;
+  }
+}
+// Q4_K / Q5_K sub-block mins as floats
+__device__ __forceinline__ void side_mins(const uint32_t* w, float* mf) {
+  const uint32_t m_lo = w[2] & 0x3F3F3F3Fu;
+  const uint32_t m_hi = ((w[3] >> 4) & 0x0F0F0F0Fu) | ((w[2] >> 2) & 0x30303030u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    mf[i] = (float)((m_lo >> (8 * i)) & 255u);
+    mf[4 + i] = (float)((m_hi >> (8 * i)) & 255u);
   }
 }
 
@@ -150,7 +195,7 @@ __global__ void __launch_bounds__(256) k_fused(DevMat M, const uint32_t* __restr
   }
   __syncthreads();
   if (!active) return;
-  uint32_t pos = half ? (uint32_t)M.mid[(size_t)t * 32 + l] : 0u;
+  uint32_t pos = half ? (uint32_t)M.mid[(size_t)t * 32 + l] : (uint32_t)GUARD_BITS;
   const uint32_t* lw = tw + l;
   const int n = tr * TN + half * 32 + l;
   float tot[MT];
@@ -234,6 +279,256 @@ hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipS
   }
 }
 
+// ring slot write of chunk k (2 rows; this lane's 8 bytes of row 2k + slot_lane), with the mirror of slot 0
+template <int RS>
+__device__ __forceinline__ void ring_put(uint2* ring2, int k, int slot_lane, int col2, uint2 v) {
+  const int slot = (2 * k + slot_lane) & (RS - 1);
+  ring2[slot * 16 + col2] = v;
+  if (slot == 0) ring2[RS * 16 + col2] = v;
+}
+
+// group start: write the chunks loaded two groups ago, then issue this group's loads (counts: 2 bits per group)
+template <int RS>
+__device__ __forceinline__ void ring_stage(uint2* ring2, const uint2* src, int slot_lane, int col2, uint32_t counts,
+                                           int g, int& written, int& issued, int& pend, uint2& s0, uint2& s1) {
+  if (pend > 0) ring_put<RS>(ring2, written++, slot_lane, col2, s0);
+  if (pend > 1) ring_put<RS>(ring2, written++, slot_lane, col2, s1);
+  const int nload = (int)((counts >> (2 * g)) & 3u);
+  if (nload > 0) s0 = src[32 * issued++];
+  if (nload > 1) s1 = src[32 * issued++];
+  pend = nload;
+}
+
+// ── ring-staged fused kernel, grouped over the matrices of a layer ────────────────────────────────────────
+// As k_fused, but a wave does not stage its whole tile: each front (lanes 0-31 from bit GUARD, lanes 32-63 from
+// their `mid` offsets) keeps a ring of RS word rows (+ one mirror row for the window's read-ahead) and streams 2-row
+// chunks (one 8-byte load per lane) from HBM on the tile's load-time schedule (Layout::sched): chunks loaded at
+// group g are written to the ring at the start of group g + 2, so their latency hides behind two groups of decode. Windows are 64 bits (rows r, r + 1)
+// and yield two symbols each: the first at the guard-aligned offset (alignbit), the second by a 64-bit shift.
+// block = WPB tile rows of one tile column of one matrix of the plan.
+template <int KQ, int MT, int WPB, int RS>
+__global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  constexpr int RING_WORDS = (RS + 1) * 32;
+  constexpr int NTHR = WPB * 64;
+  extern __shared__ __align__(16) uint32_t smem[];
+  uint2* lut8 = reinterpret_cast<uint2*>(smem);
+  uint32_t* xs = smem + 2 * LUTN;
+  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);
+  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);
+
+  // the block's matrix: a uniform index into the plan, read through the kernel-argument segment (scalar loads)
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < plan.n && (int)blockIdx.x >= plan.e[i].block0) mi = i;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const GroupEntry KEntry;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  KEntry* ep = (KEntry*)(kbase + offsetof(GroupPlan, e) + (size_t)mi * sizeof(GroupEntry));
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const int mt = plan.mt;
+  const int bl = (int)blockIdx.x - E.block0;
+  const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
+  const int tc = bl % KT, wave = threadIdx.x >> 6;
+  const int tr = (bl / KT) * WPB + wave;
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+
+  for (int i = threadIdx.x; i < LUTN; i += NTHR) {
+    const uint32_t e = M.lut[i], sym = e & 255u;
+    uint32_t v;
+    if (SYMB == 4) v = f2h(grid_value<KQ>(sym & 15u)) | f2h(grid_value<KQ>(sym >> 4)) << 16;
+    else v = f2h(grid_value<KQ>(sym));
+    lut8[i] = make_uint2(v, e >> 8);
+  }
+  for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
+    const int j = i / NPAIR, c = i - j * NPAIR;
+    xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
+    const int g = i / MT, j = i - g * MT;
+    float a = 0.f;
+    for (int c = g * (GW / 2); c < (g + 1) * (GW / 2); ++c) {
+      const uint32_t v = xs[c * MT + j];
+      a += h2f(v) + h2f(v >> 16);
+    }
+    xg[g * MT + j] = a;
+  }
+  __syncthreads();
+  if (tr >= NT) return;
+
+  const int t = tr * KT + tc;
+  const uint4 sc = M.sched[t];
+  const int base_f = f ? (int)(sc.z & 255u) : 0;
+  const int init_f = (int)((sc.z >> (f ? 16 : 8)) & 255u);
+  const uint32_t counts_f = f ? sc.y : sc.x;  // 2 bits per group: chunks this front loads at that group
+  uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
+  uint2* ring2 = reinterpret_cast<uint2*>(ring);
+  // chunk k of this front = rows [2k, 2k + 2) after its base row; lane l carries row 2k + l / 16, words 2 (l % 16)..
+  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t] + 32u * base_f) + l;
+  const int slot_lane = l >> 4, col2 = l & 15;
+  for (int k = 0; k < init_f; ++k) ring_put<RS>(ring2, k, slot_lane, col2, src[32 * k]);
+  int issued = init_f, written = init_f;
+  uint2 st00 = make_uint2(0, 0), st01 = st00, st10 = st00, st11 = st00;  // staged chunks by group parity
+  int pend0 = 0, pend1 = 0;
+
+  uint32_t Q = (f ? (uint32_t)M.mid[(size_t)t * 32 + l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f;
+  const uint32_t* rl = ring + l;
+  const char* lutb = reinterpret_cast<const char*>(lut8);
+  const int n = tr * TN + f * 32 + l;
+  const uint8_t* srow = M.side + ((size_t)n * (K / 256) + (size_t)tc * (TW / 256)) * SB;
+  constexpr int NSB = TW / 256;    // super-blocks per tile column
+  constexpr int GPS = 16 / NSB;    // staging groups (16 symbols) per super-block
+  constexpr int NSUB = 256 / GW;   // sub-blocks per super-block
+  constexpr int GPSUB = GPS / NSUB;  // groups per sub-block (2 for Q5_K, else 1)
+  float tot[MT], acc[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) tot[j] = acc[j] = 0.f;
+
+#pragma unroll 1
+  for (int sb = 0; sb < NSB; ++sb) {
+    uint32_t sw[5];
+    side_load<KQ>(srow + sb * SB, sw);
+    float dA, dB;
+    uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K), consumed low byte first
+    float msum[MT];
+    side_packed<KQ>(sw, scq, scq2, dA, dB);
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      msum[j] = 0.f;
+      if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
+        float mf[8];
+        side_mins(sw, mf);
+#pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj) msum[j] = fmaf(mf[jj], xg[(sb * NSUB + jj) * MT + j], msum[j]);
+      }
+    }
+    float tsum[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) tsum[j] = 0.f;
+#pragma unroll 1
+    for (int gg2 = 0; gg2 < GPS; gg2 += 2) {
+      if (KQ == KQ_Q6_K && gg2 == 8) scq = scq2;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int g = sb * GPS + gg2 + h;
+        if (h == 0) ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend0, st00, st01);
+        else ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend1, st10, st11);
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const uint32_t* a = rl + ((Q >> 5) & (RS - 1)) * 32;
+          const uint32_t lo = a[0], hi = a[32];
+          const uint32_t w1 = __builtin_amdgcn_alignbit(hi, lo, Q);
+          const uint2 e1 = *reinterpret_cast<const uint2*>(lutb + (w1 & 0x3FF8u));
+          const uint32_t d2 = (Q & 31u) + e1.y;
+          const uint32_t w2 = (uint32_t)((((uint64_t)hi << 32) | lo) >> d2);
+          const uint2 e2 = *reinterpret_cast<const uint2*>(lutb + (w2 & 0x3FF8u));
+          Q += e1.y + e2.y;
+          if (SYMB == 4) {
+            const uint32_t* x1 = xs + (16 * g + 2 * p) * MT;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) acc[j] = dot2(e2.x, x1[MT + j], dot2(e1.x, x1[j], acc[j]));
+          } else {
+            const uint32_t w = e1.x | (e2.x << 16);
+            const uint32_t* x1 = xs + (8 * g + p) * MT;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) acc[j] = dot2(w, x1[j], acc[j]);
+          }
+        }
+        if (GPSUB == 1 || h == 1) {  // sub-block end: scale x partial dot, next scale byte
+          const float scv = KQ == KQ_Q6_K ? (float)(int)(int8_t)(uint8_t)scq : (float)(uint32_t)(scq & 255u);
+          scq >>= 8;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            tsum[j] = fmaf(scv, acc[j], tsum[j]);
+            acc[j] = 0.f;
+          }
+        }
+      }
+    }
+    // super-block: y += d sum_j sc_j (x . q)_j - dmin sum_j m_j (sum x)_j
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      tot[j] = fmaf(dA, tsum[j], tot[j]);
+      if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot[j] = fmaf(-dB, msum[j], tot[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MT; ++j)
+    if (j < mt) E.P[((size_t)tc * mt + j) * N + n] = tot[j];
+}
+
+int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 8 : 4; }
+
+static size_t ring_smem(int symbits, int kqt, int MT, int WPB, int RS) {
+  const int TW = symbits == 4 ? 2 * TK : TK, GW = kq_gw(kqt);
+  return (size_t)LUTN * 8 + (size_t)(TW / 2) * MT * 4 + (size_t)(TW / GW) * MT * 4 + (size_t)WPB * 2 * (RS + 1) * 128;
+}
+
+template <int KQ, int MT, int RS>
+static hipError_t ring_launch(const GroupPlan& p, hipStream_t s) {
+  constexpr int WPB = RS == 16 ? 8 : 4;
+  const size_t smem = ring_smem(kq_symbits(KQ), KQ, MT, WPB, RS);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_ring<KQ, MT, WPB, RS>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_fused_ring<KQ, MT, WPB, RS>), dim3(p.blocks), dim3(WPB * 64), smem, s, p);
+  return hipGetLastError();
+}
+
+template <int KQ, int RS>
+static hipError_t ring_mt(const GroupPlan& p, hipStream_t s) {
+  if (p.mt <= 1) return ring_launch<KQ, 1, RS>(p, s);
+  if (p.mt <= 2) return ring_launch<KQ, 2, RS>(p, s);
+  if (p.mt <= 4) return ring_launch<KQ, 4, RS>(p, s);
+  if (p.mt <= 8) return ring_launch<KQ, 8, RS>(p, s);
+  return ring_launch<KQ, 16, RS>(p, s);
+}
+
+template <int KQ>
+static hipError_t ring_kq(const GroupPlan& p, hipStream_t s) {
+  return p.e[0].M.ring_rows == 16 ? ring_mt<KQ, 16>(p, s) : ring_mt<KQ, 32>(p, s);
+}
+
+hipError_t launch_fused_group(const GroupPlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.mt < 1 || p.mt > 16 || p.blocks < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt, rs = p.e[0].M.ring_rows;
+  for (int i = 0; i < p.n; ++i)
+    if (p.e[i].M.kqt != kqt || p.e[i].M.ring_rows != rs || !p.e[i].M.sched) return hipErrorInvalidValue;
+  if (rs != 16 && rs != 32) return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return ring_kq<KQ_Q4_K>(p, s);
+    case KQ_Q5_K: return ring_kq<KQ_Q5_K>(p, s);
+    case KQ_Q6_K: return ring_kq<KQ_Q6_K>(p, s);
+    case KQ_IQ4_XS: return ring_kq<KQ_IQ4_XS>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+__global__ void k_reduce_group(ReducePlan plan) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= plan.total) return;
+  ReduceEntry E = plan.e[0];
+#pragma unroll
+  for (int k = 1; k < MAX_GROUP; ++k)
+    if (k < plan.n && i >= plan.e[k].out0) E = plan.e[k];
+  const int o = i - E.out0, j = o / E.N, n = o - j * E.N, mt = plan.m * plan.per;
+  float a = 0.f;
+  for (int tc = 0; tc < E.KT; ++tc)
+    for (int q = 0; q < plan.per; ++q) a += E.P[((size_t)tc * mt + j * plan.per + q) * E.N + n];
+  E.Y[(size_t)j * E.ldy + n] = a;
+}
+
+hipError_t launch_reduce_group(const ReducePlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.total < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_reduce_group, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
 // ── ordered reduction over tile columns ──────────────────────────────────────────────────────────────────
 __global__ void k_reduce(const float* __restrict__ P, float* __restrict__ Y, int m, int per, int N, int ldy, int KT) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -290,7 +585,7 @@ __global__ void __launch_bounds__(256) k_decode(DevMat M, uint8_t* __restrict__ 
   __syncthreads();
   if (!active) return;
   const int tr = t / KT, tc = t - tr * KT;
-  uint32_t pos = half ? (uint32_t)M.mid[(size_t)t * 32 + l] : 0u;
+  uint32_t pos = half ? (uint32_t)M.mid[(size_t)t * 32 + l] : (uint32_t)GUARD_BITS;
   const uint32_t* lw = tw + l;
   uint8_t* row = out + (size_t)((tr - tr0) * TN + half * 32 + l) * K + (size_t)tc * TW;
 #pragma unroll 1

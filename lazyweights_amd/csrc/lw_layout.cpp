@@ -34,20 +34,19 @@ static void parallel_for(int n, int threads, const std::function<void(int, int)>
 
 namespace {
 
-// A lane's bit stream: `nw` words starting at a word-aligned position, read through `word(i)`.
-template <class W>
-inline bool decode_lane(const uint16_t* lut, W word, uint64_t nw, uint64_t start, uint32_t& mid, uint64_t& end) {
-  uint64_t bp = start;
+// Decode one lane (512 symbols) from a bit source: bits32(off) = 32 stream bits from lane offset `off`.
+// pos[i] = lane bit offset before symbol i (i = 0..512). Fails if the lane runs past `limit` bits.
+template <class B>
+inline bool decode_lane(const uint16_t* lut, B bits32, uint64_t limit, uint32_t* pos) {
+  uint64_t bp = 0;
   for (int i = 0; i < LANE_SYMS; ++i) {
-    if (i == TK) mid = (uint32_t)(bp - start);
-    const uint64_t wi = bp >> 5;
-    if (wi >= nw) return false;
-    const uint64_t lo = word(wi), hi = wi + 1 < nw ? word(wi + 1) : 0;
-    const uint16_t e = lut[((lo | (hi << 32)) >> (bp & 31)) & (LUTN - 1)];
+    pos[i] = (uint32_t)bp;
+    if (bp >= limit) return false;
+    const uint16_t e = lut[bits32(bp) & (LUTN - 1)];
     bp += e >> 8;
   }
-  end = bp;
-  return true;
+  pos[LANE_SYMS] = (uint32_t)bp;
+  return bp <= limit;
 }
 
 inline uint32_t bits_at(const uint32_t* pay, uint64_t pw, uint64_t b) {
@@ -56,9 +55,105 @@ inline uint32_t bits_at(const uint32_t* pay, uint64_t pw, uint64_t b) {
   return (uint32_t)((lo | (hi << 32)) >> (b & 31));
 }
 
-// Fill tile rows from per-lane word sources once lane lengths are known.
-void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits,
-                   const std::function<uint32_t(int, int, uint32_t)>& lane_word, int threads) {
+// Ring staging schedule of one tile (see the ring kernel): front f stages CHUNK_ROWS-row chunks of its rows, relative
+// to its base row; chunks loaded at group g reach LDS at the start of group g + 2. mn / mx = lowest / highest
+// relative row that any lane's windows touch in each group. Loads are issued just in time for group g + 2 (at most
+// MAX_CHUNKS_PER_GROUP per group). Returns false if a ring of RS rows cannot hold the schedule.
+bool ring_schedule(const int mn[2][GROUPS], const int mx[2][GROUPS], int RS, uint64_t& counts, int init[2]) {
+  counts = 0;
+  for (int f = 0; f < 2; ++f) {
+    init[f] = (std::max(mx[f][0], mx[f][1]) + CHUNK_ROWS) / CHUNK_ROWS;
+    if (CHUNK_ROWS * init[f] > RS + mn[f][0] || init[f] > 255) return false;
+    int issued = init[f], written = init[f];
+    int loads[GROUPS] = {0};
+    for (int g = 0; g < GROUPS; ++g) {
+      if (g >= 2) written += loads[g - 2];
+      if (mx[f][g] > CHUNK_ROWS * written - 1 || mn[f][g] < CHUNK_ROWS * written - RS) return false;
+      const int target = mx[f][std::min(g + 2, GROUPS - 1)];
+      while (CHUNK_ROWS * issued <= target && g + 2 < GROUPS && loads[g] < MAX_CHUNKS_PER_GROUP) {
+        ++loads[g];
+        ++issued;
+      }
+      counts |= (uint64_t)loads[g] << (32 * f + 2 * g);
+    }
+  }
+  return true;
+}
+
+// Per-tile load-time analysis shared by both input formats: lane positions -> mid offsets, lane lengths and the
+// ring schedule. `bits32(t, l, off)` reads the lane stream; `limit(t, l)` bounds its length.
+template <class B, class Lim, class Check>
+bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check check_end,
+                   std::vector<uint64_t>& lane_bits) {
+  L.mid.assign((size_t)T * LANES, 0);
+  L.sched.assign(2 * (size_t)T, 0);
+  lane_bits.assign((size_t)T * LANES, 0);
+  std::vector<uint8_t> ring_ok(T, 0);  // bit 0: RS 16 fits, bit 1: RS 32 fits
+  std::atomic<bool> bad(false);
+  parallel_for(T, threads, [&](int t0, int t1) {
+    std::vector<uint32_t> pos((size_t)LANES * (LANE_SYMS + 1));
+    for (int t = t0; t < t1 && !bad; ++t) {
+      for (int l = 0; l < LANES; ++l) {
+        uint32_t* p = pos.data() + (size_t)l * (LANE_SYMS + 1);
+        if (!decode_lane(L.lut, [&](uint64_t off) { return bits32(t, l, off); }, limit(t, l), p) ||
+            !check_end(t, l, p[LANE_SYMS])) {
+          bad = true;
+          break;
+        }
+        L.mid[(size_t)t * LANES + l] = (uint16_t)(p[TK] + GUARD);
+        lane_bits[(size_t)t * LANES + l] = p[LANE_SYMS];
+      }
+      if (bad) break;
+      int base1 = 1 << 30;
+      for (int l = 0; l < LANES; ++l) base1 = std::min<int>(base1, (int)(pos[(size_t)l * (LANE_SYMS + 1) + TK] >> 5));
+      int mn[2][GROUPS], mx[2][GROUPS];
+      for (int f = 0; f < 2; ++f)
+        for (int g = 0; g < GROUPS; ++g) {
+          const int base = f ? base1 : 0, s0 = f * TK + g * GROUP_SYMS, s1 = s0 + GROUP_SYMS - 2;
+          int lo = 1 << 30, hi = 0;
+          for (int l = 0; l < LANES; ++l) {
+            const uint32_t* p = pos.data() + (size_t)l * (LANE_SYMS + 1);
+            lo = std::min<int>(lo, (int)(p[s0] >> 5) - base);
+            hi = std::max<int>(hi, (int)(p[s1] >> 5) + 1 - base);
+          }
+          mn[f][g] = lo;
+          mx[f][g] = hi;
+        }
+      int init[2] = {0, 0};
+      uint64_t counts = 0;
+      uint8_t ok = 0;
+      for (int k = 1; k >= 0; --k) {  // a schedule valid for 16 rows is valid for 32 (same loads, looser checks)
+        uint64_t c;
+        int in[2];
+        if (base1 < 256 && ring_schedule(mn, mx, k ? 32 : 16, c, in)) {
+          ok |= (uint8_t)(1 << k);
+          counts = c;
+          init[0] = in[0];
+          init[1] = in[1];
+        }
+      }
+      ring_ok[t] = ok;
+      if (ok) {
+        L.sched[2 * (size_t)t] = counts;
+        L.sched[2 * (size_t)t + 1] = (uint64_t)base1 | (uint64_t)init[0] << 8 | (uint64_t)init[1] << 16;
+      }
+    }
+  });
+  if (bad) return false;
+  // one ring size per matrix: 16 rows if every tile fits, else 32; schedules of the chosen size
+  bool all16 = true, all32 = true;
+  for (int t = 0; t < T; ++t) {
+    all16 = all16 && (ring_ok[t] & 1);
+    all32 = all32 && (ring_ok[t] & 2);
+  }
+  L.ring_rows = all16 ? 16 : all32 ? 32 : 0;
+  return true;
+}
+
+// Fill tile rows from per-lane bit sources once lane lengths are known. Device lane streams carry GUARD leading
+// zero bits; word i of a lane holds its stream bits [32 i - GUARD, 32 i + 32 - GUARD).
+template <class B>
+void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits, B bits32, int threads) {
   L.rows.assign(T, 0);
   L.tbase.assign(T, 0);
   L.max_rows = 0;
@@ -68,7 +163,7 @@ void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits,
     for (int l = 0; l < LANES; ++l) {
       const uint64_t b = lane_bits[(size_t)t * LANES + l];
       total += b;
-      r = std::max<uint32_t>(r, (uint32_t)((b + 31) / 32));
+      r = std::max<uint32_t>(r, (uint32_t)((b + GUARD + 31) / 32));
     }
     L.rows[t] = (uint16_t)r;
     L.tbase[t] = (uint32_t)nwords;
@@ -80,10 +175,10 @@ void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits,
   parallel_for(T, threads, [&](int t0, int t1) {
     for (int t = t0; t < t1; ++t)
       for (int l = 0; l < LANES; ++l) {
-        const uint64_t nb = lane_bits[(size_t)t * LANES + l];
+        const uint64_t nb = lane_bits[(size_t)t * LANES + l] + GUARD;
         uint32_t* o = L.words.data() + L.tbase[t] + l;
         for (uint32_t i = 0; (uint64_t)i * 32 < nb; ++i) {
-          uint32_t v = lane_word(t, l, i);
+          uint32_t v = i == 0 ? bits32(t, l, 0) << GUARD : bits32(t, l, 32ull * i - GUARD);
           const uint64_t left = nb - (uint64_t)i * 32;
           if (left < 32) v &= (1u << left) - 1;
           o[(size_t)32 * i] = v;
@@ -109,41 +204,34 @@ bool build_layout_raw(const uint8_t* blob, size_t len, int N, int KS, int thread
   const uint32_t* starts = reinterpret_cast<const uint32_t*>(blob + 2 * LUTN);
   const uint32_t* pay = starts + (size_t)T * LANES;
   const uint64_t pw = (len - hdr) / 4;
-  for (size_t i = 0; i + 1 < (size_t)T * LANES; ++i)
+  const uint64_t nlanes = (uint64_t)T * LANES;
+  for (size_t i = 0; i + 1 < nlanes; ++i)
     if (starts[i] > starts[i + 1]) {
       err = "coded matrix: lane starts not increasing";
       return false;
     }
-  L.mid.assign((size_t)T * LANES, 0);
-  std::vector<uint64_t> lane_bits((size_t)T * LANES);
-  std::atomic<bool> bad(false);
-  parallel_for(T, threads, [&](int t0, int t1) {
-    for (int t = t0; t < t1 && !bad; ++t)
-      for (int l = 0; l < LANES; ++l) {
-        const size_t i = (size_t)t * LANES + l;
-        uint32_t mid = 0;
-        uint64_t end = 0;
-        if (!decode_lane(L.lut, [&](uint64_t w) { return (uint64_t)pay[w]; }, pw, starts[i], mid, end)) {
-          bad = true;
-          break;
-        }
-        // a lane ends where the next one starts; the last lane of the matrix before the 2 tail words
-        const uint64_t next = i + 1 < (size_t)T * LANES ? starts[i + 1] : (pw >= 2 ? (pw - 2) * 32 : 0);
-        if (i + 1 < (size_t)T * LANES ? end != next : end > next) {
-          bad = true;
-          break;
-        }
-        L.mid[i] = (uint16_t)mid;
-        lane_bits[i] = end - starts[i];
-      }
-  });
-  if (bad) {
+  if (pw < 2 || starts[nlanes - 1] > (pw - 2) * 32) {
+    err = "coded matrix: lane starts beyond the payload";
+    return false;
+  }
+  auto st = [&](int t, int l) { return (uint64_t)starts[(size_t)t * LANES + l]; };
+  auto bits32 = [&](int t, int l, uint64_t off) { return bits_at(pay, pw, st(t, l) + off); };
+  // a lane ends where the next one starts; the last lane of the matrix before the 2 tail words
+  auto next = [&](int t, int l) {
+    const size_t i = (size_t)t * LANES + l;
+    return i + 1 < nlanes ? (uint64_t)starts[i + 1] : (pw - 2) * 32;
+  };
+  auto limit = [&](int t, int l) { return next(t, l) - st(t, l); };
+  auto check_end = [&](int t, int l, uint64_t end) {
+    const size_t i = (size_t)t * LANES + l;
+    return i + 1 < nlanes ? end == limit(t, l) : end <= limit(t, l);
+  };
+  std::vector<uint64_t> lane_bits;
+  if (!analyse_tiles(L, T, threads, bits32, limit, check_end, lane_bits)) {
     err = "coded matrix: lane streams inconsistent with the lane starts (corrupt or truncated blob)";
     return false;
   }
-  finish_layout(L, T, lane_bits,
-                [&](int t, int l, uint32_t i) { return bits_at(pay, pw, starts[(size_t)t * LANES + l] + 32ull * i); },
-                threads);
+  finish_layout(L, T, lane_bits, bits32, threads);
   return true;
 }
 
@@ -166,48 +254,37 @@ bool build_layout_il(const uint8_t* data, size_t len, int N, int KS, bool compac
   const uint16_t* ovf = wc + ((T + 1) & ~1);
   const uint32_t* words = u + hw;
   const uint64_t nwt = len / 4 - hw;
+  for (int t = 0; t < T; ++t)
+    if ((uint64_t)tb[t] + 32ull * wc[t] > nwt || (t + 1 < T && tb[t + 1] < tb[t])) {
+      err = "pre-interleaved matrix: tile beyond the data";
+      return false;
+    }
   // lane word i of (t, l): interleaved part, then (compact) the lane's overflow run
   auto lane_avail = [&](int t, int l) -> uint64_t {
     if (!compact) return wc[t];
-    const uint64_t run_end = l < 31 ? ovf[(size_t)t * 32 + l + 1]
-                                    : (t + 1 < T ? (uint64_t)tb[t + 1] - tb[t] - 32ull * wc[t]
-                                                 : nwt - tb[t] - 32ull * wc[t]);
-    return (uint64_t)wc[t] + (run_end - ovf[(size_t)t * 32 + l]);
+    const uint64_t tile_end = t + 1 < T ? (uint64_t)tb[t + 1] : nwt;
+    const uint64_t run0 = (uint64_t)tb[t] + 32ull * wc[t] + ovf[(size_t)t * 32 + l];
+    const uint64_t run1 = l < 31 ? (uint64_t)tb[t] + 32ull * wc[t] + ovf[(size_t)t * 32 + l + 1] : tile_end;
+    return (uint64_t)wc[t] + (run1 > run0 ? std::min(run1, tile_end) - run0 : 0);
   };
   auto lane_word = [&](int t, int l, uint64_t i) -> uint32_t {
+    if (i >= lane_avail(t, l)) return 0u;
     const uint64_t idx = i < wc[t] ? (uint64_t)tb[t] + 32ull * i + l
                                    : (uint64_t)tb[t] + 32ull * wc[t] + ovf[(size_t)t * 32 + l] + (i - wc[t]);
     return idx < nwt ? words[idx] : 0u;
   };
-  for (int t = 0; t < T; ++t)
-    if ((uint64_t)tb[t] + 32ull * wc[t] > nwt) {
-      err = "pre-interleaved matrix: tile beyond the data";
-      return false;
-    }
-  L.mid.assign((size_t)T * LANES, 0);
-  std::vector<uint64_t> lane_bits((size_t)T * LANES);
-  std::atomic<bool> bad(false);
-  parallel_for(T, threads, [&](int t0, int t1) {
-    for (int t = t0; t < t1 && !bad; ++t)
-      for (int l = 0; l < LANES; ++l) {
-        const uint64_t nw = lane_avail(t, l);
-        uint32_t mid = 0;
-        uint64_t end = 0;
-        if (nw > 4096 || !decode_lane(L.lut, [&](uint64_t w) { return (uint64_t)lane_word(t, l, w); }, nw + 1, 0,
-                                      mid, end) ||
-            end > 32 * nw) {
-          bad = true;
-          break;
-        }
-        L.mid[(size_t)t * LANES + l] = (uint16_t)mid;
-        lane_bits[(size_t)t * LANES + l] = end;
-      }
-  });
-  if (bad) {
+  auto bits32 = [&](int t, int l, uint64_t off) {
+    const uint64_t w = off >> 5;
+    return (uint32_t)((((uint64_t)lane_word(t, l, w + 1) << 32) | lane_word(t, l, w)) >> (off & 31));
+  };
+  auto limit = [&](int t, int l) { return 32 * std::min<uint64_t>(lane_avail(t, l), 4096); };
+  auto check_end = [&](int, int, uint64_t) { return true; };
+  std::vector<uint64_t> lane_bits;
+  if (!analyse_tiles(L, T, threads, bits32, limit, check_end, lane_bits)) {
     err = "pre-interleaved matrix: lane streams inconsistent with the layout (corrupt export)";
     return false;
   }
-  finish_layout(L, T, lane_bits, [&](int t, int l, uint32_t i) { return lane_word(t, l, i); }, threads);
+  finish_layout(L, T, lane_bits, bits32, threads);
   return true;
 }
 

@@ -8,22 +8,36 @@
 
 namespace lw {
 
+// Every lane stream starts with GUARD zero bits in the device layout, so the window of the symbol at stream bit p is
+// read at q = p - GUARD and the table index is (window & 0x3FF8) = 8 * (11 stream bits): one AND per symbol.
+constexpr int GUARD = 3;
+// Zero rows appended after the last tile (read-ahead of the staging copies and of the 64-bit windows).
+constexpr int TAIL_ROWS = 8;
+// Symbols per staging group (one sub-block of the 4-bit formats) and groups per chain (256 symbols).
+constexpr int GROUP_SYMS = 16;
+constexpr int GROUPS = 16;
+// Rows per staged chunk (one 8-byte load per lane of a 32-lane front) and most chunks a front loads per group.
+constexpr int CHUNK_ROWS = 2;
+constexpr int MAX_CHUNKS_PER_GROUP = 2;
+
 // Device layout of one coded matrix (see DevMat in lw_kernels.h for the field meanings).
 struct Layout {
   uint16_t lut[2048];
   std::vector<uint32_t> tbase;  // [T]
-  std::vector<uint16_t> mid;    // [T][32]
+  std::vector<uint16_t> mid;    // [T][32] device bit offset of symbol 256 (guard included)
   std::vector<uint16_t> rows;   // [T]
   std::vector<uint32_t> words;  // tiles' word rows + zero tail
+  // ring staging schedule per tile, 2 x u64: word 0 = 2-bit counts of 2-row chunks that front 0 (bits 2g) and
+  // front 1 (bits 32 + 2g) load at group g; word 1 = base row of front 1 (bits 0-7), initial chunks of front 0
+  // (8-15) and front 1 (16-23)
+  std::vector<uint64_t> sched;
+  int ring_rows = 0;            // 16 or 32 rows per front; 0: the ring schedule does not fit (whole-tile kernels)
   int max_rows = 0;
   uint64_t payload_bits = 0;    // coded bits of all lanes
 };
 
-// Zero rows appended after the last tile (read-ahead of the staging copy and of the 64-bit window).
-constexpr int TAIL_ROWS = 3;
-
 // From a raw huf8/huf4p blob (lazyweights/bundle.py:14-21). N rows, KS symbols per row. Every lane is decoded once
-// on the host to find its second-row offset and exact length, which also validates the blob.
+// on the host to find its second-row offset, exact length and the staging schedule, which also validates the blob.
 bool build_layout_raw(const uint8_t* blob, size_t len, int N, int KS, int threads, Layout& L, std::string& err);
 
 // From the reference's pre-interleaved export (enc suffix _il / _ilc; kernels/llmrt.cu:454-470, 1206-1257).

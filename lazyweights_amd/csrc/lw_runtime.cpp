@@ -212,15 +212,17 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][tbase 4T][mid 64T][rows 2T] padded to 256 B, then the words
+  // [lut 4096 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)] padded to 256 B, then the words
   const size_t o_tb = 2 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
-  const size_t o_words = (o_rows + 2ull * T + 255) & ~(size_t)255;
+  const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15;
+  const size_t o_words = (o_sched + 16ull * T + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
   memcpy(host.data(), L.lut, 2 * lw::LUTN);
   memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
   memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
+  memcpy(host.data() + o_sched, L.sched.data(), 16ull * T);
   void* d = nullptr;
   if (hipMalloc(&d, bytes) != hipSuccess) {
     (void)hipGetLastError();
@@ -242,6 +244,8 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
   dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
+  dm.sched = reinterpret_cast<const uint4*>(b + o_sched);
+  dm.ring_rows = L.ring_rows;
   dm.side = nullptr;
   dm.N = (int)t.N;
   dm.K = (int)t.K;
@@ -304,13 +308,70 @@ int check_matmul(Tensor* t, const char* name) {
   return 0;
 }
 
-// fused path on device buffers: X16 [mt][K] fp16 pseudo-tokens, per = pseudo-tokens per output token
-int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, int ldy, hipStream_t s) {
+// Kernel selection for the fused path: 0 = ring kernel wherever the matrix has a ring schedule (default),
+// 1 = whole-tile kernel everywhere (kept as the fallback and for tests).
+int g_kernel_mode = 0;
+
+// Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
+// ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
+// others into whole-tile launches; then one ordered reduction per MAX_GROUP matrices. Partials of all matrices
+// live side by side in the model's P scratch.
+int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
+                    const int* ldy, hipStream_t s) {
   const int mt = m * per;
-  if (grow(M.P, M.P_cap, (size_t)t.dm.KT * mt * t.N * sizeof(float))) return -1;
-  HIPCHECK(lw::launch_fused(t.dm, X16, mt, M.P, s));
-  HIPCHECK(lw::launch_reduce(M.P, Y, m, per, (int)t.N, ldy, t.dm.KT, s));
+  std::vector<size_t> off(count + 1, 0);
+  for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
+  if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
+  lw::GroupPlan plan{};
+  plan.mt = mt;
+  auto flush = [&]() -> int {
+    if (plan.n) HIPCHECK(lw::launch_fused_group(plan, s));
+    plan.n = 0;
+    plan.blocks = 0;
+    return 0;
+  };
+  for (int i = 0; i < count; ++i) {
+    const lw::DevMat& dm = ts[i]->dm;
+    float* P = M.P + off[i];
+    if (g_kernel_mode == 1 || dm.ring_rows == 0) {
+      HIPCHECK(lw::launch_fused(dm, X16[i], mt, P, s));
+      continue;
+    }
+    if (plan.n && (plan.n == lw::MAX_GROUP || plan.e[0].M.kqt != dm.kqt || plan.e[0].M.ring_rows != dm.ring_rows))
+      if (flush()) return -1;
+    lw::GroupEntry& e = plan.e[plan.n++];
+    e.M = dm;
+    e.X2 = static_cast<const uint32_t*>(X16[i]);
+    e.P = P;
+    e.block0 = plan.blocks;
+    const int wpb = lw::group_waves_per_block(dm.ring_rows);
+    plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
+  }
+  if (flush()) return -1;
+  lw::ReducePlan rp{};
+  rp.m = m;
+  rp.per = per;
+  for (int i = 0; i < count; ++i) {
+    lw::ReduceEntry& e = rp.e[rp.n++];
+    e.P = M.P + off[i];
+    e.Y = Y[i];
+    e.N = (int)ts[i]->N;
+    e.KT = ts[i]->dm.KT;
+    e.ldy = ldy[i];
+    e.out0 = rp.total;
+    rp.total += m * (int)ts[i]->N;
+    if (rp.n == lw::MAX_GROUP || i + 1 == count) {
+      HIPCHECK(lw::launch_reduce_group(rp, s));
+      rp.n = 0;
+      rp.total = 0;
+    }
+  }
   return 0;
+}
+
+int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, int ldy, hipStream_t s) {
+  Tensor* tp = &t;
+  return fused_group_dev(M, &tp, &X16, 1, m, per, &Y, &ldy, s);
 }
 
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
@@ -642,15 +703,27 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
                         float* const* Y, void* stream) {
   Model* M = static_cast<Model*>(h);
-  if (!M || count < 1 || !names || !X || !Y) {
+  if (!M || count < 1 || !names || !X || !Y || m < 1 || m > 16) {
     g_err = "lw_group_matmul_dev: bad arguments";
     return -1;
   }
+  std::vector<Tensor*> ts(count);
+  std::vector<int> ldy(count);
   for (int i = 0; i < count; ++i) {
-    Tensor* t = M->find(names[i]);
-    if (check_matmul(t, names[i])) return -1;
-    if (lw_matmul_dev(h, names[i], X[i], 1, m, Y[i], (int)t->N, stream)) return -1;
+    ts[i] = M->find(names[i]);
+    if (check_matmul(ts[i], names[i])) return -1;
+    if (!X[i] || !Y[i]) {
+      g_err = "lw_group_matmul_dev: null buffer";
+      return -1;
+    }
+    ldy[i] = (int)ts[i]->N;
   }
+  return fused_group_dev(*M, ts.data(), X, count, m, 1, Y, ldy.data(), static_cast<hipStream_t>(stream));
+}
+
+int lw_set_kernel_mode(int mode) {
+  if (mode < 0 || mode > 1) return -1;
+  g_kernel_mode = mode;
   return 0;
 }
 
@@ -679,25 +752,57 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
   HIPCHECK(hipEventSynchronize(b));
   float ms = 0;
   HIPCHECK(hipEventElapsedTime(&ms, a, b));
-  // fused kernels alone: events around each fused launch (partials only; the ordered reduction excluded)
-  std::vector<hipEvent_t> ev(2 * (size_t)first[ngroups]);
+  // fused kernels alone: events around each group's fused launch(es), reductions excluded
+  std::vector<hipEvent_t> ev(2 * (size_t)ngroups);
   for (auto& e : ev) HIPCHECK(hipEventCreate(&e));
   double kms = 0;
+  int launches = 0;
   const int kit = std::max(1, std::min(iters, 20));
   for (int it = 0; it < kit; ++it) {
-    int idx = 0;
-    for (int g = 0; g < ngroups; ++g)
-      for (int i = first[g]; i < first[g + 1]; ++i, ++idx) {
-        Tensor* t = M->find(names[i]);
-        if (grow(M->P, M->P_cap, (size_t)t->dm.KT * m * t->N * sizeof(float))) return -1;
-        HIPCHECK(hipEventRecord(ev[2 * idx], s));
-        HIPCHECK(lw::launch_fused(t->dm, X[i], m, M->P, s));
-        HIPCHECK(hipEventRecord(ev[2 * idx + 1], s));
+    for (int g = 0; g < ngroups; ++g) {
+      std::vector<Tensor*> ts;
+      for (int i = first[g]; i < first[g + 1]; ++i) ts.push_back(M->find(names[i]));
+      const int mt = m;
+      size_t need = 0;
+      for (Tensor* t : ts) need += (size_t)t->dm.KT * mt * t->N;
+      if (grow(M->P, M->P_cap, need * sizeof(float))) return -1;
+      lw::GroupPlan plan{};
+      plan.mt = mt;
+      size_t off = 0;
+      HIPCHECK(hipEventRecord(ev[2 * g], s));
+      for (size_t i = 0; i < ts.size(); ++i) {
+        const lw::DevMat& dm = ts[i]->dm;
+        float* P = M->P + off;
+        off += (size_t)dm.KT * mt * ts[i]->N;
+        if (g_kernel_mode == 1 || dm.ring_rows == 0) {
+          HIPCHECK(lw::launch_fused(dm, X[first[g] + i], mt, P, s));
+          if (it == 0) ++launches;
+          continue;
+        }
+        if (plan.n && (plan.n == lw::MAX_GROUP || plan.e[0].M.kqt != dm.kqt || plan.e[0].M.ring_rows != dm.ring_rows)) {
+          HIPCHECK(lw::launch_fused_group(plan, s));
+          if (it == 0) ++launches;
+          plan.n = 0;
+          plan.blocks = 0;
+        }
+        lw::GroupEntry& e = plan.e[plan.n++];
+        e.M = dm;
+        e.X2 = static_cast<const uint32_t*>(X[first[g] + i]);
+        e.P = P;
+        e.block0 = plan.blocks;
+        const int wpb = lw::group_waves_per_block(dm.ring_rows);
+        plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
       }
+      if (plan.n) {
+        HIPCHECK(lw::launch_fused_group(plan, s));
+        if (it == 0) ++launches;
+      }
+      HIPCHECK(hipEventRecord(ev[2 * g + 1], s));
+    }
     HIPCHECK(hipEventSynchronize(ev.back()));
-    for (int i = 0; i < idx; ++i) {
+    for (int g = 0; g < ngroups; ++g) {
       float k = 0;
-      HIPCHECK(hipEventElapsedTime(&k, ev[2 * i], ev[2 * i + 1]));
+      HIPCHECK(hipEventElapsedTime(&k, ev[2 * g], ev[2 * g + 1]));
       kms += k;
     }
   }
@@ -706,7 +811,7 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
   (void)hipEventDestroy(b);
   out[0] = ms / iters;
   out[1] = kms / kit;
-  out[2] = first[ngroups];
+  out[2] = launches;
   return 0;
 }
 

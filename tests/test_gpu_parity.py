@@ -205,3 +205,46 @@ def test_full_config3_mixed(gpu, tmp_path):
 def test_full_config4_q5k_verify(gpu, tmp_path):
     from lazyweights_amd.configs import CONFIG4
     full_size_check(tmp_path, [m for m in CONFIG4 if m[0] in ("q5.gate", "q5.down")], (5,))
+
+
+def test_gpu_whole_tile_kernel_mode(fmt_rt, orc):
+    """The whole-tile kernel (the fallback for matrices without a ring schedule) stays exact too."""
+    import torch
+    rt, mats = fmt_rt
+    assert rt.lib.lw_set_kernel_mode(1) == 0
+    try:
+        for kqt, fmt, H in FORMATS:
+            mat = mats[fmt]
+            X = torch.randn(2, mat[3]).half()
+            _, y64 = reference_y(orc, mat, X.double().numpy())
+            say("whole-tile kernel", fmt)
+            Y = torch.zeros(2, mat[2], device="cuda")
+            rt.matmul_dev(fmt, X.cuda(), Y)
+            torch.cuda.synchronize()
+            check_err(Y.cpu().numpy(), y64, fmt + " whole-tile")
+    finally:
+        rt.lib.lw_set_kernel_mode(0)
+
+
+def test_gpu_grouped_launch_matches_single(fmt_rt):
+    """lw_group_matmul_dev over mixed formats (several grouped launches + whole batches of reductions) gives the
+    same bits as one call per matrix."""
+    import ctypes
+
+    import torch
+    rt, mats = fmt_rt
+    names = list(mats)
+    X = [torch.randn(1, mats[nm][3]).half().cuda() for nm in names]
+    Yg = [torch.zeros(1, mats[nm][2], device="cuda") for nm in names]
+    Ys = [torch.zeros(1, mats[nm][2], device="cuda") for nm in names]
+    n = len(names)
+    rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                    (ctypes.c_void_p * n)(*[x.data_ptr() for x in X]), 1,
+                                    (ctypes.c_void_p * n)(*[y.data_ptr() for y in Yg]), None)
+    assert rc == 0, rt.lib.lw_last_error()
+    for nm, x, y in zip(names, X, Ys):
+        rt.matmul_dev(nm, x, y)
+    torch.cuda.synchronize()
+    say("grouped vs single", n)
+    for a, b in zip(Yg, Ys):
+        assert torch.equal(a, b)

@@ -1,26 +1,36 @@
-"""The device layout built at load time (lane-split interleaved words), checked on the CPU.
+"""The device layout built at load time (lane-split interleaved words, 3 guard bits per lane stream, ring staging
+schedules), checked on the CPU.
 
-A numpy emulation of the kernels' chain decode (chain L of a tile: lane L % 32 from bit 0, or from its `mid` offset
-for L >= 32; window = words rows r, r + 1 of the lane) must reproduce the reference decode of the golden blobs.
+Numpy emulations of the kernels (whole-tile: chain L of a tile = lane L % 32 from bit GUARD, or from its `mid`
+offset for L >= 32, window = word rows r, r + 1 of the lane; ring: the same chains reading 2-symbol windows from a
+per-front ring of staged rows filled on the tile's schedule) must reproduce the reference decode of the golden
+blobs, and every window the ring kernel reads must equal the true rows.
 """
+GUARD = 3
 import numpy as np
 import pytest
 
 from conftest import golden_cases, load_golden
 
 
-def build_layout(lib, blob, N, KS, pre_il=0, compact=0):
+def build_layout(lib, blob, N, KS, pre_il=0, compact=0, extra=False):
+    import ctypes
     b = np.frombuffer(blob, np.uint8) if isinstance(blob, bytes) else np.ascontiguousarray(blob, np.uint8)
     T = (N // 64) * (KS // 256)
     tbase = np.zeros(T, np.uint32)
     mid = np.zeros(T * 32, np.uint16)
     rows = np.zeros(T, np.uint16)
+    sched = np.zeros(2 * T, np.uint64)
+    rr = ctypes.c_int(0)
     n = lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, tbase.ctypes.data, mid.ctypes.data,
-                            rows.ctypes.data, None, 0)
+                            rows.ctypes.data, sched.ctypes.data, ctypes.byref(rr), None, 0)
     if n < 0:
         return None
     words = np.zeros(n, np.uint32)
-    lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, None, None, None, words.ctypes.data, n)
+    lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, None, None, None, None, None,
+                        words.ctypes.data, n)
+    if extra:
+        return tbase, mid.reshape(T, 32), rows, words, sched, rr.value
     return tbase, mid.reshape(T, 32), rows, words
 
 
@@ -33,7 +43,7 @@ def emulate_decode(lut, tbase, mid, rows, words, N, KS):
     for t in range(len(tbase)):
         tr, tc = divmod(t, KT)
         lanes = np.arange(64) % 32
-        pos = np.where(np.arange(64) >= 32, mid[t][lanes], 0).astype(np.uint64)
+        pos = np.where(np.arange(64) >= 32, mid[t][lanes], GUARD).astype(np.uint64)
         base = int(tbase[t]) + lanes
         assert int(rows[t]) * 32 + int(tbase[t]) <= len(words)
         for c in range(256):
@@ -70,9 +80,9 @@ def test_layout_mid_is_first_row_length(lib, case):
         tr, tc = divmod(t, KT)
         for l in range(32):
             first = g["sym"][tr * 64 + l, tc * 256:(tc + 1) * 256]
-            assert mid[t, l] == L[first].sum()
+            assert mid[t, l] == GUARD + L[first].sum()
             second = g["sym"][tr * 64 + 32 + l, tc * 256:(tc + 1) * 256]
-            assert rows[t] >= (L[first].sum() + L[second].sum() + 31) // 32
+            assert rows[t] >= (GUARD + L[first].sum() + L[second].sum() + 31) // 32
 
 
 def test_layout_rejects_corrupt_blob(lib):
@@ -140,3 +150,79 @@ def test_layout_from_reference_export(lib, compact):
     raw = build_layout(lib, g["blob"], N, KS)
     for a, b in zip(lay, raw):      # same device layout either way
         assert np.array_equal(a, b)
+
+
+def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
+    """The ring kernel's staging and 2-symbol windows (k_fused_ring), per tile and front."""
+    KT = KS // 256
+    lut = lut.astype(np.uint64)
+    out = np.zeros((N, KS), np.uint8)
+    l = np.arange(32)
+    for t in range(len(tbase)):
+        tr, tc = divmod(t, KT)
+        counts, meta = int(sched[2 * t]), int(sched[2 * t + 1])
+        base1, init = meta & 255, [(meta >> 8) & 255, (meta >> 16) & 255]
+        for f in range(2):
+            base = base1 if f else 0
+            W = lambda r: words[int(tbase[t]) + 32 * (base + r) + l]   # noqa: E731
+            ring = np.zeros((RS + 1, 32), np.uint32)
+
+            def put(k):
+                for i in range(2):
+                    r = 2 * k + i
+                    ring[r & (RS - 1)] = W(r)
+                    if r & (RS - 1) == 0:
+                        ring[RS] = W(r)
+            for k in range(init[f]):
+                put(k)
+            issued = written = init[f]
+            pend = [[], []]
+            Q = ((mid[t].astype(np.int64) - GUARD) if f else np.zeros(32, np.int64)) - 32 * base
+            assert np.all(Q >= 0)
+            col = 0
+            for g in range(16):
+                h = g & 1
+                for k in pend[h]:
+                    put(k)
+                    written += 1
+                pend[h] = []
+                for _ in range((counts >> (32 * f + 2 * g)) & 3):
+                    pend[h].append(issued)
+                    issued += 1
+                for p in range(8):
+                    r = Q >> 5
+                    lo = ring[r & (RS - 1), l].astype(np.uint64)
+                    hi = ring[(r & (RS - 1)) + 1, l].astype(np.uint64)
+                    assert np.array_equal(lo, W(r)) and np.array_equal(hi, W(r + 1)), (t, f, g, p)
+                    win = (hi << np.uint64(32)) | lo
+                    e1 = lut[((win >> (Q & 31).astype(np.uint64)) >> np.uint64(3)) & np.uint64(2047)]
+                    d2 = (Q & 31) + (e1 >> np.uint64(8)).astype(np.int64)
+                    e2 = lut[((win >> d2.astype(np.uint64)) >> np.uint64(3)) & np.uint64(2047)]
+                    rows_out = tr * 64 + 32 * f + l
+                    out[rows_out, tc * 256 + col] = (e1 & np.uint64(255)).astype(np.uint8)
+                    out[rows_out, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
+                    col += 2
+                    Q = Q + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+    return out
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_ring_schedule_emulation(lib, case):
+    g = load_golden(case)
+    N, KS = g["sym"].shape
+    tbase, mid, rows, words, sched, RS = build_layout(lib, g["blob"], N, KS, extra=True)
+    if RS == 0:
+        pytest.skip("no ring schedule for this matrix (whole-tile kernel)")
+    got = emulate_ring(g["lut"], tbase, mid, words, sched, RS, N, KS, g["sym"])
+    assert np.array_equal(got, g["decoded"])
+
+
+def test_ring_schedules_exist_for_benchmark_shapes(lib):
+    """Every BASELINE format gets a ring schedule (16 rows) at realistic entropies."""
+    from lazyweights_amd import bundle
+    for kqt, H in ((1, 2.3), (1, 2.6), (2, 3.4), (3, 4.3), (4, 2.6)):
+        codes, _ = bundle.synth_matrix(kqt, 256, 4096, H, 77)
+        blob, _ = bundle.encode_huf8(bundle.form_symbols(kqt, codes))
+        ks = 2048 if kqt in (1, 4) else 4096
+        lay = build_layout(lib, blob, 256, ks, extra=True)
+        assert lay[5] == 16, (kqt, H, lay[5])
