@@ -90,7 +90,7 @@ __device__ __forceinline__ void side_scale(const uint32_t* w, int j, float& s, f
 
 // Sub-block scales of one super-block packed as bytes, consumed low byte first (reference llmrt.cu:125-149; Q4_K /
 // Q5_K fields per llama.cpp get_scale_min_k4, four at a time): s_j = dA * byte_j (Q6_K: signed bytes, 16 of them in
-// scq then scq2; IQ4_XS: ls_j - 32 as a signed byte), o_j = dB * m_j (side_mins).
+// scq then scq2; IQ4_XS: ls_j - 32, also signed), o_j = dB * m_j (side_mins).
 template <int KQ>
 __device__ __forceinline__ void side_packed(const uint32_t* w, uint64_t& scq, uint64_t& scq2, float& dA, float& dB) {
   if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
@@ -440,7 +440,8 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
           }
         }
         if (GPSUB == 1 || h == 1) {  // sub-block end: scale x partial dot, next scale byte
-          const float scv = KQ == KQ_Q6_K ? (float)(int)(int8_t)(uint8_t)scq : (float)(uint32_t)(scq & 255u);
+          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                               : (float)(uint32_t)(scq & 255u);
           scq >>= 8;
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
