@@ -14,7 +14,7 @@ namespace lw {
 //                              starts at bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
 //   side  u8[N][K/256][SB]     K-quant side bytes as in the bundle's <name>.kqs
 //   sched u32x4[T]             ring staging schedule of each tile (lw_layout.h, Layout::sched)
-// Every lane stream starts with GUARD = 3 zero bits (symbol 0 at stream bit 3).
+// Every lane stream starts with GUARD = 2 zero bits (symbol 0 at stream bit 2).
 struct DevMat {
   const uint16_t* lut;
   const uint32_t* tbase;

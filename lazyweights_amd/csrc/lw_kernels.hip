@@ -24,7 +24,7 @@ namespace lw {
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 // leading zero bits of every device lane stream (lw_layout.h GUARD)
-constexpr int GUARD_BITS = 3;
+constexpr int GUARD_BITS = 2;
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
@@ -303,9 +303,27 @@ __device__ __forceinline__ void ring_stage(uint2* ring2, const uint2* src, int s
 // As k_fused, but a wave does not stage its whole tile: each front (lanes 0-31 from bit GUARD, lanes 32-63 from
 // their `mid` offsets) keeps a ring of RS word rows (+ one mirror row for the window's read-ahead) and streams 2-row
 // chunks (one 8-byte load per lane) from HBM on the tile's load-time schedule (Layout::sched): chunks loaded at
-// group g are written to the ring at the start of group g + 2, so their latency hides behind two groups of decode. Windows are 64 bits (rows r, r + 1)
-// and yield two symbols each: the first at the guard-aligned offset (alignbit), the second by a 64-bit shift.
+// group g are written to the ring at the start of group g + 2, so their latency hides behind two groups of decode.
+// Windows are 64 bits (rows r, r + 1) and yield two symbols each: the first at the guard-aligned offset
+// (alignbit), the second by a 64-bit shift.
+//
+// The decode table holds 4-byte entries (8 KB, half the LDS bank traffic of {value, length} pairs): bits 0-7 =
+// code length; 4-bit formats: bytes 2 and 3 = the pair's two grid bytes (Q4_K: q; IQ4_XS: kv[q] + 128), which one
+// byte permute turns into two fp16 denormals g * 2^-24 for v_dot2 (exact: g < 256; the 2^24 is folded into d);
+// 8-bit formats: bits 16-31 = fp16(f(q)). The position update adds whole entries: only bits 0-8 of Q are ever
+// used (ring row and bit offset), and the entries' upper halves only disturb bits >= 16.
 // block = WPB tile rows of one tile column of one matrix of the plan.
+template <int KQ>
+__device__ __forceinline__ uint32_t lut4_entry(uint32_t e) {
+  const uint32_t sym = e & 255u, len = e >> 8;
+  if (kq_symbits(KQ) == 4) {
+    if (KQ == KQ_IQ4_XS)
+      return len | (uint32_t)(IQ4_GRID[sym & 15u] + 128) << 16 | (uint32_t)(IQ4_GRID[sym >> 4] + 128) << 24;
+    return len | (sym & 15u) << 16 | (sym >> 4) << 24;
+  }
+  return len | f2h(grid_value<KQ>(sym)) << 16;
+}
+
 template <int KQ, int MT, int WPB, int RS>
 __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
@@ -313,11 +331,12 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
   constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
   constexpr int RING_WORDS = (RS + 1) * 32;
   constexpr int NTHR = WPB * 64;
+  constexpr bool XS_SGPR = MT == 1;  // m = 1: activations straight from the scalar cache
+  __shared__ uint32_t lut4[LUTN];
   extern __shared__ __align__(16) uint32_t smem[];
-  uint2* lut8 = reinterpret_cast<uint2*>(smem);
-  uint32_t* xs = smem + 2 * LUTN;
-  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);
-  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);
+  uint32_t* xs = smem;                                          // [NPAIR][MT] fp16 pairs
+  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);        // [NG][MT] sub-block sums of x
+  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);  // WPB x 2 fronts x (RS + 1) rows
 
   // the block's matrix: a uniform index into the plan, read through the kernel-argument segment (scalar loads)
   int mi = 0;
@@ -337,13 +356,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
   const int tr = (bl / KT) * WPB + wave;
   const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
 
-  for (int i = threadIdx.x; i < LUTN; i += NTHR) {
-    const uint32_t e = M.lut[i], sym = e & 255u;
-    uint32_t v;
-    if (SYMB == 4) v = f2h(grid_value<KQ>(sym & 15u)) | f2h(grid_value<KQ>(sym >> 4)) << 16;
-    else v = f2h(grid_value<KQ>(sym));
-    lut8[i] = make_uint2(v, e >> 8);
-  }
+  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(M.lut[i]);
   for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
     const int j = i / NPAIR, c = i - j * NPAIR;
     xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
@@ -377,14 +390,19 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
   int pend0 = 0, pend1 = 0;
 
   uint32_t Q = (f ? (uint32_t)M.mid[(size_t)t * 32 + l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f;
-  const uint32_t* rl = ring + l;
-  const char* lutb = reinterpret_cast<const char*>(lut8);
+  // this lane's column of the ring as one opaque byte address, so a window address is (row offset) + base
+  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
+  asm volatile("" : "+v"(rlb));
   const int n = tr * TN + f * 32 + l;
   const uint8_t* srow = M.side + ((size_t)n * (K / 256) + (size_t)tc * (TW / 256)) * SB;
-  constexpr int NSB = TW / 256;    // super-blocks per tile column
-  constexpr int GPS = 16 / NSB;    // staging groups (16 symbols) per super-block
-  constexpr int NSUB = 256 / GW;   // sub-blocks per super-block
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);  // uniform: this tile column's x pairs (m = 1)
+  constexpr int NSB = TW / 256;      // super-blocks per tile column
+  constexpr int GPS = 16 / NSB;      // staging groups (16 symbols) per super-block
+  constexpr int NSUB = 256 / GW;     // sub-blocks per super-block
   constexpr int GPSUB = GPS / NSUB;  // groups per sub-block (2 for Q5_K, else 1)
+  // 4-bit formats accumulate in units of 2^-24 (denormal grid values); IQ4_XS grid bytes carry a +128 bias
+  constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
   float tot[MT], acc[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) tot[j] = acc[j] = 0.f;
@@ -394,12 +412,12 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
     uint32_t sw[5];
     side_load<KQ>(srow + sb * SB, sw);
     float dA, dB;
-    uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K), consumed low byte first
-    float msum[MT];
+    uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K / IQ4_XS), consumed low byte first
     side_packed<KQ>(sw, scq, scq2, dA, dB);
+    float msum[MT], tsum[MT], csum[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
-      msum[j] = 0.f;
+      msum[j] = tsum[j] = csum[j] = 0.f;
       if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
         float mf[8];
         side_mins(sw, mf);
@@ -407,9 +425,6 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
         for (int jj = 0; jj < NSUB; ++jj) msum[j] = fmaf(mf[jj], xg[(sb * NSUB + jj) * MT + j], msum[j]);
       }
     }
-    float tsum[MT];
-#pragma unroll
-    for (int j = 0; j < MT; ++j) tsum[j] = 0.f;
 #pragma unroll 1
     for (int gg2 = 0; gg2 < GPS; gg2 += 2) {
       if (KQ == KQ_Q6_K && gg2 == 8) scq = scq2;
@@ -420,42 +435,57 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
         else ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend1, st10, st11);
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          const uint32_t* a = rl + ((Q >> 5) & (RS - 1)) * 32;
+          typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+          LdsU32* a = (LdsU32*)(rlb + ((Q & ((RS - 1) << 5)) << 2));
           const uint32_t lo = a[0], hi = a[32];
           const uint32_t w1 = __builtin_amdgcn_alignbit(hi, lo, Q);
-          const uint2 e1 = *reinterpret_cast<const uint2*>(lutb + (w1 & 0x3FF8u));
-          const uint32_t d2 = (Q & 31u) + e1.y;
-          const uint32_t w2 = (uint32_t)((((uint64_t)hi << 32) | lo) >> d2);
-          const uint2 e2 = *reinterpret_cast<const uint2*>(lutb + (w2 & 0x3FF8u));
-          Q += e1.y + e2.y;
+          const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w1 & 0x1FFCu));
+          const uint32_t d2 = (Q & 31u) + e1;  // the 64-bit shift reads bits 0-5: offset + length
+          const uint32_t w2 = (uint32_t)((((uint64_t)hi << 32) | lo) >> (d2 & 63u));
+          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w2 & 0x1FFCu));
+          Q = Q + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
           if (SYMB == 4) {
-            const uint32_t* x1 = xs + (16 * g + 2 * p) * MT;
+            const uint32_t v1 = __builtin_amdgcn_perm(e1, e1, 0x0C030C02u), v2 = __builtin_amdgcn_perm(e2, e2, 0x0C030C02u);
+            const int c = 16 * g + 2 * p;
+            if (XS_SGPR) {
+              acc[0] = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc[0]));
+            } else {
+              const uint32_t* x1 = xs + c * MT;
 #pragma unroll
-            for (int j = 0; j < MT; ++j) acc[j] = dot2(e2.x, x1[MT + j], dot2(e1.x, x1[j], acc[j]));
+              for (int j = 0; j < MT; ++j) acc[j] = dot2(v2, x1[MT + j], dot2(v1, x1[j], acc[j]));
+            }
           } else {
-            const uint32_t w = e1.x | (e2.x << 16);
-            const uint32_t* x1 = xs + (8 * g + p) * MT;
+            const uint32_t w = __builtin_amdgcn_perm(e2, e1, 0x07060302u);
+            const int c = 8 * g + p;
+            if (XS_SGPR) {
+              acc[0] = dot2(w, xcol[c], acc[0]);
+            } else {
+              const uint32_t* x1 = xs + c * MT;
 #pragma unroll
-            for (int j = 0; j < MT; ++j) acc[j] = dot2(w, x1[j], acc[j]);
+              for (int j = 0; j < MT; ++j) acc[j] = dot2(w, x1[j], acc[j]);
+            }
           }
         }
         if (GPSUB == 1 || h == 1) {  // sub-block end: scale x partial dot, next scale byte
           const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
                                                                : (float)(uint32_t)(scq & 255u);
           scq >>= 8;
+          const int sub = sb * NSUB + (KQ == KQ_Q5_K ? (gg2 + h) / 2 : gg2 + h);
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             tsum[j] = fmaf(scv, acc[j], tsum[j]);
+            if (KQ == KQ_IQ4_XS) csum[j] = fmaf(scv, xg[sub * MT + j], csum[j]);
             acc[j] = 0.f;
           }
         }
       }
     }
-    // super-block: y += d sum_j sc_j (x . q)_j - dmin sum_j m_j (sum x)_j
+    // super-block: y += d sum_j sc_j (x . q)_j - dmin sum_j m_j (sum x)_j  (IQ4_XS: minus the +128 grid bias)
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
-      tot[j] = fmaf(dA, tsum[j], tot[j]);
+      tot[j] = fmaf(dA * VSCALE, tsum[j], tot[j]);
       if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot[j] = fmaf(-dB, msum[j], tot[j]);
+      if (KQ == KQ_IQ4_XS) tot[j] = fmaf(-128.f * dA, csum[j], tot[j]);
     }
   }
 #pragma unroll
@@ -465,9 +495,10 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
 
 int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 8 : 4; }
 
+// dynamic LDS of the ring kernel (the 8 KB decode table is static)
 static size_t ring_smem(int symbits, int kqt, int MT, int WPB, int RS) {
   const int TW = symbits == 4 ? 2 * TK : TK, GW = kq_gw(kqt);
-  return (size_t)LUTN * 8 + (size_t)(TW / 2) * MT * 4 + (size_t)(TW / GW) * MT * 4 + (size_t)WPB * 2 * (RS + 1) * 128;
+  return (size_t)(TW / 2) * MT * 4 + (size_t)(TW / GW) * MT * 4 + (size_t)WPB * 2 * (RS + 1) * 128;
 }
 
 template <int KQ, int MT, int RS>

@@ -9,8 +9,8 @@
 namespace lw {
 
 // Every lane stream starts with GUARD zero bits in the device layout, so the window of the symbol at stream bit p is
-// read at q = p - GUARD and the table index is (window & 0x3FF8) = 8 * (11 stream bits): one AND per symbol.
-constexpr int GUARD = 3;
+// read at q = p - GUARD and the byte offset of its 4-byte table entry is (window & 0x1FFC): one AND per symbol.
+constexpr int GUARD = 2;
 // Zero rows appended after the last tile (read-ahead of the staging copies and of the 64-bit windows).
 constexpr int TAIL_ROWS = 8;
 // Symbols per staging group (one sub-block of the 4-bit formats) and groups per chain (256 symbols).

@@ -1,4 +1,4 @@
-"""The device layout built at load time (lane-split interleaved words, 3 guard bits per lane stream, ring staging
+"""The device layout built at load time (lane-split interleaved words, 2 guard bits per lane stream, ring staging
 schedules), checked on the CPU.
 
 Numpy emulations of the kernels (whole-tile: chain L of a tile = lane L % 32 from bit GUARD, or from its `mid`
@@ -6,7 +6,7 @@ offset for L >= 32, window = word rows r, r + 1 of the lane; ring: the same chai
 per-front ring of staged rows filled on the tile's schedule) must reproduce the reference decode of the golden
 blobs, and every window the ring kernel reads must equal the true rows.
 """
-GUARD = 3
+GUARD = 2
 import numpy as np
 import pytest
 
@@ -195,9 +195,9 @@ def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
                     hi = ring[(r & (RS - 1)) + 1, l].astype(np.uint64)
                     assert np.array_equal(lo, W(r)) and np.array_equal(hi, W(r + 1)), (t, f, g, p)
                     win = (hi << np.uint64(32)) | lo
-                    e1 = lut[((win >> (Q & 31).astype(np.uint64)) >> np.uint64(3)) & np.uint64(2047)]
+                    e1 = lut[((win >> (Q & 31).astype(np.uint64)) >> np.uint64(GUARD)) & np.uint64(2047)]
                     d2 = (Q & 31) + (e1 >> np.uint64(8)).astype(np.int64)
-                    e2 = lut[((win >> d2.astype(np.uint64)) >> np.uint64(3)) & np.uint64(2047)]
+                    e2 = lut[((win >> d2.astype(np.uint64)) >> np.uint64(GUARD)) & np.uint64(2047)]
                     rows_out = tr * 64 + 32 * f + l
                     out[rows_out, tc * 256 + col] = (e1 & np.uint64(255)).astype(np.uint8)
                     out[rows_out, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
