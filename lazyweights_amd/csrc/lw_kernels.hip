@@ -325,7 +325,7 @@ __device__ __forceinline__ uint32_t lut4_entry(uint32_t e) {
 }
 
 template <int KQ, int MT, int WPB, int RS>
-__global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
+__global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 6 : (MT <= 8 ? 4 : 2)) k_f
     if (j < mt) E.P[((size_t)tc * mt + j) * N + n] = tot[j];
 }
 
-int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 8 : 4; }
+int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 16 : 8; }
 
 // dynamic LDS of the ring kernel (the 8 KB decode table is static)
 static size_t ring_smem(int symbits, int kqt, int MT, int WPB, int RS) {
@@ -503,7 +503,7 @@ static size_t ring_smem(int symbits, int kqt, int MT, int WPB, int RS) {
 
 template <int KQ, int MT, int RS>
 static hipError_t ring_launch(const GroupPlan& p, hipStream_t s) {
-  constexpr int WPB = RS == 16 ? 8 : 4;
+  constexpr int WPB = RS == 16 ? 16 : 8;
   const size_t smem = ring_smem(kq_symbits(KQ), KQ, MT, WPB, RS);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_ring<KQ, MT, WPB, RS>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
