@@ -44,6 +44,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
+                         "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU leg); run with --gpus 1",
@@ -93,6 +96,17 @@ def main():
                 if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, m, yy, stream) != 0:
                     raise RuntimeError(lib.lw_last_error().decode())
 
+        if a.profile:
+            for _ in range(max(1, a.steps)):
+                step()
+            src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+            dst = torch.empty_like(src)
+            dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
+            torch.cuda.synchronize()
+            lib.lw_stream_read_gbps(256 << 20, 1)  # calibration: k_stream_read, 256 MiB read per launch
+            log("bench --profile: %d passes over %d layers + 256 MiB copy done" % (max(1, a.steps), a.layers))
+            rt.close()
+            return
         for _ in range(a.warmup):
             step()
         torch.cuda.synchronize()

@@ -35,6 +35,15 @@ __host__ __device__ constexpr int kq_ncodes(int kqt) {
   return kqt == KQ_Q5_K ? 32 : kqt == KQ_Q6_K ? 64 : 16;
 }
 
+// Device order of the side records (load-time permutation of the bundle's [N][K/256][SB]): tile-major, so that the
+// 64 rows of one tile and one of its super-blocks are 64 consecutive records and a wave reads them as whole cache
+// lines once. Record of row n, super-block b (nsb = super-blocks per tile column: 2 for 4-bit symbols, 1 for 8-bit;
+// KT = tile columns): ((tile * nsb + b % nsb) * 64 + n % 64), tile = (n / 64) * KT + b / nsb.
+__host__ __device__ inline uint64_t side_record(int n, int b, int KT, int nsb) {
+  const uint64_t tile = (uint64_t)(n / TN) * (uint64_t)KT + (uint64_t)(b / nsb);
+  return (tile * (uint64_t)nsb + (uint64_t)(b % nsb)) * TN + (uint64_t)(n % TN);
+}
+
 // IQ4_XS non-linear grid (reference kernels/llmrt.cu:117, scripts/a2_kq_bundle.py:42)
 constexpr int8_t IQ4_GRID[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 

@@ -12,7 +12,7 @@ namespace lw {
 //   mid   u16[T][32]           bit offset, within lane l's stream, of the lane's second row (symbol 256)
 //   words u32[...]             tile t: word i of lane l at tbase[t] + 32 i + l, i < rows[t]; every lane stream
 //                              starts at bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
-//   side  u8[N][K/256][SB]     K-quant side bytes as in the bundle's <name>.kqs
+//   side  u8[N*K/256][SB]      K-quant side records of the bundle's <name>.kqs in tile-major order (side_record)
 //   sched u32x4[T]             ring staging schedule of each tile (lw_layout.h, Layout::sched)
 // Every lane stream starts with GUARD = 2 zero bits (symbol 0 at stream bit 2).
 struct DevMat {

@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(256) k_fused(DevMat M, const uint32_t* __restr
 #pragma unroll 1
   for (int sb = 0; sb < TW / 256; ++sb) {
     uint32_t sw[5];
-    side_load<KQ>(M.side + ((size_t)n * (K / 256) + (size_t)tc * (TW / 256) + sb) * SB, sw);
+    side_load<KQ>(M.side + side_record(n, tc * (TW / 256) + sb, M.KT, TW / 256) * SB, sw);
 #pragma unroll
     for (int jj = 0; jj < 256 / GW; ++jj) {
       const int g = sb * (256 / GW) + jj;
@@ -394,7 +394,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
   asm volatile("" : "+v"(rlb));
   const int n = tr * TN + f * 32 + l;
-  const uint8_t* srow = M.side + ((size_t)n * (K / 256) + (size_t)tc * (TW / 256)) * SB;
+  const uint8_t* srow = M.side + side_record(n, tc * (TW / 256), KT, TW / 256) * SB;  // + sb * 64 records
   typedef __attribute__((address_space(4))) const uint32_t KU32;
   KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);  // uniform: this tile column's x pairs (m = 1)
   constexpr int NSB = TW / 256;      // super-blocks per tile column
@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 #pragma unroll 1
   for (int sb = 0; sb < NSB; ++sb) {
     uint32_t sw[5];
-    side_load<KQ>(srow + sb * SB, sw);
+    side_load<KQ>(srow + sb * (TN * SB), sw);
     float dA, dB;
     uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K / IQ4_XS), consumed low byte first
     side_packed<KQ>(sw, scq, scq2, dA, dB);
@@ -668,7 +668,7 @@ __global__ void __launch_bounds__(256) k_gemm_codes(DevMat M, const uint8_t* __r
   float tot = 0.f;
   for (int b = 0; b < K / 256; ++b) {
     uint32_t sw[5];
-    side_load<KQ>(M.side + ((size_t)n * (K / 256) + b) * SB, sw);
+    side_load<KQ>(M.side + side_record(n, b, M.KT, M.symbits == 4 ? 2 : 1) * SB, sw);
     for (int jj = 0; jj < 256 / GW; ++jj) {
       float s, o;
       side_scale<KQ>(sw, jj, s, o);

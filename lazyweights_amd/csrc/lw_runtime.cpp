@@ -257,8 +257,14 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (t.kqt) {
     const Tensor& x = M.ts[t.side_idx];
     t.side_bytes = (size_t)x.N * x.K;
-    std::vector<uint8_t> sb(t.side_bytes);
-    if (!pread_all(M.fd, sb.data(), t.side_bytes, x.off)) return fail(t.name + ": side read error");
+    std::vector<uint8_t> raw(t.side_bytes), sb(t.side_bytes);
+    if (!pread_all(M.fd, raw.data(), t.side_bytes, x.off)) return fail(t.name + ": side read error");
+    // bundle order [N][K/256][SB] -> the kernels' tile-major record order (lw::side_record)
+    const int SB = lw::kq_sbytes(t.kqt), nb = (int)(t.K / 256), nsb = t.symbits == 4 ? 2 : 1;
+    for (int n = 0; n < (int)t.N; ++n)
+      for (int b = 0; b < nb; ++b)
+        memcpy(sb.data() + lw::side_record(n, b, dm.KT, nsb) * SB, raw.data() + ((size_t)n * nb + b) * SB, SB);
+    std::vector<uint8_t>().swap(raw);
     if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes) != hipSuccess) {
       (void)hipGetLastError();
       return fail(t.name + ": device allocation failed (side)");
