@@ -279,12 +279,10 @@ hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipS
   }
 }
 
-// ring slot write of chunk k (2 rows; this lane's 8 bytes of row 2k + slot_lane), with the mirror of slot 0
+// ring slot write of chunk k (2 rows; this lane's 8 bytes of row 2k + slot_lane)
 template <int RS>
 __device__ __forceinline__ void ring_put(uint2* ring2, int k, int slot_lane, int col2, uint2 v) {
-  const int slot = (2 * k + slot_lane) & (RS - 1);
-  ring2[slot * 16 + col2] = v;
-  if (slot == 0) ring2[RS * 16 + col2] = v;
+  ring2[((2 * k + slot_lane) & (RS - 1)) * 16 + col2] = v;
 }
 
 // group start: write the chunks loaded two groups ago, then issue this group's loads (counts: 2 bits per group)
@@ -301,11 +299,13 @@ __device__ __forceinline__ void ring_stage(uint2* ring2, const uint2* src, int s
 
 // ── ring-staged fused kernel, grouped over the matrices of a layer ────────────────────────────────────────
 // As k_fused, but a wave does not stage its whole tile: each front (lanes 0-31 from bit GUARD, lanes 32-63 from
-// their `mid` offsets) keeps a ring of RS word rows (+ one mirror row for the window's read-ahead) and streams 2-row
-// chunks (one 8-byte load per lane) from HBM on the tile's load-time schedule (Layout::sched): chunks loaded at
-// group g are written to the ring at the start of group g + 2, so their latency hides behind two groups of decode.
-// Windows are 64 bits (rows r, r + 1) and yield two symbols each: the first at the guard-aligned offset
-// (alignbit), the second by a 64-bit shift.
+// their `mid` offsets) keeps a ring of RS word rows and streams 2-row chunks (one 8-byte load per lane) from HBM on
+// the tile's load-time schedule (Layout::sched): chunks loaded at group g are written to the ring at the start of
+// group g + 2, so their latency hides behind two groups of decode.
+// Each lane holds its window rows r, r + 1 in registers (A, B) and the next row r + 2 (C), re-read from its ring
+// column after every pair of symbols; when a pair crosses into row r + 1 the window slides (A = B, B = C). A pair
+// decodes from one 32-bit window w1 = alignbit(B, A, pos): the first symbol at the guard-aligned offset, the second
+// from w1 >> len1. So the only LDS reads on a pair's dependency chain are its two table lookups.
 //
 // The decode table holds 4-byte entries (8 KB, half the LDS bank traffic of {value, length} pairs): bits 0-7 =
 // code length; 4-bit formats: bytes 2 and 3 = the pair's two grid bytes (Q4_K: q; IQ4_XS: kv[q] + 128), which one
@@ -329,14 +329,15 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
-  constexpr int RING_WORDS = (RS + 1) * 32;
+  static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
+  constexpr int RING_WORDS = RS * 32, RS_BITS = RS == 16 ? 4 : 5;
   constexpr int NTHR = WPB * 64;
   constexpr bool XS_SGPR = MT == 1;  // m = 1: activations straight from the scalar cache
   __shared__ uint32_t lut4[LUTN];
   extern __shared__ __align__(16) uint32_t smem[];
   uint32_t* xs = smem;                                          // [NPAIR][MT] fp16 pairs
   float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);        // [NG][MT] sub-block sums of x
-  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);  // WPB x 2 fronts x (RS + 1) rows
+  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);  // WPB x 2 fronts x RS rows
 
   // the block's matrix: a uniform index into the plan, read through the kernel-argument segment (scalar loads)
   int mi = 0;
@@ -389,10 +390,17 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   uint2 st00 = make_uint2(0, 0), st01 = st00, st10 = st00, st11 = st00;  // staged chunks by group parity
   int pend0 = 0, pend1 = 0;
 
-  uint32_t Q = (f ? (uint32_t)M.mid[(size_t)t * 32 + l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f;
-  // this lane's column of the ring as one opaque byte address, so a window address is (row offset) + base
+  // P = the lane's bit position (relative to the front's base row) + 64: bits 0-4 are the window offset and the
+  // row field (bits 5+) names row r + 2, the row C holds
+  uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
+  // this lane's column of the ring as one opaque byte address, so a row address is (slot * 128) + base
   uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
   asm volatile("" : "+v"(rlb));
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
+  uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
+  uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & (RS - 1)) << 7));
+  uint32_t C = *(LdsU32*)(rlb + (slot << 7));
   const int n = tr * TN + f * 32 + l;
   const uint8_t* srow = M.side + side_record(n, tc * (TW / 256), KT, TW / 256) * SB;  // + sb * 64 records
   typedef __attribute__((address_space(4))) const uint32_t KU32;
@@ -435,15 +443,19 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
         else ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend1, st10, st11);
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          typedef __attribute__((address_space(3))) const uint32_t LdsU32;
-          LdsU32* a = (LdsU32*)(rlb + ((Q & ((RS - 1) << 5)) << 2));
-          const uint32_t lo = a[0], hi = a[32];
-          const uint32_t w1 = __builtin_amdgcn_alignbit(hi, lo, Q);
+          const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
           const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w1 & 0x1FFCu));
-          const uint32_t d2 = (Q & 31u) + e1;  // the 64-bit shift reads bits 0-5: offset + length
-          const uint32_t w2 = (uint32_t)((((uint64_t)hi << 32) | lo) >> (d2 & 63u));
+          // the second symbol lies within w1: it starts len1 <= 11 bits further and its table index ends by bit 24
+          const uint32_t w2 = w1 >> (e1 & 31u);
           const uint32_t e2 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w2 & 0x1FFCu));
-          Q = Q + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
+          P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
+          // a pair advances at most 22 bits: the window slides by at most one row
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
+          const bool slide = nslot != slot;
+          A = slide ? B : A;
+          B = slide ? C : B;
+          slot = nslot;
+          C = *(LdsU32*)(rlb + (nslot << 7));
           if (SYMB == 4) {
             const uint32_t v1 = __builtin_amdgcn_perm(e1, e1, 0x0C030C02u), v2 = __builtin_amdgcn_perm(e2, e2, 0x0C030C02u);
             const int c = 16 * g + 2 * p;
@@ -498,7 +510,7 @@ int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 16 : 8; }
 // dynamic LDS of the ring kernel (the 8 KB decode table is static)
 static size_t ring_smem(int symbits, int kqt, int MT, int WPB, int RS) {
   const int TW = symbits == 4 ? 2 * TK : TK, GW = kq_gw(kqt);
-  return (size_t)(TW / 2) * MT * 4 + (size_t)(TW / GW) * MT * 4 + (size_t)WPB * 2 * (RS + 1) * 128;
+  return (size_t)(TW / 2) * MT * 4 + (size_t)(TW / GW) * MT * 4 + (size_t)WPB * 2 * RS * 128;
 }
 
 template <int KQ, int MT, int RS>

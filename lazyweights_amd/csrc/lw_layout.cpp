@@ -57,13 +57,15 @@ inline uint32_t bits_at(const uint32_t* pay, uint64_t pw, uint64_t b) {
 
 // Ring staging schedule of one tile (see the ring kernel): front f stages CHUNK_ROWS-row chunks of its rows, relative
 // to its base row; chunks loaded at group g reach LDS at the start of group g + 2. mn / mx = lowest / highest
-// relative row that any lane's windows touch in each group. Loads are issued just in time for group g + 2 (at most
-// MAX_CHUNKS_PER_GROUP per group). Returns false if a ring of RS rows cannot hold the schedule.
-bool ring_schedule(const int mn[2][GROUPS], const int mx[2][GROUPS], int RS, uint64_t& counts, int init[2]) {
+// relative row that any lane reads from the ring in each group; r0 = lowest row of the windows read before group 0.
+// Loads are issued just in time for group g + 2 (at most MAX_CHUNKS_PER_GROUP per group). Returns false if a ring
+// of RS rows cannot hold the schedule.
+bool ring_schedule(const int mn[2][GROUPS], const int mx[2][GROUPS], const int r0[2], int RS, uint64_t& counts,
+                   int init[2]) {
   counts = 0;
   for (int f = 0; f < 2; ++f) {
     init[f] = (std::max(mx[f][0], mx[f][1]) + CHUNK_ROWS) / CHUNK_ROWS;
-    if (CHUNK_ROWS * init[f] > RS + mn[f][0] || init[f] > 255) return false;
+    if (CHUNK_ROWS * init[f] > RS + r0[f] || init[f] > 255) return false;
     int issued = init[f], written = init[f];
     int loads[GROUPS] = {0};
     for (int g = 0; g < GROUPS; ++g) {
@@ -106,26 +108,34 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
       if (bad) break;
       int base1 = 1 << 30;
       for (int l = 0; l < LANES; ++l) base1 = std::min<int>(base1, (int)(pos[(size_t)l * (LANE_SYMS + 1) + TK] >> 5));
-      int mn[2][GROUPS], mx[2][GROUPS];
-      for (int f = 0; f < 2; ++f)
+      // The kernel reads rows r, r + 1, r + 2 of the window at a front's first symbol (r = its row), then, after
+      // each pair of symbols, row r + 2 of the window at the next pair: in group g (pairs at s0, s0 + 2, ..,
+      // s0 + 14) that is rows row(s0 + 2) + 2 .. row(s0 + 16) + 2.
+      int mn[2][GROUPS], mx[2][GROUPS], r0[2];
+      for (int f = 0; f < 2; ++f) {
+        const int base = f ? base1 : 0;
+        r0[f] = 1 << 30;
+        for (int l = 0; l < LANES; ++l)
+          r0[f] = std::min<int>(r0[f], (int)(pos[(size_t)l * (LANE_SYMS + 1) + f * TK] >> 5) - base);
         for (int g = 0; g < GROUPS; ++g) {
-          const int base = f ? base1 : 0, s0 = f * TK + g * GROUP_SYMS, s1 = s0 + GROUP_SYMS - 2;
+          const int s0 = f * TK + g * GROUP_SYMS;
           int lo = 1 << 30, hi = 0;
           for (int l = 0; l < LANES; ++l) {
             const uint32_t* p = pos.data() + (size_t)l * (LANE_SYMS + 1);
-            lo = std::min<int>(lo, (int)(p[s0] >> 5) - base);
-            hi = std::max<int>(hi, (int)(p[s1] >> 5) + 1 - base);
+            lo = std::min<int>(lo, (int)(p[s0 + 2] >> 5) + 2 - base);
+            hi = std::max<int>(hi, (int)(p[s0 + GROUP_SYMS] >> 5) + 2 - base);
           }
           mn[f][g] = lo;
           mx[f][g] = hi;
         }
+      }
       int init[2] = {0, 0};
       uint64_t counts = 0;
       uint8_t ok = 0;
       for (int k = 1; k >= 0; --k) {  // a schedule valid for 16 rows is valid for 32 (same loads, looser checks)
         uint64_t c;
         int in[2];
-        if (base1 < 256 && ring_schedule(mn, mx, k ? 32 : 16, c, in)) {
+        if (base1 < 256 && ring_schedule(mn, mx, r0, k ? 32 : 16, c, in)) {
           ok |= (uint8_t)(1 << k);
           counts = c;
           init[0] = in[0];

@@ -153,56 +153,62 @@ def test_layout_from_reference_export(lib, compact):
 
 
 def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
-    """The ring kernel's staging and 2-symbol windows (k_fused_ring), per tile and front."""
+    """The ring kernel's staging and register window (k_fused_ring), per tile and front: rows r, r + 1 of the
+    window in registers A, B, row r + 2 re-read from the ring (C) after every pair, one 32-bit window per pair."""
     KT = KS // 256
     lut = lut.astype(np.uint64)
     out = np.zeros((N, KS), np.uint8)
     l = np.arange(32)
+    M32 = np.uint64(0xFFFFFFFF)
     for t in range(len(tbase)):
         tr, tc = divmod(t, KT)
         counts, meta = int(sched[2 * t]), int(sched[2 * t + 1])
         base1, init = meta & 255, [(meta >> 8) & 255, (meta >> 16) & 255]
         for f in range(2):
             base = base1 if f else 0
-            W = lambda r: words[int(tbase[t]) + 32 * (base + r) + l]   # noqa: E731
-            ring = np.zeros((RS + 1, 32), np.uint32)
+            W = lambda r: words[int(tbase[t]) + 32 * (base + r) + l].astype(np.uint64)   # noqa: E731
+            ring = np.zeros((RS, 32), np.uint64)
 
             def put(k):
                 for i in range(2):
-                    r = 2 * k + i
-                    ring[r & (RS - 1)] = W(r)
-                    if r & (RS - 1) == 0:
-                        ring[RS] = W(r)
+                    ring[(2 * k + i) & (RS - 1)] = W(2 * k + i)
             for k in range(init[f]):
                 put(k)
-            issued = written = init[f]
+            issued = init[f]
             pend = [[], []]
-            Q = ((mid[t].astype(np.int64) - GUARD) if f else np.zeros(32, np.int64)) - 32 * base
-            assert np.all(Q >= 0)
+            P = ((mid[t].astype(np.int64) - GUARD) if f else np.zeros(32, np.int64)) - 32 * base + 64
+            assert np.all(P >= 64)
+            slot = (P >> 5) & (RS - 1)
+            A, B, C = ring[(slot - 2) & (RS - 1), l], ring[(slot - 1) & (RS - 1), l], ring[slot, l]
+            for k, v in ((2, A), (1, B), (0, C)):
+                assert np.array_equal(v, W((P >> 5) - k)), (t, f, "initial window")
             col = 0
             for g in range(16):
                 h = g & 1
                 for k in pend[h]:
                     put(k)
-                    written += 1
                 pend[h] = []
                 for _ in range((counts >> (32 * f + 2 * g)) & 3):
                     pend[h].append(issued)
                     issued += 1
                 for p in range(8):
-                    r = Q >> 5
-                    lo = ring[r & (RS - 1), l].astype(np.uint64)
-                    hi = ring[(r & (RS - 1)) + 1, l].astype(np.uint64)
-                    assert np.array_equal(lo, W(r)) and np.array_equal(hi, W(r + 1)), (t, f, g, p)
-                    win = (hi << np.uint64(32)) | lo
-                    e1 = lut[((win >> (Q & 31).astype(np.uint64)) >> np.uint64(GUARD)) & np.uint64(2047)]
-                    d2 = (Q & 31) + (e1 >> np.uint64(8)).astype(np.int64)
-                    e2 = lut[((win >> d2.astype(np.uint64)) >> np.uint64(GUARD)) & np.uint64(2047)]
+                    w1 = (((B << np.uint64(32)) | A) >> (P & 31).astype(np.uint64)) & M32
+                    e1 = lut[(w1 >> np.uint64(GUARD)) & np.uint64(2047)]
+                    w2 = w1 >> (e1 >> np.uint64(8))                  # second symbol from the same 32 bits
+                    e2 = lut[(w2 >> np.uint64(GUARD)) & np.uint64(2047)]
                     rows_out = tr * 64 + 32 * f + l
                     out[rows_out, tc * 256 + col] = (e1 & np.uint64(255)).astype(np.uint8)
                     out[rows_out, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
                     col += 2
-                    Q = Q + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+                    P = P + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+                    nslot = (P >> 5) & (RS - 1)
+                    slide = nslot != slot
+                    A, B = np.where(slide, B, A), np.where(slide, C, B)
+                    slot = nslot
+                    C = ring[slot, l]
+                    assert np.array_equal(A, W((P >> 5) - 2)) and np.array_equal(B, W((P >> 5) - 1)), (t, f, g, p)
+                    last = g == 15 and p == 7          # the final re-read is never used
+                    assert last or np.array_equal(C, W(P >> 5)), (t, f, g, p)
     return out
 
 
