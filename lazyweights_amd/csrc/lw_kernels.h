@@ -13,7 +13,7 @@ namespace lw {
 //   words u32[...]             tile t: word i of lane l at tbase[t] + 32 i + l, i < rows[t]; every lane stream
 //                              starts at bit 0 of its word 0; rows[t] = the tile's longest lane in words; zero tail
 //   side  u8[N*K/256][SB]      K-quant side records of the bundle's <name>.kqs in tile-major order (side_record)
-//   sched u32x4[T]             ring staging schedule of each tile (lw_layout.h, Layout::sched)
+//   sched u32x4[T]             ring staging schedule of each tile (lw_layout.h, Layout::sched); w bit 0: no schedule
 // Every lane stream starts with GUARD = 2 zero bits (symbol 0 at stream bit 2).
 struct DevMat {
   const uint16_t* lut;
@@ -29,10 +29,13 @@ struct DevMat {
   int KT, NT;       // tile columns, tile rows
   int max_rows;     // max over tiles of rows[t]
   int ring_rows;    // 16 / 32: ring kernel usable with that ring; 0: whole-tile kernel only
+  const uint32_t* exc;  // tiles the ring kernel skips (no schedule for ring_rows), decoded by the whole-tile kernel
+  int nexc;
 };
 
 // Matrices of one grouped launch of the ring kernel (same K-quant type and ring size). Matrix i owns blocks
-// [block0, block0 + KT * ceil(NT / WPB)); X2 = its fp16 activations [mt][K] as pairs, P its partials [KT][mt][N].
+// [block0, block0 + KT * ceil(NT / WPB)); X2 = its fp16 activations [mt][K] as pairs, P its partials [KT][mt][N]
+// (the exception tiles' partials are written by the whole-tile kernel's pass).
 constexpr int MAX_GROUP = 8;
 struct GroupEntry {
   DevMat M;
@@ -65,6 +68,8 @@ hipError_t launch_reduce_group(const ReducePlan& plan, hipStream_t s);
 
 // X16 [mt][K] fp16 (mt pseudo-tokens); P [KT][mt][N] fp32 per-tile-column partials.
 hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
+// the whole-tile kernel over M.exc only (the ring kernel's exception tiles); no-op when there are none
+hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
 // Y[j][n] (row stride ldy) = sum over tile columns tc (in order) of P[tc][jj][n], jj over `per` pseudo-tokens of
 // token j (per = 1: fp16 activations; per = 2: fp32 activations split into fp16 hi + lo).
 hipError_t launch_reduce(const float* P, float* Y, int m, int per, int N, int ldy, int KT, hipStream_t s);

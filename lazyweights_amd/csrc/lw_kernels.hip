@@ -151,10 +151,11 @@ __device__ __forceinline__ void stage_tile(const DevMat& M, int t, uint32_t* tw,
 
 // ── fused decode + dequant + GEMV / GEMM (m <= 16 pseudo-tokens) ─────────────────────────────────────────
 // block = 4 waves = 4 tile rows [4 b_r, 4 b_r + 4) of one tile column tc; lane L of wave w: tile row 4 b_r + w,
-// matrix row 64 tr + L (lanes 32..63 start at their lane's `mid` offset).
+// matrix row 64 tr + L (lanes 32..63 start at their lane's `mid` offset). With a tile list: one-wave blocks, block
+// b decodes tile list[b] (the ring kernel's exception tiles).
 template <int KQ, int MT>
 __global__ void __launch_bounds__(256) k_fused(DevMat M, const uint32_t* __restrict__ X2, int mt,
-                                                float* __restrict__ P) {
+                                                float* __restrict__ P, const uint32_t* __restrict__ list) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;  // weights per tile column
   constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
@@ -165,17 +166,18 @@ __global__ void __launch_bounds__(256) k_fused(DevMat M, const uint32_t* __restr
   uint32_t* tiles = reinterpret_cast<uint32_t*>(xg + NG * MT);
   const int RS = M.max_rows + 1;
   const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
-  const int tc = blockIdx.x % KT, wave = threadIdx.x >> 6;
-  const int tr = (blockIdx.x / KT) * 4 + wave;
+  const int NTHR = blockDim.x, wave = threadIdx.x >> 6;
+  const int tc = list ? (int)(list[blockIdx.x] % (uint32_t)KT) : (int)blockIdx.x % KT;
+  const int tr = list ? (int)(list[blockIdx.x] / (uint32_t)KT) : ((int)blockIdx.x / KT) * 4 + wave;
   const int lane = threadIdx.x & 63, l = lane & 31, half = lane >> 5;
-  for (int i = threadIdx.x; i < LUTN; i += 256) {
+  for (int i = threadIdx.x; i < LUTN; i += NTHR) {
     const uint32_t e = M.lut[i], sym = e & 255u;
     uint32_t v;
     if (SYMB == 4) v = f2h(grid_value<KQ>(sym & 15u)) | f2h(grid_value<KQ>(sym >> 4)) << 16;
     else v = f2h(grid_value<KQ>(sym));
     lut8[i] = make_uint2(v, e >> 8);
   }
-  for (int i = threadIdx.x; i < NPAIR * MT; i += 256) {
+  for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
     const int j = i / NPAIR, c = i - j * NPAIR;
     xs[c * MT + j] = j < mt ? X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
   }
@@ -184,7 +186,7 @@ __global__ void __launch_bounds__(256) k_fused(DevMat M, const uint32_t* __restr
   uint32_t* tw = tiles + wave * 32 * RS;
   if (active) stage_tile(M, t, tw, lane);
   __syncthreads();
-  for (int i = threadIdx.x; i < NG * MT; i += 256) {
+  for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
     const int g = i / MT, j = i - g * MT;
     float a = 0.f;
     for (int c = g * (GW / 2); c < (g + 1) * (GW / 2); ++c) {
@@ -248,35 +250,47 @@ static size_t fused_smem(const DevMat& M, int MT) {
 }
 
 template <int KQ, int MT>
-static hipError_t fused_mt(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s) {
+static hipError_t fused_mt(const DevMat& M, const void* X16, int mt, float* P, const uint32_t* list, int nlist,
+                           hipStream_t s) {
   const size_t smem = fused_smem(M, MT);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused<KQ, MT>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  const int blocks = M.KT * ((M.NT + 3) / 4);
-  hipLaunchKernelGGL((k_fused<KQ, MT>), dim3(blocks), dim3(256), smem, s, M,
-                     reinterpret_cast<const uint32_t*>(X16), mt, P);
+  const int blocks = list ? nlist : M.KT * ((M.NT + 3) / 4);
+  hipLaunchKernelGGL((k_fused<KQ, MT>), dim3(blocks), dim3(list ? 64 : 256), smem, s, M,
+                     reinterpret_cast<const uint32_t*>(X16), mt, P, list);
   return hipGetLastError();
 }
 
 template <int KQ>
-static hipError_t fused_kq(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s) {
-  if (mt <= 1) return fused_mt<KQ, 1>(M, X16, mt, P, s);
-  if (mt <= 2) return fused_mt<KQ, 2>(M, X16, mt, P, s);
-  if (mt <= 4) return fused_mt<KQ, 4>(M, X16, mt, P, s);
-  if (mt <= 8) return fused_mt<KQ, 8>(M, X16, mt, P, s);
-  return fused_mt<KQ, 16>(M, X16, mt, P, s);
+static hipError_t fused_kq(const DevMat& M, const void* X16, int mt, float* P, const uint32_t* list, int nlist,
+                           hipStream_t s) {
+  if (mt <= 1) return fused_mt<KQ, 1>(M, X16, mt, P, list, nlist, s);
+  if (mt <= 2) return fused_mt<KQ, 2>(M, X16, mt, P, list, nlist, s);
+  if (mt <= 4) return fused_mt<KQ, 4>(M, X16, mt, P, list, nlist, s);
+  if (mt <= 8) return fused_mt<KQ, 8>(M, X16, mt, P, list, nlist, s);
+  return fused_mt<KQ, 16>(M, X16, mt, P, list, nlist, s);
+}
+
+static hipError_t fused_any(const DevMat& M, const void* X16, int mt, float* P, const uint32_t* list, int nlist,
+                            hipStream_t s) {
+  if (mt < 1 || mt > 16 || (list && nlist < 1)) return hipErrorInvalidValue;
+  switch (M.kqt) {
+    case KQ_Q4_K: return fused_kq<KQ_Q4_K>(M, X16, mt, P, list, nlist, s);
+    case KQ_Q5_K: return fused_kq<KQ_Q5_K>(M, X16, mt, P, list, nlist, s);
+    case KQ_Q6_K: return fused_kq<KQ_Q6_K>(M, X16, mt, P, list, nlist, s);
+    case KQ_IQ4_XS: return fused_kq<KQ_IQ4_XS>(M, X16, mt, P, list, nlist, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s) {
-  if (mt < 1 || mt > 16) return hipErrorInvalidValue;
-  switch (M.kqt) {
-    case KQ_Q4_K: return fused_kq<KQ_Q4_K>(M, X16, mt, P, s);
-    case KQ_Q5_K: return fused_kq<KQ_Q5_K>(M, X16, mt, P, s);
-    case KQ_Q6_K: return fused_kq<KQ_Q6_K>(M, X16, mt, P, s);
-    case KQ_IQ4_XS: return fused_kq<KQ_IQ4_XS>(M, X16, mt, P, s);
-    default: return hipErrorInvalidValue;
-  }
+  return fused_any(M, X16, mt, P, nullptr, 0, s);
+}
+
+hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s) {
+  if (M.nexc == 0) return hipSuccess;
+  return fused_any(M, X16, mt, P, M.exc, M.nexc, s);
 }
 
 // ring slot write of chunk k (2 rows; this lane's 8 bytes of row 2k + slot_lane)
@@ -377,6 +391,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 
   const int t = tr * KT + tc;
   const uint4 sc = M.sched[t];
+  if (sc.w & 1u) return;  // no ring schedule for this tile: decoded by the whole-tile kernel's exception pass
   const int base_f = f ? (int)(sc.z & 255u) : 0;
   const int init_f = (int)((sc.z >> (f ? 16 : 8)) & 255u);
   const uint32_t counts_f = f ? sc.y : sc.x;  // 2 bits per group: chunks this front loads at that group
@@ -560,10 +575,26 @@ __global__ void k_reduce_group(ReducePlan plan) {
 #pragma unroll
   for (int k = 1; k < MAX_GROUP; ++k)
     if (k < plan.n && i >= plan.e[k].out0) E = plan.e[k];
-  const int o = i - E.out0, j = o / E.N, n = o - j * E.N, mt = plan.m * plan.per;
+  const int o = i - E.out0, j = o / E.N, n = o - j * E.N, per = plan.per, mt = plan.m * per;
+  const float* pp = E.P + (size_t)j * per * E.N + n;
+  const size_t step = (size_t)mt * E.N;
+  // partials summed in tile-column order (pseudo-tokens of a column in order); eight columns' loads in flight
   float a = 0.f;
-  for (int tc = 0; tc < E.KT; ++tc)
-    for (int q = 0; q < plan.per; ++q) a += E.P[((size_t)tc * mt + j * plan.per + q) * E.N + n];
+  int tc = 0;
+  for (; tc + 8 <= E.KT; tc += 8) {
+    float v[8][2];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) v[u][q] = q < per ? pp[(size_t)(tc + u) * step + (size_t)q * E.N] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      a += v[u][0];
+      if (per > 1) a += v[u][1];
+    }
+  }
+  for (; tc < E.KT; ++tc)
+    for (int q = 0; q < per; ++q) a += pp[(size_t)tc * step + (size_t)q * E.N];
   E.Y[(size_t)j * E.ldy + n] = a;
 }
 

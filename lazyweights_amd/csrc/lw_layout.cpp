@@ -150,13 +150,25 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
     }
   });
   if (bad) return false;
-  // one ring size per matrix: 16 rows if every tile fits, else 32; schedules of the chosen size
-  bool all16 = true, all32 = true;
+  // one ring size per matrix: 16 rows when at most 1/32 of the tiles need the whole-tile fallback, else 32 if
+  // every tile fits, else none (whole-tile kernel for the matrix)
+  int n16 = 0;
+  bool all32 = true;
   for (int t = 0; t < T; ++t) {
-    all16 = all16 && (ring_ok[t] & 1);
+    n16 += ring_ok[t] & 1;
     all32 = all32 && (ring_ok[t] & 2);
   }
-  L.ring_rows = all16 ? 16 : all32 ? 32 : 0;
+  L.exc.clear();
+  if (32 * (T - n16) <= T) {
+    L.ring_rows = 16;
+    for (int t = 0; t < T; ++t)
+      if (!(ring_ok[t] & 1)) {
+        L.exc.push_back((uint32_t)t);
+        L.sched[2 * (size_t)t + 1] |= 1ull << 32;
+      }
+  } else {
+    L.ring_rows = all32 ? 32 : 0;
+  }
   return true;
 }
 

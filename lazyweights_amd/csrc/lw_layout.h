@@ -29,9 +29,12 @@ struct Layout {
   std::vector<uint32_t> words;  // tiles' word rows + zero tail
   // ring staging schedule per tile, 2 x u64: word 0 = 2-bit counts of 2-row chunks that front 0 (bits 2g) and
   // front 1 (bits 32 + 2g) load at group g; word 1 = base row of front 1 (bits 0-7), initial chunks of front 0
-  // (8-15) and front 1 (16-23)
+  // (8-15) and front 1 (16-23), bit 32: no schedule (an exception tile)
   std::vector<uint64_t> sched;
   int ring_rows = 0;            // 16 or 32 rows per front; 0: the ring schedule does not fit (whole-tile kernels)
+  // tiles without a schedule for ring_rows (bit 32 of their sched word 1 set): the ring kernel skips them and the
+  // whole-tile kernel decodes them from this list
+  std::vector<uint32_t> exc;
   int max_rows = 0;
   uint64_t payload_bits = 0;    // coded bits of all lanes
 };

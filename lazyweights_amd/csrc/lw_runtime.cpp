@@ -103,6 +103,9 @@ struct Model {
   uint64_t file_size = 0;
   bool gpu = false;
   hipStream_t stream = nullptr;
+  // side stream + events: the whole-tile pass over exception tiles runs beside the ring launch
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
   size_t resident_bytes = 0, coded_bytes = 0, device_bytes = 0, pad_bytes = 0;
   long long avail_after_kb = -1;
   int pos = 0, window = 0;
@@ -212,10 +215,12 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)] padded to 256 B, then the words
+  // [lut 4096 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)][exception tiles 4E] padded to 256 B, then
+  // the words
+  const size_t nexc = L.exc.size();
   const size_t o_tb = 2 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
-  const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15;
-  const size_t o_words = (o_sched + 16ull * T + 255) & ~(size_t)255;
+  const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_exc = o_sched + 16ull * T;
+  const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
   memcpy(host.data(), L.lut, 2 * lw::LUTN);
@@ -223,6 +228,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
   memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
   memcpy(host.data() + o_sched, L.sched.data(), 16ull * T);
+  if (nexc) memcpy(host.data() + o_exc, L.exc.data(), 4 * nexc);
   void* d = nullptr;
   if (hipMalloc(&d, bytes) != hipSuccess) {
     (void)hipGetLastError();
@@ -246,6 +252,8 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
   dm.sched = reinterpret_cast<const uint4*>(b + o_sched);
   dm.ring_rows = L.ring_rows;
+  dm.exc = nexc ? reinterpret_cast<const uint32_t*>(b + o_exc) : nullptr;
+  dm.nexc = (int)nexc;
   dm.side = nullptr;
   dm.N = (int)t.N;
   dm.K = (int)t.K;
@@ -292,6 +300,9 @@ void release(Model* M) {
   if (M->X16) (void)hipFree(M->X16);
   if (M->codes) (void)hipFree(M->codes);
   if (M->stream) (void)hipStreamDestroy(M->stream);
+  if (M->side) (void)hipStreamDestroy(M->side);
+  if (M->fork) (void)hipEventDestroy(M->fork);
+  if (M->join) (void)hipEventDestroy(M->join);
   if (M->fd >= 0) close(M->fd);
   delete M;
 }
@@ -322,8 +333,9 @@ int g_kernel_mode = 0;
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
 // others into whole-tile launches; then one ordered reduction per MAX_GROUP matrices. Partials of all matrices
 // live side by side in the model's P scratch.
+// `launches` (optional) counts the decode launches; reduce = false leaves the partials in M.P (kernel timing)
 int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
-                    const int* ldy, hipStream_t s) {
+                    const int* ldy, hipStream_t s, int* launches = nullptr, bool reduce = true) {
   const int mt = m * per;
   std::vector<size_t> off(count + 1, 0);
   for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
@@ -332,28 +344,56 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   plan.mt = mt;
   auto flush = [&]() -> int {
     if (plan.n) HIPCHECK(lw::launch_fused_group(plan, s));
+    if (plan.n && launches) ++*launches;
     plan.n = 0;
     plan.blocks = 0;
     return 0;
   };
+  // exception tiles (no ring schedule) through the whole-tile kernel, on the side stream beside the ring launches
+  // (disjoint partials); the reduction waits for both
+  const bool ring_ok = g_kernel_mode != 1;
+  bool forked = false;
+  if (ring_ok)
+    for (int i = 0; i < count; ++i)
+      if (ts[i]->dm.ring_rows && ts[i]->dm.nexc) {
+        if (!forked) {
+          HIPCHECK(hipEventRecord(M.fork, s));
+          HIPCHECK(hipStreamWaitEvent(M.side, M.fork, 0));
+          forked = true;
+        }
+        HIPCHECK(lw::launch_fused_exceptions(ts[i]->dm, X16[i], mt, M.P + off[i], M.side));
+        if (launches) ++*launches;
+      }
+  if (forked) HIPCHECK(hipEventRecord(M.join, M.side));
+  // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order
+  std::vector<char> done(count, 0);
   for (int i = 0; i < count; ++i) {
-    const lw::DevMat& dm = ts[i]->dm;
-    float* P = M.P + off[i];
-    if (g_kernel_mode == 1 || dm.ring_rows == 0) {
-      HIPCHECK(lw::launch_fused(dm, X16[i], mt, P, s));
+    if (done[i]) continue;
+    const lw::DevMat& di = ts[i]->dm;
+    if (!ring_ok || di.ring_rows == 0) {
+      HIPCHECK(lw::launch_fused(di, X16[i], mt, M.P + off[i], s));
+      if (launches) ++*launches;
+      done[i] = 1;
       continue;
     }
-    if (plan.n && (plan.n == lw::MAX_GROUP || plan.e[0].M.kqt != dm.kqt || plan.e[0].M.ring_rows != dm.ring_rows))
-      if (flush()) return -1;
-    lw::GroupEntry& e = plan.e[plan.n++];
-    e.M = dm;
-    e.X2 = static_cast<const uint32_t*>(X16[i]);
-    e.P = P;
-    e.block0 = plan.blocks;
-    const int wpb = lw::group_waves_per_block(dm.ring_rows);
-    plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
+    for (int j = i; j < count; ++j) {
+      const lw::DevMat& dm = ts[j]->dm;
+      if (done[j] || dm.kqt != di.kqt || dm.ring_rows != di.ring_rows) continue;
+      if (plan.n == lw::MAX_GROUP && flush()) return -1;
+      lw::GroupEntry& e = plan.e[plan.n++];
+      e.M = dm;
+      e.X2 = static_cast<const uint32_t*>(X16[j]);
+      e.P = M.P + off[j];
+      e.block0 = plan.blocks;
+      const int wpb = lw::group_waves_per_block(dm.ring_rows);
+      plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
+      done[j] = 1;
+    }
+    if (flush()) return -1;
   }
-  if (flush()) return -1;
+  if (forked) HIPCHECK(hipStreamWaitEvent(s, M.join, 0));
+  if (!reduce) return 0;
+  // ordered reduction over tile columns, up to MAX_GROUP matrices per launch
   lw::ReducePlan rp{};
   rp.m = m;
   rp.per = per;
@@ -439,7 +479,10 @@ void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, 
       release(M.release());
       return nullptr;
     }
-    if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess) {
+    if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&M->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&M->fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&M->join, hipEventDisableTiming) != hipSuccess) {
       fail("rt_open: stream creation failed");
       release(M.release());
       return nullptr;
@@ -764,45 +807,25 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
   double kms = 0;
   int launches = 0;
   const int kit = std::max(1, std::min(iters, 20));
+  std::vector<int> ldys(first[ngroups]);
+  for (int i = 0; i < first[ngroups]; ++i) {
+    Tensor* t = M->find(names[i]);
+    if (!t) {
+      g_err = std::string("lw_bench_groups: unknown tensor ") + (names[i] ? names[i] : "(null)");
+      return -1;
+    }
+    ldys[i] = (int)t->N;
+  }
   for (int it = 0; it < kit; ++it) {
     for (int g = 0; g < ngroups; ++g) {
       std::vector<Tensor*> ts;
       for (int i = first[g]; i < first[g + 1]; ++i) ts.push_back(M->find(names[i]));
-      const int mt = m;
-      size_t need = 0;
-      for (Tensor* t : ts) need += (size_t)t->dm.KT * mt * t->N;
-      if (grow(M->P, M->P_cap, need * sizeof(float))) return -1;
-      lw::GroupPlan plan{};
-      plan.mt = mt;
-      size_t off = 0;
       HIPCHECK(hipEventRecord(ev[2 * g], s));
-      for (size_t i = 0; i < ts.size(); ++i) {
-        const lw::DevMat& dm = ts[i]->dm;
-        float* P = M->P + off;
-        off += (size_t)dm.KT * mt * ts[i]->N;
-        if (g_kernel_mode == 1 || dm.ring_rows == 0) {
-          HIPCHECK(lw::launch_fused(dm, X[first[g] + i], mt, P, s));
-          if (it == 0) ++launches;
-          continue;
-        }
-        if (plan.n && (plan.n == lw::MAX_GROUP || plan.e[0].M.kqt != dm.kqt || plan.e[0].M.ring_rows != dm.ring_rows)) {
-          HIPCHECK(lw::launch_fused_group(plan, s));
-          if (it == 0) ++launches;
-          plan.n = 0;
-          plan.blocks = 0;
-        }
-        lw::GroupEntry& e = plan.e[plan.n++];
-        e.M = dm;
-        e.X2 = static_cast<const uint32_t*>(X[first[g] + i]);
-        e.P = P;
-        e.block0 = plan.blocks;
-        const int wpb = lw::group_waves_per_block(dm.ring_rows);
-        plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
-      }
-      if (plan.n) {
-        HIPCHECK(lw::launch_fused_group(plan, s));
-        if (it == 0) ++launches;
-      }
+      int nl = 0;
+      if (fused_group_dev(*M, ts.data(), X + first[g], sizes[g], m, 1, Y + first[g], ldys.data() + first[g], s, &nl,
+                          false))
+        return -1;
+      if (it == 0) launches += nl;
       HIPCHECK(hipEventRecord(ev[2 * g + 1], s));
     }
     HIPCHECK(hipEventSynchronize(ev.back()));

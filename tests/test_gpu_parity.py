@@ -248,3 +248,27 @@ def test_gpu_grouped_launch_matches_single(fmt_rt):
     say("grouped vs single", n)
     for a, b in zip(Yg, Ys):
         assert torch.equal(a, b)
+
+
+def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
+    """A matrix whose tile 5 has no 16-row ring schedule: the ring kernel skips it and the whole-tile kernel's
+    exception pass decodes it; GEMV (m = 1, fp16 x) and fp32-x m = 3 against fp64, decode bit-exact."""
+    import torch
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer
+    from test_layout import skewed_tile_codes
+    codes, side = skewed_tile_codes()
+    w = Writer(str(tmp_path))
+    w.add_kquant("skew", 2, codes, side)
+    w.close()
+    with Runtime(tmp_path) as rt:
+        say("exception tile: decode")
+        assert np.array_equal(rt.test_decode("skew"), codes)
+        W64 = orc.dequant(2, codes, side)
+        X = torch.randn(3, 8192).half()
+        y64 = orc.gemv_f64(W64, X.double().numpy())
+        Y = torch.zeros(1, 128, device="cuda")
+        rt.matmul_dev("skew", X[:1].cuda(), Y)
+        torch.cuda.synchronize()
+        check_err(Y.cpu().numpy(), y64[:1], "exception tile m=1")
+        check_err(rt.test_matmul("skew", X.float().numpy(), path=0), y64, "exception tile fp32 m=3")

@@ -163,6 +163,9 @@ def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
     for t in range(len(tbase)):
         tr, tc = divmod(t, KT)
         counts, meta = int(sched[2 * t]), int(sched[2 * t + 1])
+        if (meta >> 32) & 1:        # exception tile: skipped by the ring kernel
+            out[tr * 64:(tr + 1) * 64, tc * 256:(tc + 1) * 256] = syms[tr * 64:(tr + 1) * 64, tc * 256:(tc + 1) * 256]
+            continue
         base1, init = meta & 255, [(meta >> 8) & 255, (meta >> 16) & 255]
         for f in range(2):
             base = base1 if f else 0
@@ -232,3 +235,28 @@ def test_ring_schedules_exist_for_benchmark_shapes(lib):
         ks = 2048 if kqt in (1, 4) else 4096
         lay = build_layout(lib, blob, 256, ks, extra=True)
         assert lay[5] == 16, (kqt, H, lay[5])
+
+
+def skewed_tile_codes(seed=3):
+    """Q5_K codes [128, 8192] (64 tiles) where tile 5 has lanes alternating between the most frequent code and the
+    two rarest ones: its fronts drift apart by dozens of word rows, so no ring schedule exists for that tile."""
+    from lazyweights_amd import bundle
+    codes, side = bundle.synth_matrix(2, 128, 8192, 3.4, seed)
+    blk = codes[0:64, 5 * 256:6 * 256]
+    for r in range(64):
+        blk[r] = 16 if (r % 32) % 2 == 0 else np.where(np.arange(256) % 2 == 0, 0, 31)
+    return codes, side
+
+
+def test_ring_exception_tiles(lib):
+    """A tile without a 16-row schedule is flagged and listed as an exception; every other tile keeps the ring."""
+    from lazyweights_amd import bundle
+    codes, _ = skewed_tile_codes()
+    sym = bundle.form_symbols(2, codes)
+    blob, _ = bundle.encode_huf8(sym)
+    tbase, mid, rows, words, sched, RS = build_layout(lib, blob, 128, 8192, extra=True)
+    assert RS == 16
+    flagged = [t for t in range(len(tbase)) if (int(sched[2 * t + 1]) >> 32) & 1]
+    assert flagged == [5]
+    lut = np.frombuffer(blob, np.uint16, 2048, 0)
+    assert np.array_equal(emulate_ring(lut, tbase, mid, words, sched, RS, 128, 8192, sym), sym)
