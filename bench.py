@@ -10,9 +10,12 @@ seven GEMVs launched back to back (grouped per layer). value = algorithmic coded
 the algorithmic bytes of a GEMV are blob + side tensor + 2 K (x) + 4 m N (y) (the reference's own size
 accounting; device-layout padding is not credited).
 
-roofline: the dominant kernel (k_fused) timed with HIP events around each launch on its stream; achieved = the same
-algorithmic bytes / mean launch duration, peak = 8 TB/s. cpu_baseline: the oracle's restatement of the reference CPU
-path (cpu_decode, kernels/llmrt.cu:2513-2541, then dequant + fp32 GEMV) on layer 0, timed on this host.
+roofline: the dominant kernel (k_fused_ring, one grouped launch per layer) timed with HIP events around each layer's
+launch on its stream; achieved = the layer's algorithmic bytes / mean launch duration, peak = 8 TB/s. traffic = HBM
+bytes per layer launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --profile`,
+each scaled by what the counter reads for the 256 MiB device copy that --profile also runs (null when rocprofv3 is
+unavailable or a pass fails). cpu_baseline: the oracle's restatement of the reference CPU path (cpu_decode,
+kernels/llmrt.cu:2513-2541, then dequant + fp32 GEMV) on layer 0, timed on this host.
 One JSON line on stdout.
 """
 import argparse
@@ -34,6 +37,64 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def counter_pass(counter, layers, tmp, timeout=240):
+    """One rocprofv3 --pmc pass over `bench.py --profile`: {kernel: [(grid, KiB), ...]} or None."""
+    import csv
+    import signal
+    import subprocess
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None
+    out = os.path.join(tmp, counter)
+    cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "t", "--", sys.executable,
+           os.path.abspath(__file__), "--profile", "--steps", "2", "--layers", str(layers)]
+    log("bench: counter pass %s" % counter)
+    p = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, start_new_session=True)
+    try:
+        p.wait(timeout=timeout)
+    except subprocess.TimeoutExpired:
+        os.killpg(p.pid, signal.SIGKILL)
+        p.wait()
+        log("bench: counter pass %s timed out" % counter)
+        return None
+    rows = {}
+    for root, _, files in os.walk(out):
+        for f in files:
+            if f.endswith("counter_collection.csv"):
+                with open(os.path.join(root, f)) as fh:
+                    for r in csv.DictReader(fh):
+                        if r["Counter_Name"] == counter:
+                            rows.setdefault(r["Kernel_Name"], []).append((int(r["Grid_Size"]),
+                                                                          float(r["Counter_Value"])))
+    return rows or None
+
+
+def measure_traffic(layers):
+    """HBM bytes per full-layer k_fused_ring launch: calibrated FETCH_SIZE + WRITE_SIZE (see the module docstring)."""
+    tmp = tempfile.mkdtemp(prefix="lw_pmc_")
+    try:
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            rows = counter_pass(counter, layers, tmp)
+            if not rows:
+                return None
+            ring = [v for k, vs in rows.items() if "k_fused_ring" in k for v in vs]
+            copy = [v for k, vs in rows.items() if "copyBuffer" in k for v in vs]
+            if not ring or not copy:
+                return None
+            grid = max(g for g, _ in ring)
+            vals = [v for g, v in ring if g == grid]
+            cal = max(copy)[1]                      # the 256 MiB copy: 262144 KiB read and written
+            factor = (256 << 10) / cal if cal > 0 else 0.0
+            res[counter] = (sum(vals) / len(vals), factor, grid)
+        f, w = res["FETCH_SIZE"], res["WRITE_SIZE"]
+        log("bench: traffic per layer launch (grid %d): FETCH %.0f KiB x %.3f, WRITE %.0f KiB x %.3f"
+            % (f[2], f[0], f[1], w[0], w[1]))
+        return (f[0] * f[1] + w[0] * w[1]) * 1024.0, f[1], w[1]
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -44,6 +105,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
@@ -128,10 +190,20 @@ def main():
         launches = int(out[2])
         kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
         achieved = kbytes / (kernel_ms_per_pass * 1e-3) / 1e9
-        log("bench: fused kernels %.3f ms per pass (%d launches, mean %.1f us), %.1f GB/s"
-            % (kernel_ms_per_pass, launches, kernel_ms_per_pass * 1e3 / launches, achieved))
+        layer_us = kernel_ms_per_pass * 1e3 / a.layers
+        log("bench: fused kernels %.3f ms per pass (%d launches for %d layers, %.1f us per layer), %.1f GB/s"
+            % (kernel_ms_per_pass, launches, a.layers, layer_us, achieved))
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
+
+        traffic = None
+        if not a.no_traffic:
+            t = measure_traffic(a.layers)
+            if t:
+                traffic = {"bytes_per_layer_launch": int(t[0]), "algorithmic_bytes_per_layer": int(kbytes / a.layers),
+                           "fetch_factor": round(t[1], 3), "write_factor": round(t[2], 3)}
+                log("bench: HBM traffic %.1f MB per layer launch vs %.1f MB algorithmic"
+                    % (t[0] / 1e6, kbytes / a.layers / 1e6))
 
         cpu = None
         if not a.no_cpu:
@@ -166,8 +238,10 @@ def main():
                        "layers": a.layers, "m": m, "coded_bytes_per_step": int(bytes_per_step),
                        "hbm_fraction": round(value / HBM_PEAK_GBS, 4)},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                         "kernel": "k_fused", "mean_launch_us": round(kernel_ms_per_pass * 1e3 / launches, 2)},
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic["bytes_per_layer_launch"] if traffic else None,
+                         "traffic_detail": traffic, "kernel": "k_fused_ring", "launch": "one grouped launch per layer",
+                         "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
         }

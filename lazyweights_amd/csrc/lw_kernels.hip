@@ -367,8 +367,9 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   const int mt = plan.mt;
   const int bl = (int)blockIdx.x - E.block0;
   const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
-  const int tc = bl % KT, wave = threadIdx.x >> 6;
-  const int tr = (bl / KT) * WPB + wave;
+  // wave-uniform indices are made explicit (scalar registers): the tile, its schedule and its base addresses
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tc = bl % KT, tr = (bl / KT) * WPB + wave;
   const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
 
   for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(M.lut[i]);
@@ -398,7 +399,8 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
   uint2* ring2 = reinterpret_cast<uint2*>(ring);
   // chunk k of this front = rows [2k, 2k + 2) after its base row; lane l carries row 2k + l / 16, words 2 (l % 16)..
-  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t] + 32u * base_f) + l;
+  // (a uniform tile base plus a 32-bit per-lane offset: chunk k at src[32 k])
+  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
   const int slot_lane = l >> 4, col2 = l & 15;
   for (int k = 0; k < init_f; ++k) ring_put<RS>(ring2, k, slot_lane, col2, src[32 * k]);
   int issued = init_f, written = init_f;
@@ -407,7 +409,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 
   // P = the lane's bit position (relative to the front's base row) + 64: bits 0-4 are the window offset and the
   // row field (bits 5+) names row r + 2, the row C holds
-  uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
+  uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
   // this lane's column of the ring as one opaque byte address, so a row address is (slot * 128) + base
   uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
   asm volatile("" : "+v"(rlb));
@@ -416,8 +418,8 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
   uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & (RS - 1)) << 7));
   uint32_t C = *(LdsU32*)(rlb + (slot << 7));
-  const int n = tr * TN + f * 32 + l;
-  const uint8_t* srow = M.side + side_record(n, tc * (TW / 256), KT, TW / 256) * SB;  // + sb * 64 records
+  // this tile's side records (uniform base) + the lane's record (super-block sb: + sb * 64 records)
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)((f * 32 + l) * SB);
   typedef __attribute__((address_space(4))) const uint32_t KU32;
   KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);  // uniform: this tile column's x pairs (m = 1)
   constexpr int NSB = TW / 256;      // super-blocks per tile column
@@ -517,7 +519,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   }
 #pragma unroll
   for (int j = 0; j < MT; ++j)
-    if (j < mt) E.P[((size_t)tc * mt + j) * N + n] = tot[j];
+    if (j < mt) (E.P + ((size_t)tc * mt + j) * N + (size_t)tr * TN)[(uint32_t)(f * 32 + l)] = tot[j];
 }
 
 int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 16 : 8; }
