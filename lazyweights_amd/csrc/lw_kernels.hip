@@ -293,23 +293,39 @@ hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, flo
   return fused_any(M, X16, mt, P, M.exc, M.nexc, s);
 }
 
-// ring slot write of chunk k (2 rows; this lane's 8 bytes of row 2k + slot_lane)
-template <int RS>
-__device__ __forceinline__ void ring_put(uint2* ring2, int k, int slot_lane, int col2, uint2 v) {
-  ring2[((2 * k + slot_lane) & (RS - 1)) * 16 + col2] = v;
-}
+// Ring staging of one front: chunk k = rows [2k, 2k + 2) after the front's base row; lane l carries row
+// 2k + l / 16, words 2 (l % 16) .. + 1 (`src` points at that lane's 8 bytes of chunk 0, `lane_slot` at its place in
+// ring slot 0). At the start of group g the chunks loaded at g - 2 are written and group g's loads are issued
+// (2-bit counts per group). Tiles whose two fronts share one schedule use the scalar form (wave-uniform counts,
+// branches and offsets); the others keep one schedule per front (per-lane counts).
+template <int RS, class I, class U>
+struct RingStager {
+  uint2* lane_slot;
+  const uint2* src;
+  U counts;
+  I written, issued, pend0, pend1;
+  uint2 s00, s01, s10, s11;  // chunks in flight, by group parity
 
-// group start: write the chunks loaded two groups ago, then issue this group's loads (counts: 2 bits per group)
-template <int RS>
-__device__ __forceinline__ void ring_stage(uint2* ring2, const uint2* src, int slot_lane, int col2, uint32_t counts,
-                                           int g, int& written, int& issued, int& pend, uint2& s0, uint2& s1) {
-  if (pend > 0) ring_put<RS>(ring2, written++, slot_lane, col2, s0);
-  if (pend > 1) ring_put<RS>(ring2, written++, slot_lane, col2, s1);
-  const int nload = (int)((counts >> (2 * g)) & 3u);
-  if (nload > 0) s0 = src[32 * issued++];
-  if (nload > 1) s1 = src[32 * issued++];
-  pend = nload;
-}
+  __device__ __forceinline__ void put(I k, uint2 v) { lane_slot[((2 * k) & (RS - 1)) * 16] = v; }
+  __device__ __forceinline__ void init(I n) {
+    for (I k = 0; k < n; ++k) put(k, src[32 * k]);
+    written = issued = n;
+    pend0 = pend1 = 0;
+    s00 = s01 = s10 = s11 = make_uint2(0, 0);
+  }
+  __device__ __forceinline__ void step(int g, I& pend, uint2& a, uint2& b) {
+    if (pend > 0) put(written++, a);
+    if (pend > 1) put(written++, b);
+    const I nload = (I)((counts >> (2 * g)) & 3u);
+    if (nload > 0) a = src[32 * issued++];
+    if (nload > 1) b = src[32 * issued++];
+    pend = nload;
+  }
+  __device__ __forceinline__ void stage(int g) {
+    if (g & 1) step(g, pend1, s10, s11);
+    else step(g, pend0, s00, s01);
+  }
+};
 
 // ── ring-staged fused kernel, grouped over the matrices of a layer ────────────────────────────────────────
 // As k_fused, but a wave does not stage its whole tile: each front (lanes 0-31 from bit GUARD, lanes 32-63 from
@@ -338,90 +354,21 @@ __device__ __forceinline__ uint32_t lut4_entry(uint32_t e) {
   return len | f2h(grid_value<KQ>(sym)) << 16;
 }
 
-template <int KQ, int MT, int WPB, int RS>
-__global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
+// One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring.
+template <int KQ, int MT, int RS, class Stager>
+__device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, const uint32_t* xs, const float* xg,
+                                          __attribute__((address_space(4))) const uint32_t* xcol,
+                                          const uint8_t* srow, uint32_t P, uint32_t rlb, int mt, int N, float* out) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
-  constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
-  static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
-  constexpr int RING_WORDS = RS * 32, RS_BITS = RS == 16 ? 4 : 5;
-  constexpr int NTHR = WPB * 64;
-  constexpr bool XS_SGPR = MT == 1;  // m = 1: activations straight from the scalar cache
-  __shared__ uint32_t lut4[LUTN];
-  extern __shared__ __align__(16) uint32_t smem[];
-  uint32_t* xs = smem;                                          // [NPAIR][MT] fp16 pairs
-  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);        // [NG][MT] sub-block sums of x
-  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);  // WPB x 2 fronts x RS rows
-
-  // the block's matrix: a uniform index into the plan, read through the kernel-argument segment (scalar loads)
-  int mi = 0;
-#pragma unroll
-  for (int i = 1; i < MAX_GROUP; ++i)
-    if (i < plan.n && (int)blockIdx.x >= plan.e[i].block0) mi = i;
-  typedef __attribute__((address_space(4))) const char KChar;
-  typedef __attribute__((address_space(4))) const GroupEntry KEntry;
-  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
-  KEntry* ep = (KEntry*)(kbase + offsetof(GroupPlan, e) + (size_t)mi * sizeof(GroupEntry));
-  const auto& E = *ep;
-  const auto& M = E.M;
-  const int mt = plan.mt;
-  const int bl = (int)blockIdx.x - E.block0;
-  const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
-  // wave-uniform indices are made explicit (scalar registers): the tile, its schedule and its base addresses
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tc = bl % KT, tr = (bl / KT) * WPB + wave;
-  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
-
-  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(M.lut[i]);
-  for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
-    const int j = i / NPAIR, c = i - j * NPAIR;
-    xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
-    const int g = i / MT, j = i - g * MT;
-    float a = 0.f;
-    for (int c = g * (GW / 2); c < (g + 1) * (GW / 2); ++c) {
-      const uint32_t v = xs[c * MT + j];
-      a += h2f(v) + h2f(v >> 16);
-    }
-    xg[g * MT + j] = a;
-  }
-  __syncthreads();
-  if (tr >= NT) return;
-
-  const int t = tr * KT + tc;
-  const uint4 sc = M.sched[t];
-  if (sc.w & 1u) return;  // no ring schedule for this tile: decoded by the whole-tile kernel's exception pass
-  const int base_f = f ? (int)(sc.z & 255u) : 0;
-  const int init_f = (int)((sc.z >> (f ? 16 : 8)) & 255u);
-  const uint32_t counts_f = f ? sc.y : sc.x;  // 2 bits per group: chunks this front loads at that group
-  uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
-  uint2* ring2 = reinterpret_cast<uint2*>(ring);
-  // chunk k of this front = rows [2k, 2k + 2) after its base row; lane l carries row 2k + l / 16, words 2 (l % 16)..
-  // (a uniform tile base plus a 32-bit per-lane offset: chunk k at src[32 k])
-  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
-  const int slot_lane = l >> 4, col2 = l & 15;
-  for (int k = 0; k < init_f; ++k) ring_put<RS>(ring2, k, slot_lane, col2, src[32 * k]);
-  int issued = init_f, written = init_f;
-  uint2 st00 = make_uint2(0, 0), st01 = st00, st10 = st00, st11 = st00;  // staged chunks by group parity
-  int pend0 = 0, pend1 = 0;
-
-  // P = the lane's bit position (relative to the front's base row) + 64: bits 0-4 are the window offset and the
-  // row field (bits 5+) names row r + 2, the row C holds
-  uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
-  // this lane's column of the ring as one opaque byte address, so a row address is (slot * 128) + base
-  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
-  asm volatile("" : "+v"(rlb));
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr int RS_BITS = RS == 16 ? 4 : 5;
+  constexpr bool XS_SGPR = MT == 1;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   uint32_t slot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
   uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
   uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & (RS - 1)) << 7));
   uint32_t C = *(LdsU32*)(rlb + (slot << 7));
-  // this tile's side records (uniform base) + the lane's record (super-block sb: + sb * 64 records)
-  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)((f * 32 + l) * SB);
-  typedef __attribute__((address_space(4))) const uint32_t KU32;
-  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);  // uniform: this tile column's x pairs (m = 1)
   constexpr int NSB = TW / 256;      // super-blocks per tile column
   constexpr int GPS = 16 / NSB;      // staging groups (16 symbols) per super-block
   constexpr int NSUB = 256 / GW;     // sub-blocks per super-block
@@ -456,8 +403,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int g = sb * GPS + gg2 + h;
-        if (h == 0) ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend0, st00, st01);
-        else ring_stage<RS>(ring2, src, slot_lane, col2, counts_f, g, written, issued, pend1, st10, st11);
+        st.stage(g);
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
           const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
@@ -519,7 +465,96 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   }
 #pragma unroll
   for (int j = 0; j < MT; ++j)
-    if (j < mt) (E.P + ((size_t)tc * mt + j) * N + (size_t)tr * TN)[(uint32_t)(f * 32 + l)] = tot[j];
+    if (j < mt) out[(size_t)j * N] = tot[j];
+}
+
+
+template <int KQ, int MT, int WPB, int RS>
+__global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_fused_ring(GroupPlan plan) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
+  constexpr int RING_WORDS = RS * 32, RS_BITS = RS == 16 ? 4 : 5;
+  constexpr int NTHR = WPB * 64;
+  constexpr bool XS_SGPR = MT == 1;  // m = 1: activations straight from the scalar cache
+  __shared__ uint32_t lut4[LUTN];
+  extern __shared__ __align__(16) uint32_t smem[];
+  uint32_t* xs = smem;                                          // [NPAIR][MT] fp16 pairs
+  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);        // [NG][MT] sub-block sums of x
+  uint32_t* rings = reinterpret_cast<uint32_t*>(xg + NG * MT);  // WPB x 2 fronts x RS rows
+
+  // the block's matrix: a uniform index into the plan, read through the kernel-argument segment (scalar loads)
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < plan.n && (int)blockIdx.x >= plan.e[i].block0) mi = i;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const GroupEntry KEntry;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  KEntry* ep = (KEntry*)(kbase + offsetof(GroupPlan, e) + (size_t)mi * sizeof(GroupEntry));
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const int mt = plan.mt;
+  const int bl = (int)blockIdx.x - E.block0;
+  const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
+  // wave-uniform indices are made explicit (scalar registers): the tile, its schedule and its base addresses
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tc = bl % KT, tr = (bl / KT) * WPB + wave;
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+
+  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(M.lut[i]);
+  for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
+    const int j = i / NPAIR, c = i - j * NPAIR;
+    xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
+    const int g = i / MT, j = i - g * MT;
+    float a = 0.f;
+    for (int c = g * (GW / 2); c < (g + 1) * (GW / 2); ++c) {
+      const uint32_t v = xs[c * MT + j];
+      a += h2f(v) + h2f(v >> 16);
+    }
+    xg[g * MT + j] = a;
+  }
+  __syncthreads();
+  if (tr >= NT) return;
+
+  const int t = tr * KT + tc;
+  const uint4 sc = M.sched[t];
+  if (sc.w & 1u) return;  // no ring schedule for this tile: decoded by the whole-tile kernel's exception pass
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  const int base_f = f ? (int)(sc.z & 255u) : 0;
+  uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
+  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
+  uint2* lane_slot = reinterpret_cast<uint2*>(ring) + (l >> 4) * 16 + (l & 15);
+  // P = the lane's bit position (relative to the front's base row) + 64: bits 0-4 are the window offset and the
+  // row field (bits 5+) names row r + 2, the row C holds
+  const uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
+  // this lane's column of the ring as one opaque byte address, so a row address is (slot * 128) + base
+  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
+  asm volatile("" : "+v"(rlb));
+  // this tile's side records (uniform base) + the lane's record (super-block sb: + sb * 64 records)
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)((f * 32 + l) * SB);
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);  // uniform: this tile column's x pairs (m = 1)
+  float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
+  const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
+  if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
+    RingStager<RS, int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = sc.x;
+    st.init((int)init0);
+    ring_tile<KQ, MT, RS>(st, lut4, xs, xg, xcol, srow, P, rlb, mt, N, out);
+  } else {
+    RingStager<RS, int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = f ? sc.y : sc.x;
+    st.init((int)(f ? init1 : init0));
+    ring_tile<KQ, MT, RS>(st, lut4, xs, xg, xcol, srow, P, rlb, mt, N, out);
+  }
 }
 
 int group_waves_per_block(int ring_rows) { return ring_rows == 16 ? 16 : 8; }

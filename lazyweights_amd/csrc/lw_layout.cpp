@@ -55,13 +55,43 @@ inline uint32_t bits_at(const uint32_t* pay, uint64_t pw, uint64_t b) {
   return (uint32_t)((lo | (hi << 32)) >> (b & 31));
 }
 
-// Ring staging schedule of one tile (see the ring kernel): front f stages CHUNK_ROWS-row chunks of its rows, relative
-// to its base row; chunks loaded at group g reach LDS at the start of group g + 2. mn / mx = lowest / highest
-// relative row that any lane reads from the ring in each group; r0 = lowest row of the windows read before group 0.
-// Loads are issued just in time for group g + 2 (at most MAX_CHUNKS_PER_GROUP per group). Returns false if a ring
-// of RS rows cannot hold the schedule.
-bool ring_schedule(const int mn[2][GROUPS], const int mx[2][GROUPS], const int r0[2], int RS, uint64_t& counts,
-                   int init[2]) {
+// Ring staging schedule of one tile (see the ring kernel): each front stages CHUNK_ROWS-row chunks of its rows,
+// relative to its base row; chunks loaded at group g reach LDS at the start of group g + 2. mn / mx = lowest /
+// highest relative row that any lane of front f reads from the ring in each group; r0 = lowest row of the windows
+// read before group 0. The schedule is the same for both fronts (one chunk count per group and one initial count),
+// so the kernel's staging is wave-uniform: loads are issued just in time for the front that needs them first (at
+// most MAX_CHUNKS_PER_GROUP per group). Returns false if a ring of RS rows cannot hold it for either front.
+bool ring_schedule_shared(const int mn[2][GROUPS], const int mx[2][GROUPS], const int r0[2], int RS, uint64_t& counts,
+                          int init[2]) {
+  counts = 0;
+  int in = 0;
+  for (int f = 0; f < 2; ++f) in = std::max(in, (std::max(mx[f][0], mx[f][1]) + CHUNK_ROWS) / CHUNK_ROWS);
+  if (in > 255) return false;
+  for (int f = 0; f < 2; ++f)
+    if (CHUNK_ROWS * in > RS + r0[f]) return false;
+  int issued = in, written = in;
+  int loads[GROUPS] = {0};
+  for (int g = 0; g < GROUPS; ++g) {
+    if (g >= 2) written += loads[g - 2];
+    for (int f = 0; f < 2; ++f)
+      if (mx[f][g] > CHUNK_ROWS * written - 1 || mn[f][g] < CHUNK_ROWS * written - RS) return false;
+    const int gt = std::min(g + 2, GROUPS - 1);
+    const int target = std::max(mx[0][gt], mx[1][gt]);
+    while (CHUNK_ROWS * issued <= target && g + 2 < GROUPS && loads[g] < MAX_CHUNKS_PER_GROUP) {
+      ++loads[g];
+      ++issued;
+    }
+    counts |= (uint64_t)loads[g] << (2 * g);
+  }
+  counts |= counts << 32;  // the same counts for front 1 (bits 32 + 2g)
+  init[0] = init[1] = in;
+  return true;
+}
+
+// The same with one schedule per front (per-lane counts in the kernel): each front's loads are issued just in time
+// for its own rows. Used for tiles the shared schedule cannot hold.
+bool ring_schedule_fronts(const int mn[2][GROUPS], const int mx[2][GROUPS], const int r0[2], int RS,
+                          uint64_t& counts, int init[2]) {
   counts = 0;
   for (int f = 0; f < 2; ++f) {
     init[f] = (std::max(mx[f][0], mx[f][1]) + CHUNK_ROWS) / CHUNK_ROWS;
@@ -129,23 +159,47 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
           mx[f][g] = hi;
         }
       }
-      int init[2] = {0, 0};
+      // Preferably both fronts share one schedule (front 1 may then start its staging up to 4 rows below its first
+      // needed row, base1 - d, to align the two fronts' progress; the first shift that fits is taken), else each
+      // front gets its own.
+      int init[2] = {0, 0}, base_used = base1;
       uint64_t counts = 0;
       uint8_t ok = 0;
       for (int k = 1; k >= 0; --k) {  // a schedule valid for 16 rows is valid for 32 (same loads, looser checks)
+        bool found = false;
+        for (int d = 0; d <= 4 && d <= base1 && !found; ++d) {
+          int mn1[2][GROUPS], mx1[2][GROUPS], r01[2] = {r0[0], r0[1] + d};
+          for (int g = 0; g < GROUPS; ++g) {
+            mn1[0][g] = mn[0][g];
+            mx1[0][g] = mx[0][g];
+            mn1[1][g] = mn[1][g] + d;
+            mx1[1][g] = mx[1][g] + d;
+          }
+          uint64_t c;
+          int in[2];
+          if (base1 - d < 256 && ring_schedule_shared(mn1, mx1, r01, k ? 32 : 16, c, in)) {
+            ok |= (uint8_t)(1 << k);
+            counts = c;
+            init[0] = in[0];
+            init[1] = in[1];
+            base_used = base1 - d;
+            found = true;
+          }
+        }
         uint64_t c;
         int in[2];
-        if (base1 < 256 && ring_schedule(mn, mx, r0, k ? 32 : 16, c, in)) {
+        if (!found && base1 < 256 && ring_schedule_fronts(mn, mx, r0, k ? 32 : 16, c, in)) {
           ok |= (uint8_t)(1 << k);
           counts = c;
           init[0] = in[0];
           init[1] = in[1];
+          base_used = base1;
         }
       }
       ring_ok[t] = ok;
       if (ok) {
         L.sched[2 * (size_t)t] = counts;
-        L.sched[2 * (size_t)t + 1] = (uint64_t)base1 | (uint64_t)init[0] << 8 | (uint64_t)init[1] << 16;
+        L.sched[2 * (size_t)t + 1] = (uint64_t)base_used | (uint64_t)init[0] << 8 | (uint64_t)init[1] << 16;
       }
     }
   });
