@@ -78,7 +78,7 @@ def measure_traffic(layers):
             rows = counter_pass(counter, layers, tmp)
             if not rows:
                 return None
-            ring = [v for k, vs in rows.items() if "k_fused_ring" in k for v in vs]
+            ring = [v for k, vs in rows.items() if ("k_fused_ring" in k or "k_fused_flat" in k) for v in vs]
             copy = [v for k, vs in rows.items() if "copyBuffer" in k for v in vs]
             if not ring or not copy:
                 return None
@@ -240,7 +240,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic["bytes_per_layer_launch"] if traffic else None,
-                         "traffic_detail": traffic, "kernel": "k_fused_ring", "launch": "one grouped launch per layer",
+                         "traffic_detail": traffic, "kernel": "k_fused_flat", "launch": "one grouped launch per layer",
                          "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),

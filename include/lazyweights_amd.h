@@ -86,8 +86,9 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
                         float* const* Y, void* stream);
 
-/* Fused-kernel selection for all handles: 0 (default) = the ring-staged kernel, grouped per layer, wherever a
- * matrix has a ring schedule; 1 = the whole-tile kernel everywhere (the fallback path). Returns 0 or -1. */
+/* Fused-kernel selection for all handles: 0 (default) = the ring-staged kernels wherever a matrix has a ring
+ * schedule (the flat, load-balanced kernel for m = 1; the block-per-column kernel otherwise); 1 = the whole-tile
+ * kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m. Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in

@@ -49,6 +49,23 @@ struct GroupPlan {
   int mt;
   int blocks;
 };
+// Matrices of one launch of the flat ring kernel (m = 1; same K-quant type and ring size). Their tiles form one list:
+// matrix i owns tiles [tile0, tile0 + NT * KT), column-major; block b decodes tiles [b W, b W + W). Every matrix must
+// have at least W tiles, so a block spans at most two matrices.
+struct FlatEntry {
+  DevMat M;
+  const uint32_t* X2;
+  float* P;
+  int tile0;
+};
+struct FlatPlan {
+  FlatEntry e[MAX_GROUP];
+  int n;
+  int W;       // waves (tiles) per block, <= 16 (<= 8 for 32-row rings)
+  int ntiles;  // all tiles of the plan
+};
+hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
+
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
 // K-quant types or ring sizes, or a matrix has no ring schedule).
 hipError_t launch_fused_group(const GroupPlan& plan, hipStream_t s);

@@ -354,10 +354,24 @@ __device__ __forceinline__ uint32_t lut4_entry(uint32_t e) {
   return len | f2h(grid_value<KQ>(sym)) << 16;
 }
 
-// One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring.
-template <int KQ, int MT, int RS, class Stager>
-__device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, const uint32_t* xs, const float* xg,
-                                          __attribute__((address_space(4))) const uint32_t* xcol,
+// x sub-block sums held in LDS per block ([NG][MT], the block-per-column kernel)
+struct XgLds {
+  const float* xg;
+  int MT, nsub;
+  __device__ __forceinline__ float operator()(int sb, int jj, int j) const { return xg[(sb * nsub + jj) * MT + j]; }
+};
+// one token's x sub-block sums of the wave's tile column in scalar registers (the flat kernel): super-block 0, 1
+struct XgRegs {
+  float x0[8], x1[8];
+  __device__ __forceinline__ float operator()(int sb, int jj, int) const { return sb ? x1[jj] : x0[jj]; }
+};
+
+// One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring,
+// `xgf(sub, j)` = sum of token j's x over sub-block `sub` of the tile column, `lutsel` = byte offset of the tile's
+// decode table within `lut4` (0 or 8192, OR-ed into the index).
+template <int KQ, int MT, int RS, class Stager, class Xg>
+__device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint32_t lutsel, const uint32_t* xs,
+                                          const Xg& xgf, __attribute__((address_space(4))) const uint32_t* xcol,
                                           const uint8_t* srow, uint32_t P, uint32_t rlb, int mt, int N, float* out) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -365,6 +379,7 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, cons
   constexpr int RS_BITS = RS == 16 ? 4 : 5;
   constexpr bool XS_SGPR = MT == 1;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  __builtin_amdgcn_s_setprio(3);
   uint32_t slot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
   uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
   uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & (RS - 1)) << 7));
@@ -386,6 +401,7 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, cons
     float dA, dB;
     uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K / IQ4_XS), consumed low byte first
     side_packed<KQ>(sw, scq, scq2, dA, dB);
+    // per super-block x terms: Q4_K / Q5_K mins sum_j m_j (sum x)_j; IQ4_XS bias sum_j s_j (sum x)_j
     float msum[MT], tsum[MT], csum[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
@@ -394,7 +410,12 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, cons
         float mf[8];
         side_mins(sw, mf);
 #pragma unroll
-        for (int jj = 0; jj < NSUB; ++jj) msum[j] = fmaf(mf[jj], xg[(sb * NSUB + jj) * MT + j], msum[j]);
+        for (int jj = 0; jj < NSUB; ++jj) msum[j] = fmaf(mf[jj], xgf(sb, jj, j), msum[j]);
+      }
+      if (KQ == KQ_IQ4_XS) {
+#pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj)
+          csum[j] = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgf(sb, jj, j), csum[j]);
       }
     }
 #pragma unroll 1
@@ -403,14 +424,19 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, cons
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int g = sb * GPS + gg2 + h;
+        // issue priority falls with progress (3 for the first quarter of the tile .. 0 for the last), so the waves
+        // sharing a SIMD keep pace instead of the oldest finishing first and the youngest running alone at the end
+        if (g == 4) __builtin_amdgcn_s_setprio(2);
+        if (g == 8) __builtin_amdgcn_s_setprio(1);
+        if (g == 12) __builtin_amdgcn_s_setprio(0);
         st.stage(g);
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
           const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
-          const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w1 & 0x1FFCu));
+          const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + ((w1 & 0x1FFCu) | lutsel));
           // the second symbol lies within w1: it starts len1 <= 11 bits further and its table index ends by bit 24
           const uint32_t w2 = w1 >> (e1 & 31u);
-          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + (w2 & 0x1FFCu));
+          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + ((w2 & 0x1FFCu) | lutsel));
           P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
           // a pair advances at most 22 bits: the window slides by at most one row
           const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
@@ -445,11 +471,9 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, cons
           const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
                                                                : (float)(uint32_t)(scq & 255u);
           scq >>= 8;
-          const int sub = sb * NSUB + (KQ == KQ_Q5_K ? (gg2 + h) / 2 : gg2 + h);
 #pragma unroll
           for (int j = 0; j < MT; ++j) {
             tsum[j] = fmaf(scv, acc[j], tsum[j]);
-            if (KQ == KQ_IQ4_XS) csum[j] = fmaf(scv, xg[sub * MT + j], csum[j]);
             acc[j] = 0.f;
           }
         }
@@ -546,14 +570,145 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
     st.src = src;
     st.counts = sc.x;
     st.init((int)init0);
-    ring_tile<KQ, MT, RS>(st, lut4, xs, xg, xcol, srow, P, rlb, mt, N, out);
+    ring_tile<KQ, MT, RS>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
   } else {
     RingStager<RS, int, uint32_t> st;
     st.lane_slot = lane_slot;
     st.src = src;
     st.counts = f ? sc.y : sc.x;
     st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, MT, RS>(st, lut4, xs, xg, xcol, srow, P, rlb, mt, N, out);
+    ring_tile<KQ, MT, RS>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
+  }
+}
+
+// ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
+// The tiles of the plan's matrices form one list (matrix by matrix, each column-major: tile rows of one tile
+// column are consecutive) and block b decodes tiles [b W, b W + W), one per wave. W is chosen so that the launch
+// has about two blocks per CU: every CU gets the same number of waves (the block-per-column kernel leaves a
+// third of the CUs at half load for a Mistral layer). A block spans at most two matrices (W <= the smallest
+// matrix's tile count): both decode tables sit in LDS (slot 0, slot 1) and a wave ORs its slot into every table
+// index. Activations come through the scalar cache; each wave sums its column's x per sub-block itself.
+template <int KQ, int RS>
+__global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
+  constexpr int RING_WORDS = RS * 32;
+  __shared__ uint32_t lut4[2 * LUTN];
+  extern __shared__ __align__(16) uint32_t rings[];  // W x 2 fronts x RS rows
+
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * W, Tl = min(T0 + W, plan.ntiles) - 1;
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  const int NTHR = blockDim.x;
+  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(ea->M.lut[i]);
+  if (mb != ma)
+    for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[LUTN + i] = lut4_entry<KQ>(eb->M.lut[i]);
+  __syncthreads();
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = T0 + wave;
+  if (T >= plan.ntiles) return;
+  const bool second = mb != ma && T >= eb->tile0;
+  KEntry* ep = second ? eb : ea;
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const uint32_t lutsel = second ? (uint32_t)(LUTN * 4) : 0u;
+  const int KT = M.KT, NT = M.NT, N = M.N;
+  const int u = T - E.tile0, tc = u / NT, tr = u - tc * NT;
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  const int t = tr * KT + tc;
+  const uint4 sc = M.sched[t];
+  if (sc.w & 1u) return;  // exception tile: decoded by the whole-tile kernel's pass
+
+  // this column's x: pairs through the scalar cache; sub-block sums by lane g, in the same order as the
+  // block-per-column kernel's (so both kernels give the same bits)
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
+  XgRegs xgr;
+  if (KQ != KQ_Q6_K) {
+    constexpr int NSUBT = TW / GW;  // sub-blocks per tile column
+    float a = 0.f;
+    if (lane < NSUBT) {
+      const uint32_t* xl = E.X2 + (size_t)tc * NPAIR + (uint32_t)(lane * (GW / 2));
+      for (int c = 0; c < GW / 2; ++c) {
+        const uint32_t v = xl[c];
+        a += h2f(v) + h2f(v >> 16);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      xgr.x0[g] = g < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), g)) : 0.f;
+      xgr.x1[g] = g + 8 < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), g + 8)) : 0.f;
+    }
+  }
+
+  const int base_f = f ? (int)(sc.z & 255u) : 0;
+  uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
+  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
+  uint2* lane_slot = reinterpret_cast<uint2*>(ring) + (l >> 4) * 16 + (l & 15);
+  const uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
+  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
+  asm volatile("" : "+v"(rlb));
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)((f * 32 + l) * SB);
+  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
+  const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
+  if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
+    RingStager<RS, int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = sc.x;
+    st.init((int)init0);
+    ring_tile<KQ, 1, RS>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+  } else {
+    RingStager<RS, int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = f ? sc.y : sc.x;
+    st.init((int)(f ? init1 : init0));
+    ring_tile<KQ, 1, RS>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+  }
+}
+
+template <int KQ, int RS>
+static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
+  const size_t smem = (size_t)p.W * 2 * RS * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  const int blocks = (p.ntiles + p.W - 1) / p.W;
+  hipLaunchKernelGGL((k_fused_flat<KQ, RS>), dim3(blocks), dim3(p.W * 64), smem, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || p.ntiles < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt, rs = p.e[0].M.ring_rows;
+  for (int i = 0; i < p.n; ++i) {
+    const DevMat& M = p.e[i].M;
+    const int tiles = M.NT * M.KT, end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (M.kqt != kqt || M.ring_rows != rs || !M.sched || p.e[i].tile0 + tiles != end || tiles < p.W ||
+        (i == 0 && p.e[0].tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  if (rs != 16 && rs != 32) return hipErrorInvalidValue;
+  if (rs == 32 && p.W > 8) return hipErrorInvalidValue;  // LDS: 16 KB of tables + W x 8 KB of rings
+  switch (kqt) {
+    case KQ_Q4_K: return rs == 16 ? flat_launch<KQ_Q4_K, 16>(p, s) : flat_launch<KQ_Q4_K, 32>(p, s);
+    case KQ_Q5_K: return rs == 16 ? flat_launch<KQ_Q5_K, 16>(p, s) : flat_launch<KQ_Q5_K, 32>(p, s);
+    case KQ_Q6_K: return rs == 16 ? flat_launch<KQ_Q6_K, 16>(p, s) : flat_launch<KQ_Q6_K, 32>(p, s);
+    case KQ_IQ4_XS: return rs == 16 ? flat_launch<KQ_IQ4_XS, 16>(p, s) : flat_launch<KQ_IQ4_XS, 32>(p, s);
+    default: return hipErrorInvalidValue;
   }
 }
 

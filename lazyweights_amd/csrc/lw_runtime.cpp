@@ -325,7 +325,8 @@ int check_matmul(Tensor* t, const char* name) {
   return 0;
 }
 
-// Kernel selection for the fused path: 0 = ring kernel wherever the matrix has a ring schedule (default),
+// Kernel selection for the fused path: 0 = ring kernels wherever the matrix has a ring schedule (default; the flat
+// kernel for m = 1), 2 = the block-per-column ring kernel for every m,
 // 1 = whole-tile kernel everywhere (kept as the fallback and for tests).
 int g_kernel_mode = 0;
 
@@ -365,8 +366,37 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         if (launches) ++*launches;
       }
   if (forked) HIPCHECK(hipEventRecord(M.join, M.side));
-  // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order
+  // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order;
+  // m = 1 (fp16 x): the flat kernel with balanced blocks
   std::vector<char> done(count, 0);
+  if (ring_ok && mt == 1 && g_kernel_mode != 2) {
+    for (int i = 0; i < count; ++i) {
+      if (done[i] || !ts[i]->dm.ring_rows) continue;
+      const lw::DevMat& di = ts[i]->dm;
+      std::vector<int> sel;
+      for (int j = i; j < count && (int)sel.size() < lw::MAX_GROUP; ++j)
+        if (!done[j] && ts[j]->dm.kqt == di.kqt && ts[j]->dm.ring_rows == di.ring_rows) sel.push_back(j);
+      lw::FlatPlan fp{};
+      int total = 0, mintiles = 1 << 30;
+      for (int j : sel) {
+        const lw::DevMat& dm = ts[j]->dm;
+        lw::FlatEntry& e = fp.e[fp.n++];
+        e.M = dm;
+        e.X2 = static_cast<const uint32_t*>(X16[j]);
+        e.P = M.P + off[j];
+        e.tile0 = total;
+        total += dm.NT * dm.KT;
+        mintiles = std::min(mintiles, dm.NT * dm.KT);
+        done[j] = 1;
+      }
+      // about two blocks per CU (256 CUs), within the table rule (W <= smallest matrix) and the LDS budget
+      const int wmax = di.ring_rows == 16 ? 16 : 8;
+      fp.ntiles = total;
+      fp.W = std::max(1, std::min({(total + 511) / 512, wmax, mintiles}));
+      HIPCHECK(lw::launch_fused_flat(fp, s));
+      if (launches) ++*launches;
+    }
+  }
   for (int i = 0; i < count; ++i) {
     if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
@@ -771,7 +801,7 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 1) return -1;
+  if (mode < 0 || mode > 2) return -1;
   g_kernel_mode = mode;
   return 0;
 }

@@ -272,3 +272,39 @@ def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
         torch.cuda.synchronize()
         check_err(Y.cpu().numpy(), y64[:1], "exception tile m=1")
         check_err(rt.test_matmul("skew", X.float().numpy(), path=0), y64, "exception tile fp32 m=3")
+
+
+def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
+    """The m = 1 flat kernel: one launch over matrices of different sizes (blocks spanning two matrices and two
+    tile columns) gives the same bits as one call per matrix and as the block-per-column ring kernel (mode 2),
+    and every result is within tolerance of fp64."""
+    import ctypes
+
+    import torch
+    rt, mats = fmt_rt
+    for kqt, fmt, H in FORMATS:
+        names = [fmt, fmt + "_small", fmt, fmt + "_small"]
+        X = [torch.randn(1, mats[nm][3]).half() for nm in names]
+        Xd = [x.cuda() for x in X]
+        Yg = [torch.zeros(1, mats[nm][2], device="cuda") for nm in names]
+        n = len(names)
+        rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                        (ctypes.c_void_p * n)(*[x.data_ptr() for x in Xd]), 1,
+                                        (ctypes.c_void_p * n)(*[y.data_ptr() for y in Yg]), None)
+        assert rc == 0, rt.lib.lw_last_error()
+        assert rt.lib.lw_set_kernel_mode(2) == 0
+        try:
+            Yb = [torch.zeros_like(y) for y in Yg]
+            for nm, x, y in zip(names, Xd, Yb):
+                rt.matmul_dev(nm, x, y)
+        finally:
+            rt.lib.lw_set_kernel_mode(0)
+        Ys = [torch.zeros_like(y) for y in Yg]
+        for nm, x, y in zip(names, Xd, Ys):
+            rt.matmul_dev(nm, x, y)
+        torch.cuda.synchronize()
+        say("flat kernel spans / modes", fmt)
+        for nm, x, a, b, c in zip(names, X, Yg, Yb, Ys):
+            assert torch.equal(a, c) and torch.equal(a, b), nm
+            _, y64 = reference_y(orc, mats[nm], x.double().numpy())
+            check_err(a.cpu().numpy(), y64, "%s flat" % nm)
