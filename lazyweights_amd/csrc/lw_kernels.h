@@ -17,6 +17,7 @@ namespace lw {
 // Every lane stream starts with GUARD = 2 zero bits (symbol 0 at stream bit 2).
 struct DevMat {
   const uint16_t* lut;
+  const uint32_t* lut4;  // the ring kernels' 4-byte table entries (decode_table4 in lw_layout.h); null if kqt == 0
   const uint32_t* tbase;
   const uint16_t* mid;
   const uint16_t* rows;
@@ -29,8 +30,10 @@ struct DevMat {
   int KT, NT;       // tile columns, tile rows
   int max_rows;     // max over tiles of rows[t]
   int ring_rows;    // 16 / 32: ring kernel usable with that ring; 0: whole-tile kernel only
-  const uint32_t* exc;  // tiles the ring kernel skips (no schedule for ring_rows), decoded by the whole-tile kernel
-  int nexc;
+  // tiles the ring kernel skips (no schedule for ring_rows): the first nexc32 have a 32-row ring schedule (decoded
+  // by the flat ring kernel from this list), the rest go through the whole-tile kernel
+  const uint32_t* exc;
+  int nexc, nexc32;
 };
 
 // Matrices of one grouped launch of the ring kernel (same K-quant type and ring size). Matrix i owns blocks
@@ -56,7 +59,8 @@ struct FlatEntry {
   DevMat M;
   const uint32_t* X2;
   float* P;
-  int tile0;
+  const uint32_t* list;  // null: the matrix's tiles in column-major order; else these tile indices (exception pass)
+  int tile0, ntile;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];
@@ -85,7 +89,7 @@ hipError_t launch_reduce_group(const ReducePlan& plan, hipStream_t s);
 
 // X16 [mt][K] fp16 (mt pseudo-tokens); P [KT][mt][N] fp32 per-tile-column partials.
 hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
-// the whole-tile kernel over M.exc only (the ring kernel's exception tiles); no-op when there are none
+// the whole-tile kernel over M.exc[nexc32 .. nexc) (exception tiles without any ring schedule); no-op if none
 hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
 // Y[j][n] (row stride ldy) = sum over tile columns tc (in order) of P[tc][jj][n], jj over `per` pseudo-tokens of
 // token j (per = 1: fp16 activations; per = 2: fp32 activations split into fp16 hi + lo).

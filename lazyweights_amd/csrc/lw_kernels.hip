@@ -289,8 +289,25 @@ hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipS
 }
 
 hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s) {
-  if (M.nexc == 0) return hipSuccess;
+  if (M.nexc <= 0) return hipSuccess;
   return fused_any(M, X16, mt, P, M.exc, M.nexc, s);
+}
+
+// Sum of x over one sub-block (GW weights = GW / 2 fp16 pairs, pair(c) for c < GW / 2) in a fixed order shared by
+// every kernel: four quarter sums, each sequential, combined as (q0 + q1) + (q2 + q3).
+template <int GW, class Pair>
+__device__ __forceinline__ float xsum_sub(Pair pair) {
+  constexpr int Q = GW / 8;  // pairs per quarter
+  float q[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q[k] = 0.f;
+    for (int c = 0; c < Q; ++c) {
+      const uint32_t v = pair(k * Q + c);
+      q[k] += h2f(v) + h2f(v >> 16);
+    }
+  }
+  return (q[0] + q[1]) + (q[2] + q[3]);
 }
 
 // Ring staging of one front: chunk k = rows [2k, 2k + 2) after the front's base row; lane l carries row
@@ -337,22 +354,12 @@ struct RingStager {
 // decodes from one 32-bit window w1 = alignbit(B, A, pos): the first symbol at the guard-aligned offset, the second
 // from w1 >> len1. So the only LDS reads on a pair's dependency chain are its two table lookups.
 //
-// The decode table holds 4-byte entries (8 KB, half the LDS bank traffic of {value, length} pairs): bits 0-7 =
-// code length; 4-bit formats: bytes 2 and 3 = the pair's two grid bytes (Q4_K: q; IQ4_XS: kv[q] + 128), which one
-// byte permute turns into two fp16 denormals g * 2^-24 for v_dot2 (exact: g < 256; the 2^24 is folded into d);
-// 8-bit formats: bits 16-31 = fp16(f(q)). The position update adds whole entries: only bits 0-8 of Q are ever
-// used (ring row and bit offset), and the entries' upper halves only disturb bits >= 16.
+// The decode table holds 4-byte entries (8 KB, built at load time: DevMat::lut4, decode_table4): bits 0-7 = code
+// length; 4-bit formats: bytes 2 and 3 = the pair's two grid bytes (Q4_K: q; IQ4_XS: kv[q] + 128), which one byte
+// permute turns into two fp16 denormals g * 2^-24 for v_dot2 (exact: g < 256; the 2^24 is folded into d); 8-bit
+// formats: bits 16-31 = fp16(f(q)). The position update adds whole entries: only bits 0-15 of the position are
+// used (ring slot and bit offset), and the entries' upper halves only disturb bits >= 16.
 // block = WPB tile rows of one tile column of one matrix of the plan.
-template <int KQ>
-__device__ __forceinline__ uint32_t lut4_entry(uint32_t e) {
-  const uint32_t sym = e & 255u, len = e >> 8;
-  if (kq_symbits(KQ) == 4) {
-    if (KQ == KQ_IQ4_XS)
-      return len | (uint32_t)(IQ4_GRID[sym & 15u] + 128) << 16 | (uint32_t)(IQ4_GRID[sym >> 4] + 128) << 24;
-    return len | (sym & 15u) << 16 | (sym >> 4) << 24;
-  }
-  return len | f2h(grid_value<KQ>(sym)) << 16;
-}
 
 // x sub-block sums held in LDS per block ([NG][MT], the block-per-column kernel)
 struct XgLds {
@@ -527,7 +534,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   const int tc = bl % KT, tr = (bl / KT) * WPB + wave;
   const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
 
-  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(M.lut[i]);
+  for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
   for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
     const int j = i / NPAIR, c = i - j * NPAIR;
     xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
@@ -535,12 +542,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   __syncthreads();
   for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
     const int g = i / MT, j = i - g * MT;
-    float a = 0.f;
-    for (int c = g * (GW / 2); c < (g + 1) * (GW / 2); ++c) {
-      const uint32_t v = xs[c * MT + j];
-      a += h2f(v) + h2f(v >> 16);
-    }
-    xg[g * MT + j] = a;
+    xg[g * MT + j] = xsum_sub<GW>([&](int c) { return xs[(g * (GW / 2) + c) * MT + j]; });
   }
   __syncthreads();
   if (tr >= NT) return;
@@ -612,9 +614,10 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
   const int NTHR = blockDim.x;
-  for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[i] = lut4_entry<KQ>(ea->M.lut[i]);
+  for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(ea->M.lut4)[i];
   if (mb != ma)
-    for (int i = threadIdx.x; i < LUTN; i += NTHR) lut4[LUTN + i] = lut4_entry<KQ>(eb->M.lut[i]);
+    for (int i = threadIdx.x; i < LUTN / 4; i += NTHR)
+      reinterpret_cast<uint4*>(lut4 + LUTN)[i] = reinterpret_cast<const uint4*>(eb->M.lut4)[i];
   __syncthreads();
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -626,30 +629,34 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   const auto& M = E.M;
   const uint32_t lutsel = second ? (uint32_t)(LUTN * 4) : 0u;
   const int KT = M.KT, NT = M.NT, N = M.N;
-  const int u = T - E.tile0, tc = u / NT, tr = u - tc * NT;
+  const int u = T - E.tile0;
+  const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;  // column-major order, or the exception list
+  const int tc = t % KT, tr = t / KT;
   const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
-  const int t = tr * KT + tc;
   const uint4 sc = M.sched[t];
-  if (sc.w & 1u) return;  // exception tile: decoded by the whole-tile kernel's pass
+  if (!E.list && (sc.w & 1u)) return;  // exception tile: decoded by the exception pass
 
   // this column's x: pairs through the scalar cache; sub-block sums by lane g, in the same order as the
   // block-per-column kernel's (so both kernels give the same bits)
   KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
   XgRegs xgr;
   if (KQ != KQ_Q6_K) {
-    constexpr int NSUBT = TW / GW;  // sub-blocks per tile column
+    // lane 4 g + k sums quarter k of sub-block g; two exchanges give (q0 + q1) + (q2 + q3), as xsum_sub
+    constexpr int NSUBT = TW / GW, Q = GW / 8;  // sub-blocks per tile column, pairs per quarter
     float a = 0.f;
-    if (lane < NSUBT) {
-      const uint32_t* xl = E.X2 + (size_t)tc * NPAIR + (uint32_t)(lane * (GW / 2));
-      for (int c = 0; c < GW / 2; ++c) {
+    if (lane < 4 * NSUBT) {
+      const uint32_t* xl = E.X2 + (size_t)tc * NPAIR + (uint32_t)(lane * Q);
+      for (int c = 0; c < Q; ++c) {
         const uint32_t v = xl[c];
         a += h2f(v) + h2f(v >> 16);
       }
     }
+    a += __shfl_xor(a, 1);
+    a += __shfl_xor(a, 2);
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
-      xgr.x0[g] = g < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), g)) : 0.f;
-      xgr.x1[g] = g + 8 < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), g + 8)) : 0.f;
+      xgr.x0[g] = g < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * g)) : 0.f;
+      xgr.x1[g] = g + 8 < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * (g + 8))) : 0.f;
     }
   }
 
@@ -695,10 +702,11 @@ hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || p.ntiles < 1) return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt, rs = p.e[0].M.ring_rows;
   for (int i = 0; i < p.n; ++i) {
-    const DevMat& M = p.e[i].M;
-    const int tiles = M.NT * M.KT, end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
-    if (M.kqt != kqt || M.ring_rows != rs || !M.sched || p.e[i].tile0 + tiles != end || tiles < p.W ||
-        (i == 0 && p.e[0].tile0 != 0))
+    const FlatEntry& e = p.e[i];
+    const DevMat& M = e.M;
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (M.kqt != kqt || M.ring_rows != rs || !M.sched || !M.lut4 || e.tile0 + e.ntile != end || e.ntile < p.W ||
+        (!e.list && e.ntile != M.NT * M.KT) || (i == 0 && e.tile0 != 0))
       return hipErrorInvalidValue;
   }
   if (rs != 16 && rs != 32) return hipErrorInvalidValue;
@@ -749,7 +757,7 @@ hipError_t launch_fused_group(const GroupPlan& p, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.mt < 1 || p.mt > 16 || p.blocks < 1) return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt, rs = p.e[0].M.ring_rows;
   for (int i = 0; i < p.n; ++i)
-    if (p.e[i].M.kqt != kqt || p.e[i].M.ring_rows != rs || !p.e[i].M.sched) return hipErrorInvalidValue;
+    if (p.e[i].M.kqt != kqt || p.e[i].M.ring_rows != rs || !p.e[i].M.sched || !p.e[i].M.lut4) return hipErrorInvalidValue;
   if (rs != 16 && rs != 32) return hipErrorInvalidValue;
   switch (kqt) {
     case KQ_Q4_K: return ring_kq<KQ_Q4_K>(p, s);

@@ -9,6 +9,7 @@
 #include <mutex>
 #include <thread>
 
+#include "lw_codec.h"
 #include "lw_format.h"
 
 namespace lw {
@@ -213,13 +214,16 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
     all32 = all32 && (ring_ok[t] & 2);
   }
   L.exc.clear();
+  L.nexc32 = 0;
   if (32 * (T - n16) <= T) {
     L.ring_rows = 16;
-    for (int t = 0; t < T; ++t)
-      if (!(ring_ok[t] & 1)) {
-        L.exc.push_back((uint32_t)t);
-        L.sched[2 * (size_t)t + 1] |= 1ull << 32;
-      }
+    for (int pass = 0; pass < 2; ++pass)  // exception tiles with a 32-row schedule first
+      for (int t = 0; t < T; ++t)
+        if (!(ring_ok[t] & 1) && (pass == 0) == ((ring_ok[t] & 2) != 0)) {
+          L.exc.push_back((uint32_t)t);
+          L.sched[2 * (size_t)t + 1] |= 1ull << 32;
+          L.nexc32 += pass == 0;
+        }
   } else {
     L.ring_rows = all32 ? 32 : 0;
   }
@@ -394,6 +398,26 @@ double cpu_decode(const uint8_t* blob, int N, int KS, int threads, uint8_t* out)
   work(0);
   for (auto& x : th) x.join();
   return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+}  // namespace lw
+
+namespace lw {
+
+void decode_table4(int kqt, const uint16_t* lut, uint32_t* out) {
+  for (int i = 0; i < LUTN; ++i) {
+    const uint32_t sym = lut[i] & 255u, len = lut[i] >> 8;
+    uint32_t v = len;
+    if (kq_symbits(kqt) == 4) {
+      const uint32_t lo = sym & 15u, hi = sym >> 4;
+      if (kqt == KQ_IQ4_XS) v |= (uint32_t)(IQ4_GRID[lo] + 128) << 16 | (uint32_t)(IQ4_GRID[hi] + 128) << 24;
+      else v |= lo << 16 | hi << 24;
+    } else {
+      const float g = kqt == KQ_Q6_K ? (float)sym - 32.f : (float)sym;
+      v |= (uint32_t)f32_to_f16(g) << 16;
+    }
+    out[i] = v;
+  }
 }
 
 }  // namespace lw

@@ -35,6 +35,7 @@ struct Layout {
   // tiles without a schedule for ring_rows (bit 32 of their sched word 1 set): the ring kernel skips them and the
   // whole-tile kernel decodes them from this list
   std::vector<uint32_t> exc;
+  int nexc32 = 0;  // the first nexc32 exception tiles have a 32-row ring schedule (in sched)
   int max_rows = 0;
   uint64_t payload_bits = 0;    // coded bits of all lanes
 };
@@ -52,5 +53,10 @@ bool build_layout_il(const uint8_t* data, size_t len, int N, int KS, bool compac
 double cpu_decode(const uint8_t* blob, int N, int KS, int threads, uint8_t* out);
 
 int default_threads();
+
+// The ring kernels' decode table for K-quant type kqt (1..4): entry i = code length (bits 0-7) and, for 4-bit
+// symbols, the two grid bytes at bytes 2 and 3 (Q4_K: q; IQ4_XS: kv[q] + 128), for 8-bit symbols fp16(f(q)) in bits
+// 16-31 (Q5_K: q; Q6_K: q - 32).
+void decode_table4(int kqt, const uint16_t* lut, uint32_t* out);
 
 }  // namespace lw

@@ -215,15 +215,16 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)][exception tiles 4E] padded to 256 B, then
-  // the words
+  // [lut 4096 B][4-byte table 8192 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)][exception tiles 4E]
+  // padded to 256 B, then the words
   const size_t nexc = L.exc.size();
-  const size_t o_tb = 2 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
+  const size_t o_lut4 = 2 * lw::LUTN, o_tb = o_lut4 + 4 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
   const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_exc = o_sched + 16ull * T;
   const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
   memcpy(host.data(), L.lut, 2 * lw::LUTN);
+  if (t.kqt) lw::decode_table4(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_lut4));
   memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
   memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
@@ -246,6 +247,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   lw::DevMat& dm = t.dm;
   uint8_t* b = static_cast<uint8_t*>(d);
   dm.lut = reinterpret_cast<const uint16_t*>(b);
+  dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_lut4) : nullptr;
   dm.tbase = reinterpret_cast<const uint32_t*>(b + o_tb);
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
   dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
@@ -254,6 +256,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.ring_rows = L.ring_rows;
   dm.exc = nexc ? reinterpret_cast<const uint32_t*>(b + o_exc) : nullptr;
   dm.nexc = (int)nexc;
+  dm.nexc32 = L.nexc32;
   dm.side = nullptr;
   dm.N = (int)t.N;
   dm.K = (int)t.K;
@@ -350,21 +353,58 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     plan.blocks = 0;
     return 0;
   };
-  // exception tiles (no ring schedule) through the whole-tile kernel, on the side stream beside the ring launches
-  // (disjoint partials); the reduction waits for both
+  // exception tiles (no 16-row ring schedule), on the side stream beside the ring launches (disjoint partials):
+  // those with a 32-row schedule through the flat ring kernel (m = 1) in one launch per K-quant type, the rest
+  // (and every exception tile when m > 1) through the whole-tile kernel; the reduction waits for both streams
   const bool ring_ok = g_kernel_mode != 1;
   bool forked = false;
-  if (ring_ok)
-    for (int i = 0; i < count; ++i)
-      if (ts[i]->dm.ring_rows && ts[i]->dm.nexc) {
-        if (!forked) {
-          HIPCHECK(hipEventRecord(M.fork, s));
-          HIPCHECK(hipStreamWaitEvent(M.side, M.fork, 0));
-          forked = true;
-        }
-        HIPCHECK(lw::launch_fused_exceptions(ts[i]->dm, X16[i], mt, M.P + off[i], M.side));
-        if (launches) ++*launches;
+  auto fork = [&]() -> int {
+    if (!forked) {
+      HIPCHECK(hipEventRecord(M.fork, s));
+      HIPCHECK(hipStreamWaitEvent(M.side, M.fork, 0));
+      forked = true;
+    }
+    return 0;
+  };
+  if (ring_ok) {
+    const bool flat = mt == 1 && g_kernel_mode != 2;
+    std::vector<char> xdone(count, 0);
+    for (int i = 0; flat && i < count; ++i) {
+      if (xdone[i] || !ts[i]->dm.ring_rows || !ts[i]->dm.nexc32) continue;
+      lw::FlatPlan fp{};
+      for (int j = i; j < count && fp.n < lw::MAX_GROUP; ++j) {
+        const lw::DevMat& dm = ts[j]->dm;
+        if (xdone[j] || !dm.ring_rows || !dm.nexc32 || dm.kqt != ts[i]->dm.kqt) continue;
+        lw::FlatEntry& e = fp.e[fp.n++];
+        e.M = dm;
+        e.M.ring_rows = 32;  // these tiles' schedules are for a 32-row ring
+        e.X2 = static_cast<const uint32_t*>(X16[j]);
+        e.P = M.P + off[j];
+        e.list = dm.exc;
+        e.tile0 = fp.ntiles;
+        e.ntile = dm.nexc32;
+        fp.ntiles += dm.nexc32;
+        xdone[j] = 1;
       }
+      fp.W = 1;
+      if (fork()) return -1;
+      HIPCHECK(lw::launch_fused_flat(fp, M.side));
+      if (launches) ++*launches;
+    }
+    for (int i = 0; i < count; ++i) {
+      const lw::DevMat& dm = ts[i]->dm;
+      if (!dm.ring_rows || !dm.nexc) continue;
+      lw::DevMat rest = dm;
+      if (flat) {  // the flat pass took the first nexc32
+        rest.exc = dm.exc + dm.nexc32;
+        rest.nexc = dm.nexc - dm.nexc32;
+      }
+      if (!rest.nexc) continue;
+      if (fork()) return -1;
+      HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], M.side));
+      if (launches) ++*launches;
+    }
+  }
   if (forked) HIPCHECK(hipEventRecord(M.join, M.side));
   // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order;
   // m = 1 (fp16 x): the flat kernel with balanced blocks
@@ -384,7 +424,9 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         e.M = dm;
         e.X2 = static_cast<const uint32_t*>(X16[j]);
         e.P = M.P + off[j];
+        e.list = nullptr;
         e.tile0 = total;
+        e.ntile = dm.NT * dm.KT;
         total += dm.NT * dm.KT;
         mintiles = std::min(mintiles, dm.NT * dm.KT);
         done[j] = 1;
