@@ -437,7 +437,8 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
         if (g == 8) __builtin_amdgcn_s_setprio(1);
         if (g == 12) __builtin_amdgcn_s_setprio(0);
         st.stage(g);
-#pragma unroll
+        // m = 1 unrolls the group fully; more tokens unroll less (their x operands come from LDS per pair)
+#pragma unroll(MT == 1 ? 8 : 2)
         for (int p = 0; p < 8; ++p) {
           const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
           const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + ((w1 & 0x1FFCu) | lutsel));
@@ -768,6 +769,7 @@ hipError_t launch_fused_group(const GroupPlan& p, hipStream_t s) {
   }
 }
 
+template <int PER>
 __global__ void k_reduce_group(ReducePlan plan) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= plan.total) return;
@@ -775,32 +777,32 @@ __global__ void k_reduce_group(ReducePlan plan) {
 #pragma unroll
   for (int k = 1; k < MAX_GROUP; ++k)
     if (k < plan.n && i >= plan.e[k].out0) E = plan.e[k];
-  const int o = i - E.out0, j = o / E.N, n = o - j * E.N, per = plan.per, mt = plan.m * per;
-  const float* pp = E.P + (size_t)j * per * E.N + n;
-  const size_t step = (size_t)mt * E.N;
-  // partials summed in tile-column order (pseudo-tokens of a column in order); eight columns' loads in flight
+  const int o = i - E.out0, j = o / E.N, n = o - j * E.N;
+  const uint32_t o0 = (uint32_t)(j * PER * E.N + n), step = (uint32_t)(plan.m * PER * E.N);
+  // partials summed in tile-column order (a column's pseudo-tokens in order), the loads of up to 32 / PER columns
+  // in flight
+  constexpr int B = 32 / PER;
   float a = 0.f;
-  int tc = 0;
-  for (; tc + 8 <= E.KT; tc += 8) {
-    float v[8][2];
+  for (int tc = 0; tc < E.KT; tc += B) {
+    float v[B][PER];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < B; ++u)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) v[u][q] = q < per ? pp[(size_t)(tc + u) * step + (size_t)q * E.N] : 0.f;
+      for (int q = 0; q < PER; ++q)
+        v[u][q] = tc + u < E.KT ? E.P[o0 + (uint32_t)(tc + u) * step + (uint32_t)(q * E.N)] : 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      a += v[u][0];
-      if (per > 1) a += v[u][1];
-    }
+    for (int u = 0; u < B; ++u)
+      if (tc + u < E.KT)
+#pragma unroll
+        for (int q = 0; q < PER; ++q) a += v[u][q];
   }
-  for (; tc < E.KT; ++tc)
-    for (int q = 0; q < per; ++q) a += pp[(size_t)tc * step + (size_t)q * E.N];
   E.Y[(size_t)j * E.ldy + n] = a;
 }
 
 hipError_t launch_reduce_group(const ReducePlan& p, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.total < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_reduce_group, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
+  if (p.n < 1 || p.n > MAX_GROUP || p.total < 1 || p.per < 1 || p.per > 2) return hipErrorInvalidValue;
+  if (p.per == 1) hipLaunchKernelGGL(k_reduce_group<1>, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(k_reduce_group<2>, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
