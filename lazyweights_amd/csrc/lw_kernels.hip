@@ -361,6 +361,14 @@ struct RingStager {
 // used (ring slot and bit offset), and the entries' upper halves only disturb bits >= 16.
 // block = WPB tile rows of one tile column of one matrix of the plan.
 
+// LDS address of the table entry indexed by window bits 2..12 of w: (w & 0x1FFC) | table base, one instruction (the
+// base is a multiple of 8 KB and wave-uniform)
+__device__ __forceinline__ uint32_t table_addr(uint32_t w, uint32_t base, uint32_t mask) {
+  uint32_t a;  // VOP3 takes no literal here: the mask 0x1FFC lives in a register
+  asm("v_and_or_b32 %0, %1, %3, %2" : "=v"(a) : "v"(w), "s"(base), "v"(mask));
+  return a;
+}
+
 // x sub-block sums held in LDS per block ([NG][MT], the block-per-column kernel)
 struct XgLds {
   const float* xg;
@@ -386,6 +394,10 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
   constexpr int RS_BITS = RS == 16 ? 4 : 5;
   constexpr bool XS_SGPR = MT == 1;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  // LDS byte address of the tile's table (a multiple of 8 KB: the tables are the kernels' only static LDS object)
+  const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4 + lutsel;
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
   __builtin_amdgcn_s_setprio(3);
   uint32_t slot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
   uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
@@ -438,13 +450,13 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
         if (g == 12) __builtin_amdgcn_s_setprio(0);
         st.stage(g);
         // m = 1 unrolls the group fully; more tokens unroll less (their x operands come from LDS per pair)
-#pragma unroll(MT == 1 ? 8 : 2)
+#pragma unroll MT == 1 ? 8 : 2
         for (int p = 0; p < 8; ++p) {
           const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
-          const uint32_t e1 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + ((w1 & 0x1FFCu) | lutsel));
+          const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
           // the second symbol lies within w1: it starts len1 <= 11 bits further and its table index ends by bit 24
           const uint32_t w2 = w1 >> (e1 & 31u);
-          const uint32_t e2 = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut4) + ((w2 & 0x1FFCu) | lutsel));
+          const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
           P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
           // a pair advances at most 22 bits: the window slides by at most one row
           const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
