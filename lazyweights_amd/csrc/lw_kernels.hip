@@ -603,14 +603,14 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 // third of the CUs at half load for a Mistral layer). A block spans at most two matrices (W <= the smallest
 // matrix's tile count): both decode tables sit in LDS (slot 0, slot 1) and a wave ORs its slot into every table
 // index. Activations come through the scalar cache; each wave sums its column's x per sub-block itself.
-template <int KQ, int RS>
+template <int KQ, int RS, int NTAB>
 __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ), NPAIR = TW / 2;
   static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
   constexpr int RING_WORDS = RS * 32;
-  __shared__ uint32_t lut4[2 * LUTN];
+  __shared__ uint32_t lut4[NTAB * LUTN];             // NTAB = 1: every block holds one matrix (W = 1 launches)
   extern __shared__ __align__(16) uint32_t rings[];  // W x 2 fronts x RS rows
 
   typedef __attribute__((address_space(4))) const char KChar;
@@ -628,7 +628,7 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
   const int NTHR = blockDim.x;
   for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(ea->M.lut4)[i];
-  if (mb != ma)
+  if (NTAB > 1 && mb != ma)
     for (int i = threadIdx.x; i < LUTN / 4; i += NTHR)
       reinterpret_cast<uint4*>(lut4 + LUTN)[i] = reinterpret_cast<const uint4*>(eb->M.lut4)[i];
   __syncthreads();
@@ -700,15 +700,21 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   }
 }
 
-template <int KQ, int RS>
-static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
+template <int KQ, int RS, int NTAB>
+static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
   const size_t smem = (size_t)p.W * 2 * RS * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + p.W - 1) / p.W;
-  hipLaunchKernelGGL((k_fused_flat<KQ, RS>), dim3(blocks), dim3(p.W * 64), smem, s, p);
+  hipLaunchKernelGGL((k_fused_flat<KQ, RS, NTAB>), dim3(blocks), dim3(p.W * 64), smem, s, p);
   return hipGetLastError();
+}
+
+// one-wave blocks never span two matrices: one table
+template <int KQ, int RS>
+static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
+  return p.W == 1 ? flat_launch_t<KQ, RS, 1>(p, s) : flat_launch_t<KQ, RS, 2>(p, s);
 }
 
 hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {

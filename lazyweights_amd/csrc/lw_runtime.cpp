@@ -103,9 +103,6 @@ struct Model {
   uint64_t file_size = 0;
   bool gpu = false;
   hipStream_t stream = nullptr;
-  // side stream + events: the whole-tile pass over exception tiles runs beside the ring launch
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
   size_t resident_bytes = 0, coded_bytes = 0, device_bytes = 0, pad_bytes = 0;
   long long avail_after_kb = -1;
   int pos = 0, window = 0;
@@ -303,9 +300,6 @@ void release(Model* M) {
   if (M->X16) (void)hipFree(M->X16);
   if (M->codes) (void)hipFree(M->codes);
   if (M->stream) (void)hipStreamDestroy(M->stream);
-  if (M->side) (void)hipStreamDestroy(M->side);
-  if (M->fork) (void)hipEventDestroy(M->fork);
-  if (M->join) (void)hipEventDestroy(M->join);
   if (M->fd >= 0) close(M->fd);
   delete M;
 }
@@ -353,19 +347,11 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     plan.blocks = 0;
     return 0;
   };
-  // exception tiles (no 16-row ring schedule), on the side stream beside the ring launches (disjoint partials):
-  // those with a 32-row schedule through the flat ring kernel (m = 1) in one launch per K-quant type, the rest
-  // (and every exception tile when m > 1) through the whole-tile kernel; the reduction waits for both streams
+  // exception tiles (no 16-row ring schedule) ahead of the ring launches, on the same stream: those with a 32-row
+  // schedule through the flat ring kernel (m = 1) in one launch per K-quant type, the rest (and every exception
+  // tile when m > 1) through the whole-tile kernel. (A second stream overlapped them with the ring launch but its
+  // join cost more than the serial pass: these are one-wave launches over a few tiles.)
   const bool ring_ok = g_kernel_mode != 1;
-  bool forked = false;
-  auto fork = [&]() -> int {
-    if (!forked) {
-      HIPCHECK(hipEventRecord(M.fork, s));
-      HIPCHECK(hipStreamWaitEvent(M.side, M.fork, 0));
-      forked = true;
-    }
-    return 0;
-  };
   if (ring_ok) {
     const bool flat = mt == 1 && g_kernel_mode != 2;
     std::vector<char> xdone(count, 0);
@@ -387,8 +373,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         xdone[j] = 1;
       }
       fp.W = 1;
-      if (fork()) return -1;
-      HIPCHECK(lw::launch_fused_flat(fp, M.side));
+      HIPCHECK(lw::launch_fused_flat(fp, s));
       if (launches) ++*launches;
     }
     for (int i = 0; i < count; ++i) {
@@ -400,12 +385,10 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         rest.nexc = dm.nexc - dm.nexc32;
       }
       if (!rest.nexc) continue;
-      if (fork()) return -1;
-      HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], M.side));
+      HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], s));
       if (launches) ++*launches;
     }
   }
-  if (forked) HIPCHECK(hipEventRecord(M.join, M.side));
   // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order;
   // m = 1 (fp16 x): the flat kernel with balanced blocks
   std::vector<char> done(count, 0);
@@ -463,7 +446,6 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     if (flush()) return -1;
   }
-  if (forked) HIPCHECK(hipStreamWaitEvent(s, M.join, 0));
   if (!reduce) return 0;
   // ordered reduction over tile columns, up to MAX_GROUP matrices per launch
   lw::ReducePlan rp{};
@@ -551,10 +533,7 @@ void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, 
       release(M.release());
       return nullptr;
     }
-    if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&M->side, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&M->fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&M->join, hipEventDisableTiming) != hipSuccess) {
+    if (hipStreamCreateWithFlags(&M->stream, hipStreamNonBlocking) != hipSuccess) {
       fail("rt_open: stream creation failed");
       release(M.release());
       return nullptr;
