@@ -327,6 +327,38 @@ int check_matmul(Tensor* t, const char* name) {
 // 1 = whole-tile kernel everywhere (kept as the fallback and for tests).
 int g_kernel_mode = 0;
 
+// Waves per block of the flat kernel for a launch of `total` tiles. Every block is W waves of one tile each and
+// stays resident until its slowest wave ends. The blocks spread evenly over the CUs; a CU runs its share in rounds
+// of as many blocks as fit at once, and a round takes about max(its waves, 16) tile times (below 16 waves a CU is
+// no longer issue-bound). W minimizes the busiest CU's sum over rounds (ties: the larger W), within the kernel's
+// limits: 16 waves per block, W <= the smallest matrix's tile count (a block holds at most two tables), and the
+// LDS of a CU (160 KB: two 8 KB tables + W x 2 rings of rs rows per block). Config 2's 13,312 tiles on 256 CUs
+// give W = 13: 1024 blocks, two rounds of 26 waves per CU (W = 16 leaves a third block on 64 CUs).
+int flat_width(int total, int rs, int mintiles) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+  }
+  const int wmax = std::min(rs == 16 ? 16 : 8, mintiles);
+  int best = 1;
+  long long best_cost = -1;
+  for (int w = 1; w <= wmax; ++w) {
+    const int lds = (w > 1 ? 2 : 1) * 8192 + w * 2 * rs * 128;
+    const long long per_cu = std::min(160 * 1024 / lds, 32 / w);
+    const long long blocks = (total + w - 1) / w, b = (blocks + cus - 1) / cus;
+    const long long full = b / per_cu, rest = b % per_cu;
+    const long long cost = full * std::max<long long>(per_cu * w, 16) + (rest ? std::max<long long>(rest * w, 16) : 0);
+    if (best_cost < 0 || cost <= best_cost) {
+      best_cost = cost;
+      best = w;
+    }
+  }
+  return std::max(1, best);
+}
+
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
 // others into whole-tile launches; then one ordered reduction per MAX_GROUP matrices. Partials of all matrices
@@ -414,10 +446,8 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         mintiles = std::min(mintiles, dm.NT * dm.KT);
         done[j] = 1;
       }
-      // about two blocks per CU (256 CUs), within the table rule (W <= smallest matrix) and the LDS budget
-      const int wmax = di.ring_rows == 16 ? 16 : 8;
       fp.ntiles = total;
-      fp.W = std::max(1, std::min({(total + 511) / 512, wmax, mintiles}));
+      fp.W = flat_width(total, di.ring_rows, mintiles);
       HIPCHECK(lw::launch_fused_flat(fp, s));
       if (launches) ++*launches;
     }
