@@ -88,7 +88,8 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 
 /* Fused-kernel selection for all handles: 0 (default) = the ring-staged kernels wherever a matrix has a ring
  * schedule (the flat, load-balanced kernel for m = 1; the block-per-column kernel otherwise); 1 = the whole-tile
- * kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m. Returns 0 or -1. */
+ * kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m; 3 = as 0, but exception
+ * tiles are never decoded inside the flat launch (always by the separate exception pass). Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in

@@ -67,6 +67,9 @@ struct FlatPlan {
   int n;
   int W;       // waves (tiles) per block, <= 16 (<= 8 for 32-row rings)
   int ntiles;  // all tiles of the plan
+  // 16-row launches: spare 16-row ring pairs per block for exception tiles with a 32-row schedule (>= the most
+  // such tiles in any block); 0: exception tiles are skipped (decoded by an exception pass)
+  int nspare;
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
 

@@ -315,15 +315,16 @@ __device__ __forceinline__ float xsum_sub(Pair pair) {
 // ring slot 0). At the start of group g the chunks loaded at g - 2 are written and group g's loads are issued
 // (2-bit counts per group). Tiles whose two fronts share one schedule use the scalar form (wave-uniform counts,
 // branches and offsets); the others keep one schedule per front (per-lane counts).
-template <int RS, class I, class U>
+template <class I, class U>
 struct RingStager {
   uint2* lane_slot;
   const uint2* src;
   U counts;
+  uint32_t rmask;  // ring rows - 1 (16 or 32 rows, wave-uniform)
   I written, issued, pend0, pend1;
   uint2 s00, s01, s10, s11;  // chunks in flight, by group parity
 
-  __device__ __forceinline__ void put(I k, uint2 v) { lane_slot[((2 * k) & (RS - 1)) * 16] = v; }
+  __device__ __forceinline__ void put(I k, uint2 v) { lane_slot[((2 * k) & (I)rmask) * 16] = v; }
   __device__ __forceinline__ void init(I n) {
     for (I k = 0; k < n; ++k) put(k, src[32 * k]);
     written = issued = n;
@@ -384,14 +385,14 @@ struct XgRegs {
 // One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring,
 // `xgf(sub, j)` = sum of token j's x over sub-block `sub` of the tile column, `lutsel` = byte offset of the tile's
 // decode table within `lut4` (0 or 8192, OR-ed into the index).
-template <int KQ, int MT, int RS, class Stager, class Xg>
+template <int KQ, int MT, class Stager, class Xg>
 __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint32_t lutsel, const uint32_t* xs,
                                           const Xg& xgf, __attribute__((address_space(4))) const uint32_t* xcol,
                                           const uint8_t* srow, uint32_t P, uint32_t rlb, int mt, int N, float* out) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
-  constexpr int RS_BITS = RS == 16 ? 4 : 5;
+  const uint32_t rmask = st.rmask, rbits = rmask == 15u ? 4u : 5u;  // ring of 16 or 32 rows
   constexpr bool XS_SGPR = MT == 1;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   // LDS byte address of the tile's table (a multiple of 8 KB: the tables are the kernels' only static LDS object)
@@ -399,9 +400,9 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
   uint32_t tmask = 0x1FFCu;
   asm volatile("" : "+v"(tmask));
   __builtin_amdgcn_s_setprio(3);
-  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
-  uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & (RS - 1)) << 7));
-  uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & (RS - 1)) << 7));
+  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, rbits);
+  uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & rmask) << 7));
+  uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & rmask) << 7));
   uint32_t C = *(LdsU32*)(rlb + (slot << 7));
   constexpr int NSB = TW / 256;      // super-blocks per tile column
   constexpr int GPS = 16 / NSB;      // staging groups (16 symbols) per super-block
@@ -459,7 +460,7 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
           const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
           P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
           // a pair advances at most 22 bits: the window slides by at most one row
-          const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, RS_BITS);
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, rbits);
           const bool slide = nslot != slot;
           A = slide ? B : A;
           B = slide ? C : B;
@@ -519,7 +520,7 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
   static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
-  constexpr int RING_WORDS = RS * 32, RS_BITS = RS == 16 ? 4 : 5;
+  constexpr int RING_WORDS = RS * 32;
   constexpr int NTHR = WPB * 64;
   constexpr bool XS_SGPR = MT == 1;  // m = 1: activations straight from the scalar cache
   __shared__ uint32_t lut4[LUTN];
@@ -580,42 +581,87 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
   const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
   if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
-    RingStager<RS, int, uint32_t> st;
+    RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
     st.src = src;
     st.counts = sc.x;
+    st.rmask = RS - 1;
     st.init((int)init0);
-    ring_tile<KQ, MT, RS>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
+    ring_tile<KQ, MT>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
   } else {
-    RingStager<RS, int, uint32_t> st;
+    RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
     st.src = src;
     st.counts = f ? sc.y : sc.x;
+    st.rmask = RS - 1;
     st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, MT, RS>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
+    ring_tile<KQ, MT>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
   }
 }
 
 // ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
+// One tile of the flat kernel: lanes of front f stage into `ring` (RS rows of 32 words).
+template <int KQ, class KEntryRef>
+__device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4& sc, uint32_t* ring, uint32_t rmask,
+                                          const uint32_t* lut4, uint32_t lutsel, const XgRegs& xgr, int lane) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int NPAIR = TW / 2;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  const auto& M = E.M;
+  const int KT = M.KT, N = M.N, tc = t % KT, tr = t / KT;
+  const int l = lane & 31, f = lane >> 5;
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
+  const int base_f = f ? (int)(sc.z & 255u) : 0;
+  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
+  uint2* lane_slot = reinterpret_cast<uint2*>(ring) + (l >> 4) * 16 + (l & 15);
+  const uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
+  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
+  asm volatile("" : "+v"(rlb));
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * kq_sbytes(KQ) +
+                        (uint32_t)((f * 32 + l) * kq_sbytes(KQ));
+  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
+  const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
+  if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
+    RingStager<int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = sc.x;
+    st.rmask = rmask;
+    st.init((int)init0);
+    ring_tile<KQ, 1>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+  } else {
+    RingStager<int, uint32_t> st;
+    st.lane_slot = lane_slot;
+    st.src = src;
+    st.counts = f ? sc.y : sc.x;
+    st.rmask = rmask;
+    st.init((int)(f ? init1 : init0));
+    ring_tile<KQ, 1>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+  }
+}
+
 // The tiles of the plan's matrices form one list (matrix by matrix, each column-major: tile rows of one tile
-// column are consecutive) and block b decodes tiles [b W, b W + W), one per wave. W is chosen so that the launch
-// has about two blocks per CU: every CU gets the same number of waves (the block-per-column kernel leaves a
-// third of the CUs at half load for a Mistral layer). A block spans at most two matrices (W <= the smallest
-// matrix's tile count): both decode tables sit in LDS (slot 0, slot 1) and a wave ORs its slot into every table
-// index. Activations come through the scalar cache; each wave sums its column's x per sub-block itself.
+// column are consecutive) and block b decodes tiles [b W, b W + W), one per wave. W is chosen so that every CU gets
+// the same number of waves (the block-per-column kernel leaves a third of the CUs at half load for a Mistral
+// layer). A block spans at most two matrices (W <= the smallest matrix's tile count): both decode tables sit in LDS
+// (slot 0, slot 1) and a wave ORs its slot into every table index. Activations come through the scalar cache; each
+// wave sums its column's x per sub-block itself.
+// Exception tiles (no 16-row schedule) are skipped, except with plan.nspare > 0 in a 16-row launch: then a tile
+// with a 32-row schedule is decoded in place, front 0 in the wave's own two rings (4 KB) and front 1 in spare ring
+// k of the block, k = the number of such tiles before it in the block (the host sizes nspare to the block maximum).
 template <int KQ, int RS, int NTAB>
 __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
-  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  constexpr int GW = kq_gw(KQ);
   static_assert(RS == 16 || RS == 32, "ring of 16 or 32 rows");
   constexpr int RING_WORDS = RS * 32;
   __shared__ uint32_t lut4[NTAB * LUTN];             // NTAB = 1: every block holds one matrix (W = 1 launches)
-  extern __shared__ __align__(16) uint32_t rings[];  // W x 2 fronts x RS rows
+  extern __shared__ __align__(16) uint32_t rings[];  // (W + nspare) x 2 fronts x RS rows
 
   typedef __attribute__((address_space(4))) const char KChar;
   typedef __attribute__((address_space(4))) const FlatEntry KEntry;
-  typedef __attribute__((address_space(4))) const uint32_t KU32;
   KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
   const int W = plan.W, T0 = (int)blockIdx.x * W, Tl = min(T0 + W, plan.ntiles) - 1;
   int ma = 0, mb = 0;
@@ -636,29 +682,40 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int T = T0 + wave;
   if (T >= plan.ntiles) return;
-  const bool second = mb != ma && T >= eb->tile0;
+  const int tile0b = eb->tile0;
+  const bool second = mb != ma && T >= tile0b;
   KEntry* ep = second ? eb : ea;
   const auto& E = *ep;
   const auto& M = E.M;
   const uint32_t lutsel = second ? (uint32_t)(LUTN * 4) : 0u;
-  const int KT = M.KT, NT = M.NT, N = M.N;
+  const int KT = M.KT, NT = M.NT;
   const int u = T - E.tile0;
   const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;  // column-major order, or the exception list
-  const int tc = t % KT, tr = t / KT;
-  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  const int tc = t % KT;
+  const int lane = threadIdx.x & 63;
   const uint4 sc = M.sched[t];
-  if (!E.list && (sc.w & 1u)) return;  // exception tile: decoded by the exception pass
+  int spare = -1;
+  if (!E.list && (sc.w & 1u)) {  // exception tile
+    if (RS != 16 || !plan.nspare || !(sc.w & 2u)) return;  // decoded by the exception pass
+    spare = 0;
+    for (int q = T0; q < T; ++q) {  // 32-row exception tiles earlier in this block
+      const bool qs = mb != ma && q >= tile0b;
+      KEntry* eq = qs ? eb : ea;
+      const int uq = q - eq->tile0, NTq = eq->M.NT, KTq = eq->M.KT;
+      const uint32_t wq = reinterpret_cast<const uint32_t*>(eq->M.sched)[4 * ((uq % NTq) * KTq + uq / NTq) + 3];
+      spare += (wq & 3u) == 3u;
+    }
+    if (spare >= plan.nspare) return;  // cannot happen with the host's sizing; never overrun the spare rings
+  }
 
-  // this column's x: pairs through the scalar cache; sub-block sums by lane g, in the same order as the
-  // block-per-column kernel's (so both kernels give the same bits)
-  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
+  // this column's x sums per sub-block: lane 4 g + k sums quarter k of sub-block g; two exchanges give
+  // (q0 + q1) + (q2 + q3), the order of xsum_sub (so all kernels give the same bits)
   XgRegs xgr;
   if (KQ != KQ_Q6_K) {
-    // lane 4 g + k sums quarter k of sub-block g; two exchanges give (q0 + q1) + (q2 + q3), as xsum_sub
     constexpr int NSUBT = TW / GW, Q = GW / 8;  // sub-blocks per tile column, pairs per quarter
     float a = 0.f;
     if (lane < 4 * NSUBT) {
-      const uint32_t* xl = E.X2 + (size_t)tc * NPAIR + (uint32_t)(lane * Q);
+      const uint32_t* xl = E.X2 + (size_t)tc * (TW / 2) + (uint32_t)(lane * Q);
       for (int c = 0; c < Q; ++c) {
         const uint32_t v = xl[c];
         a += h2f(v) + h2f(v >> 16);
@@ -673,36 +730,17 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
     }
   }
 
-  const int base_f = f ? (int)(sc.z & 255u) : 0;
-  uint32_t* ring = rings + (wave * 2 + f) * RING_WORDS;
-  const uint2* src = reinterpret_cast<const uint2*>(M.words + M.tbase[t]) + (uint32_t)(16 * base_f + l);
-  uint2* lane_slot = reinterpret_cast<uint2*>(ring) + (l >> 4) * 16 + (l & 15);
-  const uint32_t P = (f ? (uint32_t)M.mid[(size_t)t * 32 + (uint32_t)l] - GUARD_BITS : 0u) - 32u * (uint32_t)base_f + 64u;
-  uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(ring + l);
-  asm volatile("" : "+v"(rlb));
-  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)((f * 32 + l) * SB);
-  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
-  const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
-  if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
-    RingStager<RS, int, uint32_t> st;
-    st.lane_slot = lane_slot;
-    st.src = src;
-    st.counts = sc.x;
-    st.init((int)init0);
-    ring_tile<KQ, 1, RS>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
-  } else {
-    RingStager<RS, int, uint32_t> st;
-    st.lane_slot = lane_slot;
-    st.src = src;
-    st.counts = f ? sc.y : sc.x;
-    st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, 1, RS>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
-  }
+  // the ring of the lane's front: 16-row launches place a 32-row exception tile's front 0 in the wave's two rings
+  // and its front 1 in spare ring pair `spare`
+  const int f = lane >> 5;
+  const bool x32 = RS == 16 && spare >= 0;
+  uint32_t* ring = rings + (x32 ? (f ? 2 * W + 2 * spare : 2 * wave) : 2 * wave + f) * RING_WORDS;
+  flat_tile<KQ>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane);
 }
 
 template <int KQ, int RS, int NTAB>
 static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
-  const size_t smem = (size_t)p.W * 2 * RS * 128;
+  const size_t smem = (size_t)(p.W + p.nspare) * 2 * RS * 128;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
@@ -730,6 +768,8 @@ hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
   }
   if (rs != 16 && rs != 32) return hipErrorInvalidValue;
   if (rs == 32 && p.W > 8) return hipErrorInvalidValue;  // LDS: 16 KB of tables + W x 8 KB of rings
+  // spare rings: 16-row launches only, within the LDS of one CU (160 KB: 16 KB of tables + 32 x 4 KB of rings)
+  if (p.nspare < 0 || (p.nspare && (rs != 16 || p.W + p.nspare > 32))) return hipErrorInvalidValue;
   switch (kqt) {
     case KQ_Q4_K: return rs == 16 ? flat_launch<KQ_Q4_K, 16>(p, s) : flat_launch<KQ_Q4_K, 32>(p, s);
     case KQ_Q5_K: return rs == 16 ? flat_launch<KQ_Q5_K, 16>(p, s) : flat_launch<KQ_Q5_K, 32>(p, s);

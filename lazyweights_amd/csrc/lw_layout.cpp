@@ -221,7 +221,7 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
       for (int t = 0; t < T; ++t)
         if (!(ring_ok[t] & 1) && (pass == 0) == ((ring_ok[t] & 2) != 0)) {
           L.exc.push_back((uint32_t)t);
-          L.sched[2 * (size_t)t + 1] |= 1ull << 32;
+          L.sched[2 * (size_t)t + 1] |= (pass == 0 ? 3ull : 1ull) << 32;  // bit 33: has a 32-row schedule
           L.nexc32 += pass == 0;
         }
   } else {

@@ -29,11 +29,12 @@ struct Layout {
   std::vector<uint32_t> words;  // tiles' word rows + zero tail
   // ring staging schedule per tile, 2 x u64: word 0 = 2-bit counts of 2-row chunks that front 0 (bits 2g) and
   // front 1 (bits 32 + 2g) load at group g; word 1 = base row of front 1 (bits 0-7), initial chunks of front 0
-  // (8-15) and front 1 (16-23), bit 32: no schedule (an exception tile)
+  // (8-15) and front 1 (16-23), bit 32: no schedule for ring_rows (an exception tile), bit 33: an exception tile
+  // whose schedule (in words 0-1) is for a 32-row ring
   std::vector<uint64_t> sched;
   int ring_rows = 0;            // 16 or 32 rows per front; 0: the ring schedule does not fit (whole-tile kernels)
-  // tiles without a schedule for ring_rows (bit 32 of their sched word 1 set): the ring kernel skips them and the
-  // whole-tile kernel decodes them from this list
+  // tiles without a schedule for ring_rows (bit 32 of their sched word 1 set): decoded with 32-row rings (in the
+  // ring launch's spare rings, or a one-wave launch over this list) or by the whole-tile kernel
   std::vector<uint32_t> exc;
   int nexc32 = 0;  // the first nexc32 exception tiles have a 32-row ring schedule (in sched)
   int max_rows = 0;

@@ -89,6 +89,7 @@ struct Tensor {
   size_t side_bytes = 0;
   uint64_t payload_bits = 0;
   lw::DevMat dm{};
+  std::vector<uint32_t> exc32;  // host copy of the exception tiles with a 32-row schedule (dm.exc[0, nexc32))
   bool coded() const { return enc == "huf8" || enc == "huf4p"; }
   int KS() const { return (int)(symbits == 4 ? K / 2 : K); }
   int T() const { return (int)((N / lw::TN) * (KS() / lw::TK)); }
@@ -254,6 +255,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.exc = nexc ? reinterpret_cast<const uint32_t*>(b + o_exc) : nullptr;
   dm.nexc = (int)nexc;
   dm.nexc32 = L.nexc32;
+  t.exc32.assign(L.exc.begin(), L.exc.begin() + L.nexc32);
   dm.side = nullptr;
   dm.N = (int)t.N;
   dm.K = (int)t.K;
@@ -327,14 +329,11 @@ int check_matmul(Tensor* t, const char* name) {
 // 1 = whole-tile kernel everywhere (kept as the fallback and for tests).
 int g_kernel_mode = 0;
 
-// Waves per block of the flat kernel for a launch of `total` tiles. Every block is W waves of one tile each and
-// stays resident until its slowest wave ends. The blocks spread evenly over the CUs; a CU runs its share in rounds
-// of as many blocks as fit at once, and a round takes about max(its waves, 16) tile times (below 16 waves a CU is
-// no longer issue-bound). W minimizes the busiest CU's sum over rounds (ties: the larger W), within the kernel's
-// limits: 16 waves per block, W <= the smallest matrix's tile count (a block holds at most two tables), and the
-// LDS of a CU (160 KB: two 8 KB tables + W x 2 rings of rs rows per block). Config 2's 13,312 tiles on 256 CUs
-// give W = 13: 1024 blocks, two rounds of 26 waves per CU (W = 16 leaves a third block on 64 CUs).
-int flat_width(int total, int rs, int mintiles) {
+// Cost model of a flat launch: every block is w waves of one tile each and stays resident until its slowest wave
+// ends. The blocks spread evenly over the CUs; a CU runs its share in rounds of as many blocks as fit at once (LDS:
+// `lds` bytes per block of 160 KB; waves: 32), and a round takes about max(its waves, 16) tile times (below 16
+// waves a CU is no longer issue-bound). Returns the busiest CU's sum over rounds, in tile times.
+long long flat_cost(int total, int w, int lds) {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
@@ -342,15 +341,25 @@ int flat_width(int total, int rs, int mintiles) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
       cus = 256;
   }
+  const long long per_cu = std::max(1, std::min(160 * 1024 / lds, 32 / w));
+  const long long blocks = (total + w - 1) / w, b = (blocks + cus - 1) / cus;
+  const long long full = b / per_cu, rest = b % per_cu;
+  return full * std::max<long long>(per_cu * w, 16) + (rest ? std::max<long long>(rest * w, 16) : 0);
+}
+
+// LDS of a flat block: one or two 8 KB decode tables + w x 2 rings of rs rows + extra (spare rings)
+int flat_lds(int w, int rs, int extra) { return (w > 1 ? 2 : 1) * 8192 + w * 2 * rs * 128 + extra; }
+
+// Waves per block of the flat kernel for a launch of `total` tiles: the width of least flat_cost (ties: the larger
+// W) within the kernel's limits: 16 waves per block and W <= the smallest matrix's tile count (a block holds at most
+// two tables). Config 2's 13,312 tiles on 256 CUs give W = 13: 1024 blocks, two rounds of 26 waves per CU (W = 16
+// leaves a third block on 64 CUs).
+int flat_width(int total, int rs, int mintiles, int spare_bytes) {
   const int wmax = std::min(rs == 16 ? 16 : 8, mintiles);
   int best = 1;
   long long best_cost = -1;
   for (int w = 1; w <= wmax; ++w) {
-    const int lds = (w > 1 ? 2 : 1) * 8192 + w * 2 * rs * 128;
-    const long long per_cu = std::min(160 * 1024 / lds, 32 / w);
-    const long long blocks = (total + w - 1) / w, b = (blocks + cus - 1) / cus;
-    const long long full = b / per_cu, rest = b % per_cu;
-    const long long cost = full * std::max<long long>(per_cu * w, 16) + (rest ? std::max<long long>(rest * w, 16) : 0);
+    const long long cost = flat_cost(total, w, flat_lds(w, rs, spare_bytes));
     if (best_cost < 0 || cost <= best_cost) {
       best_cost = cost;
       best = w;
@@ -379,14 +388,64 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     plan.blocks = 0;
     return 0;
   };
-  // exception tiles (no 16-row ring schedule) ahead of the ring launches, on the same stream: those with a 32-row
-  // schedule through the flat ring kernel (m = 1) in one launch per K-quant type, the rest (and every exception
-  // tile when m > 1) through the whole-tile kernel. (A second stream overlapped them with the ring launch but its
-  // join cost more than the serial pass: these are one-wave launches over a few tiles.)
   const bool ring_ok = g_kernel_mode != 1;
+  const bool flat = ring_ok && mt == 1 && g_kernel_mode != 2;
+  // m = 1 (fp16 x): one flat launch (balanced blocks) per (K-quant type, ring size) and batch of MAX_GROUP
+  // matrices, whatever their order. In a 16-row launch, exception tiles with a 32-row schedule are decoded in place
+  // in spare rings when those fit the LDS the launch's block width assumed.
+  std::vector<char> done(count, 0), exc_in(count, 0);
+  std::vector<lw::FlatPlan> flat_plans;
+  for (int i = 0; flat && i < count; ++i) {
+    if (done[i] || !ts[i]->dm.ring_rows) continue;
+    const lw::DevMat& di = ts[i]->dm;
+    std::vector<int> sel;
+    for (int j = i; j < count && (int)sel.size() < lw::MAX_GROUP; ++j)
+      if (!done[j] && ts[j]->dm.kqt == di.kqt && ts[j]->dm.ring_rows == di.ring_rows) sel.push_back(j);
+    lw::FlatPlan fp{};
+    int total = 0, mintiles = 1 << 30, nx = 0;
+    for (int j : sel) {
+      const lw::DevMat& dm = ts[j]->dm;
+      lw::FlatEntry& e = fp.e[fp.n++];
+      e.M = dm;
+      e.X2 = static_cast<const uint32_t*>(X16[j]);
+      e.P = M.P + off[j];
+      e.list = nullptr;
+      e.tile0 = total;
+      e.ntile = dm.NT * dm.KT;
+      total += dm.NT * dm.KT;
+      mintiles = std::min(mintiles, dm.NT * dm.KT);
+      nx += dm.nexc32;
+      done[j] = 1;
+    }
+    fp.ntiles = total;
+    const int spare_ring = 2 * 16 * 128;
+    fp.W = flat_width(total, di.ring_rows, mintiles, nx && di.ring_rows == 16 ? spare_ring : 0);
+    if (nx && di.ring_rows == 16 && g_kernel_mode != 3) {
+      // spare rings per block = the most 32-row exception tiles in one block (tile list position / W)
+      std::map<int, int> per_block;
+      int most = 0;
+      for (int k = 0; k < fp.n; ++k) {
+        const lw::DevMat& dm = fp.e[k].M;
+        for (uint32_t t : ts[sel[k]]->exc32) {
+          const int u = (int)(t % dm.KT) * dm.NT + (int)(t / dm.KT);
+          most = std::max(most, ++per_block[(fp.e[k].tile0 + u) / fp.W]);
+        }
+      }
+      // in place when the spare rings cost no more than the one spare ring the width was chosen with
+      if (fp.W + most <= 32 && flat_cost(total, fp.W, flat_lds(fp.W, 16, most * spare_ring)) <=
+                                   flat_cost(total, fp.W, flat_lds(fp.W, 16, spare_ring))) {
+        fp.nspare = most;
+        for (int j : sel) exc_in[j] = 1;
+      }
+    }
+    flat_plans.push_back(fp);
+  }
+  // exception tiles not decoded in place, ahead of the ring launches on the same stream: those with a 32-row
+  // schedule through the flat kernel (m = 1) in one-wave blocks, one launch per K-quant type; the rest (and every
+  // exception tile when m > 1) through the whole-tile kernel. (A second stream overlapped them with the ring launch
+  // but its join cost more than the serial pass.)
   if (ring_ok) {
-    const bool flat = mt == 1 && g_kernel_mode != 2;
-    std::vector<char> xdone(count, 0);
+    std::vector<char> xdone(exc_in);
     for (int i = 0; flat && i < count; ++i) {
       if (xdone[i] || !ts[i]->dm.ring_rows || !ts[i]->dm.nexc32) continue;
       lw::FlatPlan fp{};
@@ -412,7 +471,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       const lw::DevMat& dm = ts[i]->dm;
       if (!dm.ring_rows || !dm.nexc) continue;
       lw::DevMat rest = dm;
-      if (flat) {  // the flat pass took the first nexc32
+      if (flat) {  // the flat launches took the first nexc32
         rest.exc = dm.exc + dm.nexc32;
         rest.nexc = dm.nexc - dm.nexc32;
       }
@@ -421,36 +480,9 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       if (launches) ++*launches;
     }
   }
-  // one grouped ring launch per (K-quant type, ring size) and batch of MAX_GROUP matrices, whatever their order;
-  // m = 1 (fp16 x): the flat kernel with balanced blocks
-  std::vector<char> done(count, 0);
-  if (ring_ok && mt == 1 && g_kernel_mode != 2) {
-    for (int i = 0; i < count; ++i) {
-      if (done[i] || !ts[i]->dm.ring_rows) continue;
-      const lw::DevMat& di = ts[i]->dm;
-      std::vector<int> sel;
-      for (int j = i; j < count && (int)sel.size() < lw::MAX_GROUP; ++j)
-        if (!done[j] && ts[j]->dm.kqt == di.kqt && ts[j]->dm.ring_rows == di.ring_rows) sel.push_back(j);
-      lw::FlatPlan fp{};
-      int total = 0, mintiles = 1 << 30;
-      for (int j : sel) {
-        const lw::DevMat& dm = ts[j]->dm;
-        lw::FlatEntry& e = fp.e[fp.n++];
-        e.M = dm;
-        e.X2 = static_cast<const uint32_t*>(X16[j]);
-        e.P = M.P + off[j];
-        e.list = nullptr;
-        e.tile0 = total;
-        e.ntile = dm.NT * dm.KT;
-        total += dm.NT * dm.KT;
-        mintiles = std::min(mintiles, dm.NT * dm.KT);
-        done[j] = 1;
-      }
-      fp.ntiles = total;
-      fp.W = flat_width(total, di.ring_rows, mintiles);
-      HIPCHECK(lw::launch_fused_flat(fp, s));
-      if (launches) ++*launches;
-    }
+  for (const lw::FlatPlan& fp : flat_plans) {
+    HIPCHECK(lw::launch_fused_flat(fp, s));
+    if (launches) ++*launches;
   }
   for (int i = 0; i < count; ++i) {
     if (done[i]) continue;
@@ -852,7 +884,7 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 2) return -1;
+  if (mode < 0 || mode > 3) return -1;
   g_kernel_mode = mode;
   return 0;
 }

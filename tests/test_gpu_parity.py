@@ -274,6 +274,59 @@ def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
         check_err(rt.test_matmul("skew", X.float().numpy(), path=0), y64, "exception tile fp32 m=3")
 
 
+def test_gpu_exception_tiles_in_place(gpu, tmp_path, orc):
+    """Two adjacent exception tiles with 32-row schedules (one block of the flat kernel): decoded in place in two
+    spare rings, alone (W = 16) and grouped with an 8-tile matrix (W = 8); the same bits as the separate one-wave
+    exception pass (mode 3) and within tolerance of fp64. m = 3 (block-per-column kernel) takes the exception pass."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from lazyweights_amd.bundle import Writer
+    from test_layout import mild_skew_codes
+    codes, side = mild_skew_codes()
+    small, small_side = bundle.synth_matrix(2, 64, 2048, 3.4, 11)
+    w = Writer(str(tmp_path))
+    w.add_kquant("mskew", 2, codes, side)
+    w.add_kquant("small", 2, small, small_side)
+    w.close()
+    with Runtime(tmp_path) as rt:
+        say("in-place exceptions: decode")
+        assert np.array_equal(rt.test_decode("mskew"), codes)
+        W64 = orc.dequant(2, codes, side)
+        Ws = orc.dequant(2, small, small_side)
+        X = torch.randn(3, 8192).half()
+        xs = torch.randn(1, 2048).half()
+        y64 = orc.gemv_f64(W64, X.double().numpy())
+        ys64 = orc.gemv_f64(Ws, xs.double().numpy())
+
+        def group(names, xs_):
+            xd = [x.cuda() for x in xs_]
+            ys = [torch.zeros(1, {"mskew": 128, "small": 64}[nm], device="cuda") for nm in names]
+            n = len(names)
+            rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                            (ctypes.c_void_p * n)(*[x.data_ptr() for x in xd]), 1,
+                                            (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+            assert rc == 0, rt.lib.lw_last_error()
+            torch.cuda.synchronize()
+            return [y.cpu().numpy() for y in ys]
+
+        runs = {}
+        for mode in (0, 3):
+            assert rt.lib.lw_set_kernel_mode(mode) == 0
+            try:
+                say("in-place exceptions: mode %d" % mode)
+                runs[mode] = group(["mskew"], [X[:1]]) + group(["small", "mskew"], [xs, X[:1]])
+            finally:
+                rt.lib.lw_set_kernel_mode(0)
+        for a, b in zip(runs[0], runs[3]):
+            assert np.array_equal(a, b)
+        check_err(runs[0][0], y64[:1], "in-place exceptions alone")
+        check_err(runs[0][1], ys64, "in-place exceptions grouped: small")
+        check_err(runs[0][2], y64[:1], "in-place exceptions grouped")
+        check_err(rt.test_matmul("mskew", X.float().numpy(), path=0), y64, "exception pass fp32 m=3")
+
+
 def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
     """The m = 1 flat kernel: one launch over matrices of different sizes (blocks spanning two matrices and two
     tile columns) gives the same bits as one call per matrix and as the block-per-column ring kernel (mode 2),

@@ -160,10 +160,14 @@ def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
     out = np.zeros((N, KS), np.uint8)
     l = np.arange(32)
     M32 = np.uint64(0xFFFFFFFF)
+    RS0 = RS
     for t in range(len(tbase)):
         tr, tc = divmod(t, KT)
         counts, meta = int(sched[2 * t]), int(sched[2 * t + 1])
-        if (meta >> 32) & 1:        # exception tile: skipped by the ring kernel
+        RS = RS0
+        if (meta >> 32) & 3 == 3:   # exception tile with a 32-row schedule
+            RS = 32
+        elif (meta >> 32) & 1:      # exception tile without a ring schedule: the whole-tile kernel's
             out[tr * 64:(tr + 1) * 64, tc * 256:(tc + 1) * 256] = syms[tr * 64:(tr + 1) * 64, tc * 256:(tc + 1) * 256]
             continue
         base1, init = meta & 255, [(meta >> 8) & 255, (meta >> 16) & 255]
@@ -248,6 +252,37 @@ def skewed_tile_codes(seed=3):
     return codes, side
 
 
+def mild_skew_codes(tiles=(5, 37), seed=3):
+    """Q5_K codes [128, 8192] (64 tiles, KT = 32) where the given tiles have every odd lane of each front replace
+    15 % of its codes with the two rarest ones: the fronts drift apart by more than a 16-row ring holds but fit a
+    32-row ring. Tiles 5 and 37 are tile rows 0 and 1 of tile column 5, adjacent in the flat kernel's order."""
+    from lazyweights_amd import bundle
+    codes, side = bundle.synth_matrix(2, 128, 8192, 3.4, seed)
+    rng = np.random.default_rng(1)
+    for t in tiles:
+        tr, tc = divmod(t, 32)
+        blk = codes[tr * 64:(tr + 1) * 64, tc * 256:(tc + 1) * 256]
+        for r in range(1, 64, 2):
+            rare = rng.random(256) < 0.15
+            blk[r] = np.where(rare, np.where(np.arange(256) % 2 == 0, 0, 31), blk[r])
+    return codes, side
+
+
+def test_ring_exception_tiles_with_32_row_schedule(lib):
+    """Mildly skewed tiles fail the 16-row check but keep a 32-row schedule (sched bits 32 and 33), listed first
+    among the exceptions; the ring emulation decodes them with 32-row rings, every window checked."""
+    from lazyweights_amd import bundle
+    codes, _ = mild_skew_codes()
+    sym = bundle.form_symbols(2, codes)
+    blob, _ = bundle.encode_huf8(sym)
+    tbase, mid, rows, words, sched, RS = build_layout(lib, blob, 128, 8192, extra=True)
+    assert RS == 16
+    flags = {t: (int(sched[2 * t + 1]) >> 32) & 3 for t in range(len(tbase)) if (int(sched[2 * t + 1]) >> 32) & 1}
+    assert flags == {5: 3, 37: 3}
+    lut = np.frombuffer(blob, np.uint16, 2048, 0)
+    assert np.array_equal(emulate_ring(lut, tbase, mid, words, sched, RS, 128, 8192, sym), sym)
+
+
 def test_ring_exception_tiles(lib):
     """A tile without a 16-row schedule is flagged and listed as an exception; every other tile keeps the ring."""
     from lazyweights_amd import bundle
@@ -258,5 +293,6 @@ def test_ring_exception_tiles(lib):
     assert RS == 16
     flagged = [t for t in range(len(tbase)) if (int(sched[2 * t + 1]) >> 32) & 1]
     assert flagged == [5]
+    assert (int(sched[2 * 5 + 1]) >> 33) & 1 == 0  # no 32-row schedule either
     lut = np.frombuffer(blob, np.uint16, 2048, 0)
     assert np.array_equal(emulate_ring(lut, tbase, mid, words, sched, RS, 128, 8192, sym), sym)
