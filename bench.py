@@ -10,8 +10,9 @@ seven GEMVs launched back to back (grouped per layer). value = algorithmic coded
 the algorithmic bytes of a GEMV are blob + side tensor + 2 K (x) + 4 m N (y) (the reference's own size
 accounting; device-layout padding is not credited).
 
-roofline: the dominant kernel (k_fused_ring, one grouped launch per layer) timed with HIP events around each layer's
-launch on its stream; achieved = the layer's algorithmic bytes / mean launch duration, peak = 8 TB/s. traffic = HBM
+roofline: the dominant kernel (k_fused_flat, one grouped launch per layer that also sums the tile-column partials)
+timed with HIP events around each layer's launches on their stream; achieved = the layer's algorithmic bytes / mean
+duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view). traffic = HBM
 bytes per layer launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --profile`,
 each scaled by what the counter reads for the 256 MiB device copy that --profile also runs (null when rocprofv3 is
 unavailable or a pass fails). cpu_baseline: the oracle's restatement of the reference CPU path (cpu_decode,
@@ -158,6 +159,14 @@ def main():
                 if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, m, yy, stream) != 0:
                     raise RuntimeError(lib.lw_last_error().decode())
 
+        singles = [((ctypes.c_char_p * 1)(names[i]), (ctypes.c_void_p * 1)(xp[i]), (ctypes.c_void_p * 1)(yp[i]))
+                   for i in range(n)]
+
+        def serial_step():
+            for nm, xx, yy in singles:
+                if lib.lw_group_matmul_dev(rt.h, 1, nm, xx, m, yy, stream) != 0:
+                    raise RuntimeError(lib.lw_last_error().decode())
+
         if a.profile:
             for _ in range(max(1, a.steps)):
                 step()
@@ -179,6 +188,15 @@ def main():
         ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
         value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
         log("bench: %.3f ms per step (%d GEMVs), %.1f GB/s coded" % (ms_per_step, n, value))
+        serial_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            serial_step()
+        torch.cuda.synchronize()
+        serial_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+        log("bench: serial per-matrix launches %.3f ms per step, %.1f GB/s coded"
+            % (serial_ms, bytes_per_step / (serial_ms * 1e-3) / 1e9))
 
         # dominant kernel: HIP events around each fused launch, on the library's stream
         sizes = (ctypes.c_int * a.layers)(*([7] * a.layers))
@@ -224,10 +242,20 @@ def main():
                 t_cpu += time.perf_counter() - t0
                 reps += 1
             cpu_gbs = sample_bytes * reps / t_cpu / 1e9
+            # the reference's own CPU setting (6 threads, results/a2_orin/decode7), a shorter sample
+            reps6, t6 = 0, 0.0
+            while t6 < a.cpu_seconds / 2 and reps6 < 1000:
+                t0 = time.perf_counter()
+                for (b, s, N, K), x in zip(blobs, xs):
+                    orc.decode_gemv(1, b, s, N, K, x, min(6, threads))
+                t6 += time.perf_counter() - t0
+                reps6 += 1
             cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                    "sample": "layer 0 of the workload (7 matrices, %.1f MB coded), %d passes, %.1f s; "
-                             "oracle cpu_decode + dequant + fp32 GEMV" % (sample_bytes / 1e6, reps, t_cpu)}
-            log("bench: cpu baseline %.2f GB/s on %d threads" % (cpu_gbs, threads))
+                             "oracle cpu_decode + dequant + fp32 GEMV" % (sample_bytes / 1e6, reps, t_cpu),
+                   "value_6_threads": round(sample_bytes * reps6 / t6 / 1e9, 3)}
+            log("bench: cpu baseline %.2f GB/s on %d threads, %.2f GB/s on %d"
+                % (cpu_gbs, threads, cpu["value_6_threads"], min(6, threads)))
 
         res = {
             "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,
@@ -242,6 +270,8 @@ def main():
                          "traffic": traffic["bytes_per_layer_launch"] if traffic else None,
                          "traffic_detail": traffic, "kernel": "k_fused_flat", "launch": "one grouped launch per layer",
                          "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
+            "serial_per_matrix": {"ms_per_step": round(serial_ms, 4),
+                                  "GBps": round(bytes_per_step / (serial_ms * 1e-3) / 1e9, 1)},
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
         }

@@ -61,6 +61,10 @@ struct FlatEntry {
   float* P;
   const uint32_t* list;  // null: the matrix's tiles in column-major order; else these tile indices (exception pass)
   int tile0, ntile;
+  // Y non-null (the launch decodes every tile of the matrix): Y[n] = the ordered sum of P over tile columns, formed
+  // in the launch by the last wave of each tile row; cnt = NT zeroed counters (left zeroed)
+  float* Y;
+  uint32_t* cnt;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];

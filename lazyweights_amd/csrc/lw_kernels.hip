@@ -385,7 +385,7 @@ struct XgRegs {
 // One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring,
 // `xgf(sub, j)` = sum of token j's x over sub-block `sub` of the tile column, `lutsel` = byte offset of the tile's
 // decode table within `lut4` (0 or 8192, OR-ed into the index).
-template <int KQ, int MT, class Stager, class Xg>
+template <int KQ, int MT, bool COH = false, class Stager, class Xg>
 __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint32_t lutsel, const uint32_t* xs,
                                           const Xg& xgf, __attribute__((address_space(4))) const uint32_t* xcol,
                                           const uint8_t* srow, uint32_t P, uint32_t rlb, int mt, int N, float* out) {
@@ -510,7 +510,12 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
   }
 #pragma unroll
   for (int j = 0; j < MT; ++j)
-    if (j < mt) out[(size_t)j * N] = tot[j];
+    if (j < mt) {
+      if (COH)  // coherent across the device's caches, for a reduction inside the launch
+        __hip_atomic_store(out + (size_t)j * N, tot[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        out[(size_t)j * N] = tot[j];
+    }
 }
 
 
@@ -629,7 +634,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.counts = sc.x;
     st.rmask = rmask;
     st.init((int)init0);
-    ring_tile<KQ, 1>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+    ring_tile<KQ, 1, true>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
   } else {
     RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
@@ -637,8 +642,30 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.counts = f ? sc.y : sc.x;
     st.rmask = rmask;
     st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, 1>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+    ring_tile<KQ, 1, true>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
   }
+  if (!E.Y) return;
+  // Reduction in the launch: the wave's partials (device-coherent stores) are complete before it counts its tile
+  // in its tile row; the wave that counts the row's last tile resets the counter and sums the row's partials in
+  // tile-column order (the order of k_reduce_group, so the bits are the same) with device-coherent loads.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readlane(old, 0);
+  if (old != (uint32_t)(KT - 1)) return;
+  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
+  float a = 0.f;
+  for (int c0 = 0; c0 < KT; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c0 + c < KT) a += v[c];
+  }
+  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
 }
 
 // The tiles of the plan's matrices form one list (matrix by matrix, each column-major: tile rows of one tile

@@ -110,6 +110,8 @@ struct Model {
   // device scratch, grown on demand
   float* P = nullptr;
   size_t P_cap = 0;
+  uint32_t* cnt = nullptr;  // tile-row counters of the in-launch reduction, zeroed (every launch leaves them zeroed)
+  size_t cnt_cap = 0;
   uint16_t* X16 = nullptr;
   size_t X16_cap = 0;
   uint8_t* codes = nullptr;
@@ -134,6 +136,15 @@ int grow(T*& p, size_t& cap, size_t bytes) {
   cap = 0;
   HIPCHECK(hipMalloc(reinterpret_cast<void**>(&p), bytes));
   cap = bytes;
+  return 0;
+}
+
+// as grow, zero-filled when (re)allocated
+template <class T>
+int grow_zeroed(T*& p, size_t& cap, size_t bytes) {
+  if (bytes <= cap) return 0;
+  if (grow(p, cap, bytes)) return -1;
+  HIPCHECK(hipMemset(p, 0, cap));
   return 0;
 }
 
@@ -299,6 +310,7 @@ void release(Model* M) {
     if (t.dside) (void)hipFree(t.dside);
   }
   if (M->P) (void)hipFree(M->P);
+  if (M->cnt) (void)hipFree(M->cnt);
   if (M->X16) (void)hipFree(M->X16);
   if (M->codes) (void)hipFree(M->codes);
   if (M->stream) (void)hipStreamDestroy(M->stream);
@@ -352,8 +364,8 @@ int flat_lds(int w, int rs, int extra) { return (w > 1 ? 2 : 1) * 8192 + w * 2 *
 
 // Waves per block of the flat kernel for a launch of `total` tiles: the width of least flat_cost (ties: the larger
 // W) within the kernel's limits: 16 waves per block and W <= the smallest matrix's tile count (a block holds at most
-// two tables). Config 2's 13,312 tiles on 256 CUs give W = 13: 1024 blocks, two rounds of 26 waves per CU (W = 16
-// leaves a third block on 64 CUs).
+// two tables). Config 2's 6656 tiles on 256 CUs give W = 13: 512 blocks, one round of 26 waves on every CU (W = 16
+// leaves 96 CUs with one block of 16 waves and 160 with two).
 int flat_width(int total, int rs, int mintiles, int spare_bytes) {
   const int wmax = std::min(rs == 16 ? 16 : 8, mintiles);
   int best = 1;
@@ -370,15 +382,20 @@ int flat_width(int total, int rs, int mintiles, int spare_bytes) {
 
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
-// others into whole-tile launches; then one ordered reduction per MAX_GROUP matrices. Partials of all matrices
-// live side by side in the model's P scratch.
-// `launches` (optional) counts the decode launches; reduce = false leaves the partials in M.P (kernel timing)
+// others into whole-tile launches. The ordered reduction over tile columns runs inside the flat (m = 1) launch for
+// every matrix that launch decodes completely, else in one reduction launch per MAX_GROUP matrices. Partials of
+// all matrices live side by side in the model's P scratch; calls that overlap on one model race (P and counters).
+// `launches` (optional) counts the kernel launches.
 int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
-                    const int* ldy, hipStream_t s, int* launches = nullptr, bool reduce = true) {
+                    const int* ldy, hipStream_t s, int* launches = nullptr) {
   const int mt = m * per;
   std::vector<size_t> off(count + 1, 0);
   for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
   if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
+  std::vector<size_t> coff(count + 1, 0);  // tile-row counters per entry (in-launch reduction)
+  for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + (size_t)ts[i]->dm.NT;
+  if (grow_zeroed(M.cnt, M.cnt_cap, coff[count] * sizeof(uint32_t))) return -1;
+  std::vector<char> reduced(count, 0);  // entries whose reduction runs inside their flat launch
   lw::GroupPlan plan{};
   plan.mt = mt;
   auto flush = [&]() -> int {
@@ -437,6 +454,15 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         fp.nspare = most;
         for (int j : sel) exc_in[j] = 1;
       }
+    }
+    // the launch decodes every tile of a matrix without exceptions or with all of them in place: it also reduces
+    for (int k = 0; k < fp.n; ++k) {
+      const int j = sel[k];
+      const lw::DevMat& dm = ts[j]->dm;
+      if (dm.nexc && !(exc_in[j] && dm.nexc == dm.nexc32)) continue;
+      fp.e[k].Y = Y[j];
+      fp.e[k].cnt = M.cnt + coff[j];
+      reduced[j] = 1;
     }
     flat_plans.push_back(fp);
   }
@@ -508,12 +534,12 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     if (flush()) return -1;
   }
-  if (!reduce) return 0;
   // ordered reduction over tile columns, up to MAX_GROUP matrices per launch
   lw::ReducePlan rp{};
   rp.m = m;
   rp.per = per;
   for (int i = 0; i < count; ++i) {
+    if (reduced[i]) continue;
     lw::ReduceEntry& e = rp.e[rp.n++];
     e.P = M.P + off[i];
     e.Y = Y[i];
@@ -522,11 +548,16 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     e.ldy = ldy[i];
     e.out0 = rp.total;
     rp.total += m * (int)ts[i]->N;
-    if (rp.n == lw::MAX_GROUP || i + 1 == count) {
+    if (rp.n == lw::MAX_GROUP) {
       HIPCHECK(lw::launch_reduce_group(rp, s));
+      if (launches) ++*launches;
       rp.n = 0;
       rp.total = 0;
     }
+  }
+  if (rp.n) {
+    HIPCHECK(lw::launch_reduce_group(rp, s));
+    if (launches) ++*launches;
   }
   return 0;
 }
@@ -914,7 +945,7 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
   HIPCHECK(hipEventSynchronize(b));
   float ms = 0;
   HIPCHECK(hipEventElapsedTime(&ms, a, b));
-  // fused kernels alone: events around each group's fused launch(es), reductions excluded
+  // the layer's launches alone: events around each group's launches (decode, reduction), host work excluded
   std::vector<hipEvent_t> ev(2 * (size_t)ngroups);
   for (auto& e : ev) HIPCHECK(hipEventCreate(&e));
   double kms = 0;
@@ -935,8 +966,7 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
       for (int i = first[g]; i < first[g + 1]; ++i) ts.push_back(M->find(names[i]));
       HIPCHECK(hipEventRecord(ev[2 * g], s));
       int nl = 0;
-      if (fused_group_dev(*M, ts.data(), X + first[g], sizes[g], m, 1, Y + first[g], ldys.data() + first[g], s, &nl,
-                          false))
+      if (fused_group_dev(*M, ts.data(), X + first[g], sizes[g], m, 1, Y + first[g], ldys.data() + first[g], s, &nl))
         return -1;
       if (it == 0) launches += nl;
       HIPCHECK(hipEventRecord(ev[2 * g + 1], s));
