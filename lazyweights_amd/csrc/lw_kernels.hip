@@ -26,6 +26,17 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 // leading zero bits of every device lane stream (lw_layout.h GUARD)
 constexpr int GUARD_BITS = 2;
 
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Activations of MT pseudo-tokens staged in LDS as fp16 pairs: pair c (weights 2c, 2c + 1) of token j. With
+// MT >= 4 (the MFMA path) the two pairs of one 4-weight step are adjacent per token, so a lane reads its token's
+// four weights with one 8-byte load.
+template <int MT>
+__device__ __forceinline__ int xs_index(int c, int j) {
+  return MT >= 4 ? ((c >> 1) * MT + j) * 2 + (c & 1) : c * MT + j;
+}
+
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, a), __builtin_bit_cast(h2v, b), c, false);
 }
@@ -413,6 +424,17 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
   float tot[MT], acc[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) tot[j] = acc[j] = 0.f;
+  // MT >= 4: the products go to the matrix cores. v_mfma_f32_4x4x4f16 computes, per block of 4 lanes, D[i][j] =
+  // sum_k A[lane 4b + i][k] B[lane 4b + j][k] into lane 4b + j, register i. With A = the four x values of token
+  // 4q + i (lane 4b + i reads token i) and B = the lane's own four weights, lane 4b + j gets its own row's dot
+  // products for tokens 4q .. 4q + 3, as acc[4q + i] does on the dot2 path.
+  constexpr bool MMA = MT >= 4;
+  constexpr int NQ = MMA ? MT / 4 : 1;
+  f4v accm[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) accm[q] = f4v{0.f, 0.f, 0.f, 0.f};
+  const uint32_t ltok = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 3u;
+  uint32_t wprev = 0;
 
 #pragma unroll 1
   for (int sb = 0; sb < NSB; ++sb) {
@@ -421,21 +443,25 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
     float dA, dB;
     uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K / IQ4_XS), consumed low byte first
     side_packed<KQ>(sw, scq, scq2, dA, dB);
-    // per super-block x terms: Q4_K / Q5_K mins sum_j m_j (sum x)_j; IQ4_XS bias sum_j s_j (sum x)_j
-    float msum[MT], tsum[MT], csum[MT];
+    // per super-block x terms, applied first: y -= dmin sum_j m_j (sum x)_j (Q4_K / Q5_K mins) or
+    // 128 d sum_j s_j (sum x)_j (the IQ4_XS +128 grid bias); y += d sum_j sc_j (x . q)_j follows at the end
+    float tsum[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
-      msum[j] = tsum[j] = csum[j] = 0.f;
+      tsum[j] = 0.f;
       if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
-        float mf[8];
+        float mf[8], msum = 0.f;
         side_mins(sw, mf);
 #pragma unroll
-        for (int jj = 0; jj < NSUB; ++jj) msum[j] = fmaf(mf[jj], xgf(sb, jj, j), msum[j]);
+        for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xgf(sb, jj, j), msum);
+        tot[j] = fmaf(-dB, msum, tot[j]);
       }
       if (KQ == KQ_IQ4_XS) {
+        float csum = 0.f;
 #pragma unroll
         for (int jj = 0; jj < NSUB; ++jj)
-          csum[j] = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgf(sb, jj, j), csum[j]);
+          csum = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgf(sb, jj, j), csum);
+        tot[j] = fmaf(-128.f * dA, csum, tot[j]);
       }
     }
 #pragma unroll 1
@@ -451,7 +477,7 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
         if (g == 12) __builtin_amdgcn_s_setprio(0);
         st.stage(g);
         // m = 1 unrolls the group fully; more tokens unroll less (their x operands come from LDS per pair)
-#pragma unroll MT == 1 ? 8 : 2
+#pragma unroll MT == 1 ? 8 : (MMA && SYMB == 4 ? 1 : 2)
         for (int p = 0; p < 8; ++p) {
           const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
           const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
@@ -471,6 +497,13 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
             const int c = 16 * g + 2 * p;
             if (XS_SGPR) {
               acc[0] = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc[0]));
+            } else if (MMA) {
+              const h4v wv = __builtin_bit_cast(h4v, make_uint2(v1, v2));
+#pragma unroll
+              for (int q = 0; q < NQ; ++q) {
+                const uint2 xv = *reinterpret_cast<const uint2*>(xs + xs_index<MT>(c, 4 * q + (int)ltok));
+                accm[q] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4v, xv), wv, accm[q], 0, 0, 0);
+              }
             } else {
               const uint32_t* x1 = xs + c * MT;
 #pragma unroll
@@ -481,6 +514,17 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
             const int c = 8 * g + p;
             if (XS_SGPR) {
               acc[0] = dot2(w, xcol[c], acc[0]);
+            } else if (MMA) {  // one 4-weight product per two pairs (c odd: pairs c - 1, c)
+              if (p & 1) {
+                const h4v wv = __builtin_bit_cast(h4v, make_uint2(wprev, w));
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                  const uint2 xv = *reinterpret_cast<const uint2*>(xs + xs_index<MT>(c - 1, 4 * q + (int)ltok));
+                  accm[q] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4v, xv), wv, accm[q], 0, 0, 0);
+                }
+              } else {
+                wprev = w;
+              }
             } else {
               const uint32_t* x1 = xs + c * MT;
 #pragma unroll
@@ -492,21 +536,26 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
           const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
                                                                : (float)(uint32_t)(scq & 255u);
           scq >>= 8;
+          if (MMA) {
 #pragma unroll
-          for (int j = 0; j < MT; ++j) {
-            tsum[j] = fmaf(scv, acc[j], tsum[j]);
-            acc[j] = 0.f;
+            for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) tsum[4 * q + i] = fmaf(scv, accm[q][i], tsum[4 * q + i]);
+              accm[q] = f4v{0.f, 0.f, 0.f, 0.f};
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+              tsum[j] = fmaf(scv, acc[j], tsum[j]);
+              acc[j] = 0.f;
+            }
           }
         }
       }
     }
-    // super-block: y += d sum_j sc_j (x . q)_j - dmin sum_j m_j (sum x)_j  (IQ4_XS: minus the +128 grid bias)
+    // super-block end: y += d sum_j sc_j (x . q)_j
 #pragma unroll
-    for (int j = 0; j < MT; ++j) {
-      tot[j] = fmaf(dA * VSCALE, tsum[j], tot[j]);
-      if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot[j] = fmaf(-dB, msum[j], tot[j]);
-      if (KQ == KQ_IQ4_XS) tot[j] = fmaf(-128.f * dA, csum[j], tot[j]);
-    }
+    for (int j = 0; j < MT; ++j) tot[j] = fmaf(dA * VSCALE, tsum[j], tot[j]);
   }
 #pragma unroll
   for (int j = 0; j < MT; ++j)
@@ -556,12 +605,12 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
   for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
     const int j = i / NPAIR, c = i - j * NPAIR;
-    xs[c * MT + j] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
+    xs[xs_index<MT>(c, j)] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
     const int g = i / MT, j = i - g * MT;
-    xg[g * MT + j] = xsum_sub<GW>([&](int c) { return xs[(g * (GW / 2) + c) * MT + j]; });
+    xg[g * MT + j] = xsum_sub<GW>([&](int c) { return xs[xs_index<MT>(g * (GW / 2) + c, j)]; });
   }
   __syncthreads();
   if (tr >= NT) return;
