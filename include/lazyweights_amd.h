@@ -89,13 +89,15 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 /* Fused-kernel selection for all handles: 0 (default) = the ring-staged kernels wherever a matrix has a ring
  * schedule (the flat, load-balanced kernel for m = 1; the block-per-column kernel otherwise); 1 = the whole-tile
  * kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m; 3 = as 0, but exception
- * tiles are never decoded inside the flat launch (always by the separate exception pass). Returns 0 or -1. */
+ * tiles are never decoded inside the flat launch (always by the separate exception pass); 4 = as 0, with the
+ * low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 0, never the low-latency kernel.
+ * Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in
  * names/X/Y (group g has sizes[g] matrices), cycling through the groups, with HIP events on the launch stream.
- * out[0] = mean ms per pass over all groups, out[1] = mean ms per fused-kernel launch set (decode + GEMV kernels
- * only, events around each group's fused launches), out[2] = number of fused launches per pass. */
+ * out[0] = mean ms per pass over all groups, out[1] = mean ms per pass of the groups' kernels alone (events around
+ * each group's launches: decode + GEMV and reduction), out[2] = number of kernel launches per pass. */
 int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* names, const void* const* X, int m,
                     float* const* Y, int warmup, int iters, double* out);
 
@@ -119,12 +121,13 @@ int lw_write_bundle(const char* dir, int count, const char* const* names, const 
 int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L);
 
 /* The device layout this library builds from a blob at load time (host-side, for inspection and tests): fills tbase
- * [T], mid [T * 32], rows [T], sched [2 T] (ring staging schedule), *ring_rows and, when words_cap is large enough,
- * words; returns the word count (-1 on a bad or corrupt blob). Any output pointer may be NULL. pre_il / compact
- * select the reference's pre-interleaved export formats (_il / _ilc). */
+ * [T], mid [T * 32], split [T * 8 * 32] (bit offsets of symbols 64 k per lane, the low-latency kernel's chain
+ * starts), rows [T], sched [2 T] (ring staging schedule), *ring_rows and, when words_cap is large enough, words;
+ * returns the word count (-1 on a bad or corrupt blob). Any output pointer may be NULL. pre_il / compact select the
+ * reference's pre-interleaved export formats (_il / _ilc). */
 long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,
-                          uint16_t* mid, uint16_t* rows, uint64_t* sched, int* ring_rows, uint32_t* words,
-                          long long words_cap);
+                          uint16_t* mid, uint16_t* split, uint16_t* rows, uint64_t* sched, int* ring_rows,
+                          uint32_t* words, long long words_cap);
 
 #ifdef __cplusplus
 }

@@ -40,7 +40,7 @@ SIGNATURES = {
     "lw_encode": (_ll, [_vp, _i, _i, _vp, _ll, _c.POINTER(_u64)]),
     "lw_write_bundle": (_i, [_cp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
     "lw_huffman_lengths": (_i, [_vp, _i, _i, _vp]),
-    "lw_build_layout": (_ll, [_vp, _ll, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _ll]),
+    "lw_build_layout": (_ll, [_vp, _ll, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll]),
     "lw_set_kernel_mode": (_i, [_i]),
 }
 

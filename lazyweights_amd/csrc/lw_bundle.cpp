@@ -111,8 +111,8 @@ int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L) {
 }
 
 long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,
-                          uint16_t* mid, uint16_t* rows, uint64_t* sched, int* ring_rows, uint32_t* words,
-                          long long words_cap) {
+                          uint16_t* mid, uint16_t* split, uint16_t* rows, uint64_t* sched, int* ring_rows,
+                          uint32_t* words, long long words_cap) {
   if (!blob || len <= 0) return -1;
   lw::Layout L;
   std::string err;
@@ -122,6 +122,7 @@ long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int
   const size_t T = L.tbase.size();
   if (tbase) memcpy(tbase, L.tbase.data(), 4 * T);
   if (mid) memcpy(mid, L.mid.data(), 2 * L.mid.size());
+  if (split) memcpy(split, L.split.data(), 2 * L.split.size());
   if (rows) memcpy(rows, L.rows.data(), 2 * T);
   if (sched) memcpy(sched, L.sched.data(), 16 * T);
   if (ring_rows) *ring_rows = L.ring_rows;

@@ -20,6 +20,7 @@ struct DevMat {
   const uint32_t* lut4;  // the ring kernels' 4-byte table entries (decode_table4 in lw_layout.h); null if kqt == 0
   const uint32_t* tbase;
   const uint16_t* mid;
+  const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency kernel (Layout::split)
   const uint16_t* rows;
   const uint32_t* words;
   const uint8_t* side;
@@ -76,6 +77,11 @@ struct FlatPlan {
   int nspare;
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
+// The low-latency kernel over the same kind of plan (one tile per block of 4 waves, 8 chains per lane; W and
+// nspare are ignored; exception tiles included). Every matrix needs a K-quant table and the split offsets.
+hipError_t launch_fused_split(const FlatPlan& plan, hipStream_t s);
+// LDS rows the low-latency kernel stages per tile for this plan (max over its matrices of max_rows + 2)
+int split_stage_rows(const FlatPlan& plan);
 
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
 // K-quant types or ring sizes, or a matrix has no ring schedule).

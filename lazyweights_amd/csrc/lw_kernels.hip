@@ -653,6 +653,63 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
   }
 }
 
+// ── flat launches (m = 1): shared pieces ─────────────────────────────────────────────────────────────────
+// Reduction in the launch, after a wave stored its tile's 64 partials with device-coherent stores: they are complete
+// before the wave counts its tile in its tile row; the wave that counts the row's last tile resets the counter and
+// sums the row's partials in tile-column order (the order of k_reduce_group, so the bits are the same) with
+// device-coherent loads. No-op when the entry has no Y (the partials are reduced by a separate launch).
+template <class KEntryRef>
+__device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane) {
+  if (!E.Y) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readlane(old, 0);
+  if (old != (uint32_t)(KT - 1)) return;
+  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
+  float a = 0.f;
+  for (int c0 = 0; c0 < KT; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c0 + c < KT) a += v[c];
+  }
+  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
+}
+
+// One tile column's x sums per sub-block (m = 1), as wave-uniform values: lane 4 g + k sums quarter k of sub-block
+// g; two exchanges give (q0 + q1) + (q2 + q3), the order of xsum_sub (so all kernels give the same bits).
+template <int KQ>
+__device__ __forceinline__ XgRegs column_xsums(const uint32_t* X2, int tc, int lane) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ);
+  XgRegs xgr;
+  if (KQ != KQ_Q6_K) {
+    constexpr int NSUBT = TW / GW, Q = GW / 8;  // sub-blocks per tile column, pairs per quarter
+    float a = 0.f;
+    if (lane < 4 * NSUBT) {
+      const uint32_t* xl = X2 + (size_t)tc * (TW / 2) + (uint32_t)(lane * Q);
+      for (int c = 0; c < Q; ++c) {
+        const uint32_t v = xl[c];
+        a += h2f(v) + h2f(v >> 16);
+      }
+    }
+    a += __shfl_xor(a, 1);
+    a += __shfl_xor(a, 2);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      xgr.x0[g] = g < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * g)) : 0.f;
+      xgr.x1[g] = g + 8 < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * (g + 8))) : 0.f;
+    }
+  }
+  return xgr;
+}
+
 // ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
 // One tile of the flat kernel: lanes of front f stage into `ring` (RS rows of 32 words).
 template <int KQ, class KEntryRef>
@@ -693,28 +750,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.init((int)(f ? init1 : init0));
     ring_tile<KQ, 1, true>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
   }
-  if (!E.Y) return;
-  // Reduction in the launch: the wave's partials (device-coherent stores) are complete before it counts its tile
-  // in its tile row; the wave that counts the row's last tile resets the counter and sums the row's partials in
-  // tile-column order (the order of k_reduce_group, so the bits are the same) with device-coherent loads.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  uint32_t old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  old = __builtin_amdgcn_readlane(old, 0);
-  if (old != (uint32_t)(KT - 1)) return;
-  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
-  float a = 0.f;
-  for (int c0 = 0; c0 < KT; c0 += 16) {
-    float v[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c0 + c < KT) a += v[c];
-  }
-  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
+  row_reduce(E, tr, KT, N, lane);
 }
 
 // The tiles of the plan's matrices form one list (matrix by matrix, each column-major: tile rows of one tile
@@ -784,27 +820,7 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
     if (spare >= plan.nspare) return;  // cannot happen with the host's sizing; never overrun the spare rings
   }
 
-  // this column's x sums per sub-block: lane 4 g + k sums quarter k of sub-block g; two exchanges give
-  // (q0 + q1) + (q2 + q3), the order of xsum_sub (so all kernels give the same bits)
-  XgRegs xgr;
-  if (KQ != KQ_Q6_K) {
-    constexpr int NSUBT = TW / GW, Q = GW / 8;  // sub-blocks per tile column, pairs per quarter
-    float a = 0.f;
-    if (lane < 4 * NSUBT) {
-      const uint32_t* xl = E.X2 + (size_t)tc * (TW / 2) + (uint32_t)(lane * Q);
-      for (int c = 0; c < Q; ++c) {
-        const uint32_t v = xl[c];
-        a += h2f(v) + h2f(v >> 16);
-      }
-    }
-    a += __shfl_xor(a, 1);
-    a += __shfl_xor(a, 2);
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-      xgr.x0[g] = g < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * g)) : 0.f;
-      xgr.x1[g] = g + 8 < NSUBT ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * (g + 8))) : 0.f;
-    }
-  }
+  const XgRegs xgr = column_xsums<KQ>(E.X2, tc, lane);
 
   // the ring of the lane's front: 16-row launches place a 32-row exception tile's front 0 in the wave's two rings
   // and its front 1 in spare ring pair `spare`
@@ -812,6 +828,190 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   const bool x32 = RS == 16 && spare >= 0;
   uint32_t* ring = rings + (x32 ? (f ? 2 * W + 2 * spare : 2 * wave) : 2 * wave + f) * RING_WORDS;
   flat_tile<KQ>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane);
+}
+
+// ── low-latency kernel (m = 1): one tile per block, 8 chains per lane ───────────────────────────────────
+// A launch of few tiles per CU takes about one tile's decode time, whatever its size: the chain of 128 dependent
+// symbol pairs per lane front. Here a block of 4 waves stages its whole tile in LDS and splits every lane stream
+// into 8 chains of 64 symbols at load-time offsets (Layout::split): wave w decodes symbols [64 w, 64 w + 64) of
+// both rows of every lane (lanes 0-31 row l, lanes 32-63 row l + 32, the same x columns), with the ring kernel's
+// register window reading the tile image directly. Each chain stores its sub-block dot products in LDS; wave 0
+// then forms each row's partial exactly as ring_tile does (same operations in the same order), so the result has
+// the same bits as the ring kernels'. Exception tiles need nothing special: no staging schedule is involved.
+template <int KQ>
+__global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_rows) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr int NSUBT = TW / GW;                  // sub-blocks per tile row
+  constexpr int NSB = TW / 256;                   // super-blocks per tile row
+  constexpr int NSUB = 256 / GW;                  // sub-blocks per super-block
+  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
+  constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  // one static LDS object, so the table sits at LDS address 0 (table_addr ORs its base into the index bits)
+  __shared__ uint32_t lds_static[LUTN + TN * NSUBT];
+  uint32_t* lut4 = lds_static;
+  float* accb = reinterpret_cast<float*>(lds_static + LUTN);  // [row][sub-block] dot products of the chains
+  extern __shared__ __align__(16) uint32_t tw[];              // the tile's word rows [stage_rows][32]
+
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int T = (int)blockIdx.x;
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < plan.n && T >= plan.e[i].tile0) mi = i;
+  KEntry* ep = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mi * sizeof(FlatEntry));
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const int KT = M.KT, NT = M.NT, N = M.N;
+  const int u = T - E.tile0;
+  const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;
+  const int tc = t % KT, tr = t / KT;
+  const int R = min((int)M.rows[t] + 2, stage_rows);  // rows read: up to 2 past the longest lane's last row
+  for (int i = threadIdx.x; i < LUTN / 4; i += 256) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
+  const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
+  for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
+  __syncthreads();
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  // wave 0 forms the row partials after the decode: its side records and x sums are fetched first, so their
+  // latency hides behind the decode
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+  uint32_t sw[NSB][5];
+  XgRegs xgr;
+  if (wave == 0) {
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+    xgr = column_xsums<KQ>(E.X2, tc, lane);
+  }
+  {
+    // chain of lane front f: symbols [64 wave, 64 wave + 64) of row l + 32 f, i.e. stream symbols 256 f + 64 wave..
+    const int k = 4 * f + wave;
+    uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+    const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
+    uint32_t tmask = 0x1FFCu;
+    asm volatile("" : "+v"(tmask));
+    uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
+    asm volatile("" : "+v"(rlb));
+    KU32* xcol = (KU32*)(E.X2 + (size_t)tc * (TW / 2));
+    uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
+    uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
+    uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
+    uint32_t C = *(LdsU32*)(rlb + (slot << 7));
+    float* accrow = accb + (f * 32 + l) * NSUBT;
+    float acc = 0.f;
+#pragma unroll 1
+    for (int gi = 0; gi < 4; ++gi) {
+      const int g = 4 * wave + gi;  // 16-symbol group within the row
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
+        const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
+        const uint32_t w2 = w1 >> (e1 & 31u);
+        const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
+        P = P + e1 + e2;
+        const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, 8);
+        const bool slide = nslot != slot;
+        A = slide ? B : A;
+        B = slide ? C : B;
+        slot = nslot;
+        C = *(LdsU32*)(rlb + (nslot << 7));
+        if (SYMB == 4) {
+          const uint32_t v1 = __builtin_amdgcn_perm(e1, e1, 0x0C030C02u), v2 = __builtin_amdgcn_perm(e2, e2, 0x0C030C02u);
+          const int c = 16 * g + 2 * p;
+          acc = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc));
+        } else {
+          const uint32_t w = __builtin_amdgcn_perm(e2, e1, 0x07060302u);
+          acc = dot2(w, xcol[8 * g + p], acc);
+        }
+      }
+      if (GPSUB == 1 || (gi & 1)) {
+        accrow[g / GPSUB] = acc;
+        acc = 0.f;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+
+  // row partials, as ring_tile forms them: per super-block the min / bias term first, then d x the scaled sum of
+  // the sub-block dot products in order
+  const float* accrow = accb + lane * NSUBT;
+  float tot = 0.f;
+#pragma unroll
+  for (int sb = 0; sb < NSB; ++sb) {
+    float dA, dB;
+    uint64_t scq, scq2;
+    side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+    if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
+      float mf[8], msum = 0.f;
+      side_mins(sw[sb], mf);
+#pragma unroll
+      for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xgr(sb, jj, 0), msum);
+      tot = fmaf(-dB, msum, tot);
+    }
+    if (KQ == KQ_IQ4_XS) {
+      float csum = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < NSUB; ++jj) csum = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgr(sb, jj, 0), csum);
+      tot = fmaf(-128.f * dA, csum, tot);
+    }
+    float tsum = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < NSUB; ++jj) {
+      if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+      const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                           : (float)(uint32_t)(scq & 255u);
+      scq >>= 8;
+      tsum = fmaf(scv, accrow[sb * NSUB + jj], tsum);
+    }
+    tot = fmaf(dA * VSCALE, tsum, tot);
+  }
+  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
+  __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  row_reduce(E, tr, KT, N, lane);
+}
+
+template <int KQ>
+static hipError_t split_launch(const FlatPlan& p, int stage_rows, hipStream_t s) {
+  const size_t smem = (size_t)stage_rows * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_split<KQ>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_fused_split<KQ>, dim3(p.ntiles), dim3(256), smem, s, p, stage_rows);
+  return hipGetLastError();
+}
+
+int split_stage_rows(const FlatPlan& p) {
+  int r = 0;
+  for (int i = 0; i < p.n; ++i) r = std::max(r, p.e[i].M.max_rows + 2);
+  return r;
+}
+
+hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.ntiles < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || e.tile0 + e.ntile != end || e.ntile < 1 ||
+        (!e.list && e.ntile != e.M.NT * e.M.KT) || (i == 0 && e.tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  const int rows = split_stage_rows(p);
+  if (rows > 256 || rows * 128 + 4 * LUTN + TN * 16 * 4 > 160 * 1024) return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return split_launch<KQ_Q4_K>(p, rows, s);
+    case KQ_Q5_K: return split_launch<KQ_Q5_K>(p, rows, s);
+    case KQ_Q6_K: return split_launch<KQ_Q6_K>(p, rows, s);
+    case KQ_IQ4_XS: return split_launch<KQ_IQ4_XS>(p, rows, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int KQ, int RS, int NTAB>

@@ -119,6 +119,7 @@ template <class B, class Lim, class Check>
 bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check check_end,
                    std::vector<uint64_t>& lane_bits) {
   L.mid.assign((size_t)T * LANES, 0);
+  L.split.assign((size_t)T * SPLITS * LANES, 0);
   L.sched.assign(2 * (size_t)T, 0);
   lane_bits.assign((size_t)T * LANES, 0);
   std::vector<uint8_t> ring_ok(T, 0);  // bit 0: RS 16 fits, bit 1: RS 32 fits
@@ -134,6 +135,8 @@ bool analyse_tiles(Layout& L, int T, int threads, B bits32, Lim limit, Check che
           break;
         }
         L.mid[(size_t)t * LANES + l] = (uint16_t)(p[TK] + GUARD);
+        for (int k = 0; k < SPLITS; ++k)
+          L.split[((size_t)t * SPLITS + k) * LANES + l] = (uint16_t)(p[k * (LANE_SYMS / SPLITS)] + GUARD);
         lane_bits[(size_t)t * LANES + l] = p[LANE_SYMS];
       }
       if (bad) break;

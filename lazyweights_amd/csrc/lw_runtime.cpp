@@ -224,10 +224,11 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][4-byte table 8192 B][tbase 4T][mid 64T][rows 2T][sched 16T (16-aligned)][exception tiles 4E]
-  // padded to 256 B, then the words
+  // [lut 4096 B][4-byte table 8192 B][tbase 4T][mid 64T][split 512T][rows 2T][sched 16T (16-aligned)]
+  // [exception tiles 4E] padded to 256 B, then the words
   const size_t nexc = L.exc.size();
-  const size_t o_lut4 = 2 * lw::LUTN, o_tb = o_lut4 + 4 * lw::LUTN, o_mid = o_tb + 4ull * T, o_rows = o_mid + 64ull * T;
+  const size_t o_lut4 = 2 * lw::LUTN, o_tb = o_lut4 + 4 * lw::LUTN, o_mid = o_tb + 4ull * T;
+  const size_t o_split = o_mid + 64ull * T, o_rows = o_split + 64ull * lw::SPLITS * T;
   const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_exc = o_sched + 16ull * T;
   const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
@@ -236,6 +237,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (t.kqt) lw::decode_table4(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_lut4));
   memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
+  memcpy(host.data() + o_split, L.split.data(), 64ull * lw::SPLITS * T);
   memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
   memcpy(host.data() + o_sched, L.sched.data(), 16ull * T);
   if (nexc) memcpy(host.data() + o_exc, L.exc.data(), 4 * nexc);
@@ -259,6 +261,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_lut4) : nullptr;
   dm.tbase = reinterpret_cast<const uint32_t*>(b + o_tb);
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
+  dm.split = reinterpret_cast<const uint16_t*>(b + o_split);
   dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
   dm.sched = reinterpret_cast<const uint4*>(b + o_sched);
@@ -380,6 +383,25 @@ int flat_width(int total, int rs, int mintiles, int spare_bytes) {
   return std::max(1, best);
 }
 
+// Both kernels in units of one dependent symbol-pair step (about 630 cycles at full load). The ring kernel's waves
+// run 128 pairs per tile; the low-latency kernel's blocks (4 waves, one tile, whole tile staged in LDS) run 32 pairs
+// after staging (counted as 8 more) and a combine step.
+long long ring_cost(int total, int w, int lds) { return flat_cost(total, w, lds) * 128; }
+long long split_cost(int total, int stage_rows, int kqt) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+  }
+  const int nsubt = lw::kq_symbits(kqt) == 4 ? 2 * lw::TK / lw::kq_gw(kqt) : lw::TK / lw::kq_gw(kqt);
+  const int lds = 4 * lw::LUTN + lw::TN * nsubt * 4 + stage_rows * 128;
+  const long long per_cu = std::max(1, std::min(160 * 1024 / lds, 8));
+  const long long b = (total + cus - 1) / cus, full = b / per_cu, rest = b % per_cu;
+  return full * std::max<long long>(4 * per_cu, 16) * 40 + (rest ? std::max<long long>(4 * rest, 16) * 40 : 0);
+}
+
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
 // others into whole-tile launches. The ordered reduction over tile columns runs inside the flat (m = 1) launch for
@@ -408,12 +430,13 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   const bool ring_ok = g_kernel_mode != 1;
   const bool flat = ring_ok && mt == 1 && g_kernel_mode != 2;
   // m = 1 (fp16 x): one flat launch (balanced blocks) per (K-quant type, ring size) and batch of MAX_GROUP
-  // matrices, whatever their order. In a 16-row launch, exception tiles with a 32-row schedule are decoded in place
-  // in spare rings when those fit the LDS the launch's block width assumed.
-  std::vector<char> done(count, 0), exc_in(count, 0);
-  std::vector<lw::FlatPlan> flat_plans;
+  // matrices, whatever their order: the ring kernel, or the low-latency kernel when the cost model favours it (few
+  // tiles per CU) or a matrix has no ring schedule. In a 16-row ring launch, exception tiles with a 32-row schedule
+  // are decoded in place in spare rings when those fit the LDS the launch's block width assumed.
+  std::vector<char> done(count, 0), exc_in(count, 0), whole(count, 0);  // whole: every tile in a low-latency launch
+  std::vector<lw::FlatPlan> flat_plans, split_plans;
   for (int i = 0; flat && i < count; ++i) {
-    if (done[i] || !ts[i]->dm.ring_rows) continue;
+    if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
     std::vector<int> sel;
     for (int j = i; j < count && (int)sel.size() < lw::MAX_GROUP; ++j)
@@ -435,6 +458,20 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       done[j] = 1;
     }
     fp.ntiles = total;
+    bool split = !di.ring_rows || g_kernel_mode == 4;
+    if (!split && g_kernel_mode != 5) {
+      const int w = flat_width(total, di.ring_rows, mintiles, 0);
+      split = split_cost(total, lw::split_stage_rows(fp), di.kqt) < ring_cost(total, w, flat_lds(w, di.ring_rows, 0));
+    }
+    if (split) {  // every tile of these matrices, exceptions included; the reduction in the launch
+      for (int k = 0; k < fp.n; ++k) {
+        fp.e[k].Y = Y[sel[k]];
+        fp.e[k].cnt = M.cnt + coff[sel[k]];
+        reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
+      }
+      split_plans.push_back(fp);
+      continue;
+    }
     const int spare_ring = 2 * 16 * 128;
     fp.W = flat_width(total, di.ring_rows, mintiles, nx && di.ring_rows == 16 ? spare_ring : 0);
     if (nx && di.ring_rows == 16 && g_kernel_mode != 3) {
@@ -467,8 +504,8 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     flat_plans.push_back(fp);
   }
   // exception tiles not decoded in place, ahead of the ring launches on the same stream: those with a 32-row
-  // schedule through the flat kernel (m = 1) in one-wave blocks, one launch per K-quant type; the rest (and every
-  // exception tile when m > 1) through the whole-tile kernel. (A second stream overlapped them with the ring launch
+  // schedule through the flat kernel (m = 1) in one-wave blocks, one launch per K-quant type; the rest through the
+  // low-latency kernel (m = 1) or the whole-tile kernel (m > 1). (A second stream overlapped them with the ring launch
   // but its join cost more than the serial pass.)
   if (ring_ok) {
     std::vector<char> xdone(exc_in);
@@ -495,19 +532,34 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     for (int i = 0; i < count; ++i) {
       const lw::DevMat& dm = ts[i]->dm;
-      if (!dm.ring_rows || !dm.nexc) continue;
+      if (!dm.ring_rows || !dm.nexc || whole[i]) continue;
       lw::DevMat rest = dm;
       if (flat) {  // the flat launches took the first nexc32
         rest.exc = dm.exc + dm.nexc32;
         rest.nexc = dm.nexc - dm.nexc32;
       }
       if (!rest.nexc) continue;
-      HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], s));
+      if (flat) {  // m = 1: the low-latency kernel over the list (the same bits as the ring kernels)
+        lw::FlatPlan fp{};
+        lw::FlatEntry& e = fp.e[fp.n++];
+        e.M = dm;
+        e.X2 = static_cast<const uint32_t*>(X16[i]);
+        e.P = M.P + off[i];
+        e.list = rest.exc;
+        e.ntile = fp.ntiles = rest.nexc;
+        HIPCHECK(lw::launch_fused_split(fp, s));
+      } else {
+        HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], s));
+      }
       if (launches) ++*launches;
     }
   }
   for (const lw::FlatPlan& fp : flat_plans) {
     HIPCHECK(lw::launch_fused_flat(fp, s));
+    if (launches) ++*launches;
+  }
+  for (const lw::FlatPlan& fp : split_plans) {
+    HIPCHECK(lw::launch_fused_split(fp, s));
     if (launches) ++*launches;
   }
   for (int i = 0; i < count; ++i) {
@@ -915,7 +967,7 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 3) return -1;
+  if (mode < 0 || mode > 5) return -1;
   g_kernel_mode = mode;
   return 0;
 }

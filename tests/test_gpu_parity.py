@@ -262,8 +262,9 @@ def test_gpu_grouped_launch_matches_single(fmt_rt):
 
 
 def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
-    """A matrix whose tile 5 has no 16-row ring schedule: the ring kernel skips it and the whole-tile kernel's
-    exception pass decodes it; GEMV (m = 1, fp16 x) and fp32-x m = 3 against fp64, decode bit-exact."""
+    """A matrix whose tile 5 has no ring schedule: the ring kernel skips it and an exception pass decodes it (the
+    low-latency kernel for m = 1, the whole-tile kernel for m > 1); GEMV (m = 1, fp16 x) and fp32-x m = 3 against
+    fp64, decode bit-exact."""
     import torch
     from lazyweights_amd import Runtime
     from lazyweights_amd.bundle import Writer
@@ -336,6 +337,54 @@ def test_gpu_exception_tiles_in_place(gpu, tmp_path, orc):
         check_err(runs[0][1], ys64, "in-place exceptions grouped: small")
         check_err(runs[0][2], y64[:1], "in-place exceptions grouped")
         check_err(rt.test_matmul("mskew", X.float().numpy(), path=0), y64, "exception pass fp32 m=3")
+
+
+def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):
+    """The low-latency kernel (8 chains per lane, whole tile in LDS; mode 4) gives the same bits as the ring
+    kernels (mode 5), for every format, single matrices and a group spanning several matrices; also for matrices
+    with exception tiles (with and without a 32-row schedule), whose ring path takes the exception passes."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer
+    from test_layout import mild_skew_codes, skewed_tile_codes
+
+    def run(rt, names, xs, mode):
+        assert rt.lib.lw_set_kernel_mode(mode) == 0
+        try:
+            ys = [torch.zeros(1, rt.info(nm)["N"], device="cuda") for nm in names]
+            n = len(names)
+            rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                            (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                            (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+            assert rc == 0, rt.lib.lw_last_error()
+            torch.cuda.synchronize()
+            return [y.cpu() for y in ys]
+        finally:
+            rt.lib.lw_set_kernel_mode(0)
+
+    rt, mats = fmt_rt
+    for kqt, fmt, H in FORMATS:
+        for names in ([fmt], [fmt + "_small", fmt, fmt + "_small"]):
+            X = [torch.randn(1, mats[nm][3]).half() for nm in names]
+            xs = [x.cuda() for x in X]
+            a, b = run(rt, names, xs, 4), run(rt, names, xs, 5)
+            say("low-latency kernel", fmt, len(names))
+            for nm, x, ya, yb in zip(names, X, a, b):
+                assert torch.equal(ya, yb), nm
+                _, y64 = reference_y(orc, mats[nm], x.double().numpy())
+                check_err(ya.numpy(), y64, "%s low-latency" % nm)
+    w = Writer(str(tmp_path))
+    for nm, (codes, side) in (("mskew", mild_skew_codes()), ("skew", skewed_tile_codes())):
+        w.add_kquant(nm, 2, codes, side)
+    w.close()
+    with Runtime(tmp_path) as rt2:
+        x = torch.randn(1, 8192).half().cuda()
+        for nm in ("mskew", "skew"):
+            a, b = run(rt2, [nm], [x], 4), run(rt2, [nm], [x], 5)
+            say("low-latency kernel, exception tiles", nm)
+            assert torch.equal(a[0], b[0]), nm
 
 
 def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):

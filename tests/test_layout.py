@@ -13,22 +13,25 @@ import pytest
 from conftest import golden_cases, load_golden
 
 
-def build_layout(lib, blob, N, KS, pre_il=0, compact=0, extra=False):
+def build_layout(lib, blob, N, KS, pre_il=0, compact=0, extra=False, splits=False):
     import ctypes
     b = np.frombuffer(blob, np.uint8) if isinstance(blob, bytes) else np.ascontiguousarray(blob, np.uint8)
     T = (N // 64) * (KS // 256)
     tbase = np.zeros(T, np.uint32)
     mid = np.zeros(T * 32, np.uint16)
+    split = np.zeros(T * 8 * 32, np.uint16)
     rows = np.zeros(T, np.uint16)
     sched = np.zeros(2 * T, np.uint64)
     rr = ctypes.c_int(0)
     n = lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, tbase.ctypes.data, mid.ctypes.data,
-                            rows.ctypes.data, sched.ctypes.data, ctypes.byref(rr), None, 0)
+                            split.ctypes.data, rows.ctypes.data, sched.ctypes.data, ctypes.byref(rr), None, 0)
     if n < 0:
         return None
     words = np.zeros(n, np.uint32)
-    lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, None, None, None, None, None,
+    lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, None, None, None, None, None, None,
                         words.ctypes.data, n)
+    if splits:
+        return tbase, split.reshape(T, 8, 32), rows, words
     if extra:
         return tbase, mid.reshape(T, 32), rows, words, sched, rr.value
     return tbase, mid.reshape(T, 32), rows, words
@@ -217,6 +220,70 @@ def emulate_ring(lut, tbase, mid, words, sched, RS, N, KS, syms):
                     last = g == 15 and p == 7          # the final re-read is never used
                     assert last or np.array_equal(C, W(P >> 5)), (t, f, g, p)
     return out
+
+
+def emulate_split(lut, tbase, split, rows, words, N, KS):
+    """The low-latency kernel's decode (k_fused_split): per tile and lane 8 chains of 64 symbols from the load-time
+    split offsets, each with the register window (rows r, r + 1, then r + 2 after every pair) over the staged tile
+    image of rows[t] + 2 rows, asserting that every row read lies inside it."""
+    KT = KS // 256
+    lut = lut.astype(np.uint64)
+    out = np.zeros((N, KS), np.uint8)
+    l = np.arange(32)
+    M32 = np.uint64(0xFFFFFFFF)
+    for t in range(len(tbase)):
+        tr, tc = divmod(t, KT)
+        R = int(rows[t]) + 2
+        img = words[int(tbase[t]):int(tbase[t]) + 32 * R].astype(np.uint64).reshape(R, 32)
+
+        def row(r):
+            assert np.all(r >= 0) and np.all(r < R), (t, "row outside the staged image")
+            return img[r, l]
+        for f in range(2):
+            for w in range(4):
+                P = split[t, 4 * f + w].astype(np.int64) - GUARD + 64
+                slot = P >> 5
+                A, B, C = row(slot - 2), row(slot - 1), row(slot)
+                col = 64 * w
+                for p in range(32):
+                    w1 = (((B << np.uint64(32)) | A) >> (P & 31).astype(np.uint64)) & M32
+                    e1 = lut[(w1 >> np.uint64(GUARD)) & np.uint64(2047)]
+                    w2 = w1 >> (e1 >> np.uint64(8))
+                    e2 = lut[(w2 >> np.uint64(GUARD)) & np.uint64(2047)]
+                    rr = tr * 64 + 32 * f + l
+                    out[rr, tc * 256 + col] = (e1 & np.uint64(255)).astype(np.uint8)
+                    out[rr, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
+                    col += 2
+                    P = P + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+                    nslot = P >> 5
+                    slide = nslot != slot
+                    A, B = np.where(slide, B, A), np.where(slide, C, B)
+                    slot = nslot
+                    C = row(slot)
+    return out
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_split_chain_emulation(lib, case):
+    """The 8 chain starts per lane reproduce the golden decode (k = 0 is the guard, k = 4 is mid)."""
+    g = load_golden(case)
+    N, KS = g["sym"].shape
+    tbase, split, rows, words = build_layout(lib, g["blob"], N, KS, splits=True)
+    _, mid, _, _ = build_layout(lib, g["blob"], N, KS)
+    assert np.all(split[:, 0] == GUARD) and np.array_equal(split[:, 4], mid)
+    assert np.array_equal(emulate_split(g["lut"], tbase, split, rows, words, N, KS), g["decoded"])
+
+
+def test_split_chain_emulation_exception_tiles(lib):
+    """Tiles without a 16-row ring schedule (one with a 32-row schedule, one with none) decode through the chains
+    like any other tile."""
+    from lazyweights_amd import bundle
+    for codes, _ in (mild_skew_codes(), skewed_tile_codes()):
+        sym = bundle.form_symbols(2, codes)
+        blob, _ = bundle.encode_huf8(sym)
+        tbase, split, rows, words = build_layout(lib, blob, 128, 8192, splits=True)
+        lut = np.frombuffer(blob, np.uint16, 2048, 0)
+        assert np.array_equal(emulate_split(lut, tbase, split, rows, words, 128, 8192), sym)
 
 
 @pytest.mark.parametrize("case", golden_cases())
