@@ -107,6 +107,7 @@ def main():
     ap.add_argument("--workdir", default=None)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--no-packed", action="store_true", help="skip the packed-twin control")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
@@ -214,6 +215,33 @@ def main():
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
 
+        # packed-twin control: the same codes stored fixed-rate (pk4 / pk8), no decode chain; the achievable rate of
+        # this access pattern and arithmetic without entropy decoding (the reference's pk4 baseline)
+        packed = None
+        if not a.no_packed:
+            pdir = os.path.join(work, "packed")
+            bundle.write_packed_bundle(pdir, mats, threads=16)
+            rtp = Runtime(pdir)
+            pbytes = float(sum(rtp.info(mt[0])["blob_bytes"] + rtp.info(mt[0])["side_bytes"] + 2 * mt[3] * m
+                               + 4 * m * mt[2] for mt in mats))
+
+            def pstep():
+                for nm, xx, yy in per_layer:
+                    if lib.lw_group_matmul_dev(rtp.h, 7, nm, xx, m, yy, stream) != 0:
+                        raise RuntimeError(lib.lw_last_error().decode())
+            pstep()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(a.steps):
+                pstep()
+            torch.cuda.synchronize()
+            pms = (time.perf_counter() - t0) * 1e3 / a.steps
+            rtp.close()
+            packed = {"ms_per_step": round(pms, 4), "GBps_packed_bytes": round(pbytes / (pms * 1e-3) / 1e9, 1),
+                      "speed_vs_coded": round(ms_per_step / pms, 3), "kernel": "k_fused_packed"}
+            log("bench: packed-twin control %.3f ms per step, %.1f GB/s of packed bytes (%.2fx the coded step)"
+                % (pms, packed["GBps_packed_bytes"], ms_per_step / pms))
+
         traffic = None
         if not a.no_traffic:
             t = measure_traffic(a.layers)
@@ -274,6 +302,7 @@ def main():
                                   "GBps": round(bytes_per_step / (serial_ms * 1e-3) / 1e9, 1)},
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
+            "control_packed_twin": packed,
         }
         print(json.dumps(res), flush=True)
         rt.close()

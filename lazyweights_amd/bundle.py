@@ -70,11 +70,16 @@ class Writer:
         self.lines.append("t %s %s %d %d %.9g %d %d %d" % (name, enc, N, K, scale, zp, self.off, len(blob)))
         self.off += len(blob)
 
-    def add_kquant(self, name, kqt, codes, side):
-        """A K-quant matrix as the reference bundler writes it (scripts/a2_kq_bundle.py:216-218)."""
+    def add_kquant(self, name, kqt, codes, side, packed=False):
+        """A K-quant matrix as the reference bundler writes it (scripts/a2_kq_bundle.py:216-218): Huffman-coded
+        (huf4p / huf8), or with packed=True the fixed-rate twin (pk4 / pk8: the symbol bytes as they are)."""
         N, K = codes.shape
-        blob, _ = encode_huf8(form_symbols(kqt, codes))
-        self.add(name, "huf4p" if SYMBITS[kqt] == 4 else "huf8", N, K, 1.0, 0, blob)
+        sym = form_symbols(kqt, codes)
+        if packed:
+            self.add(name, "pk4" if SYMBITS[kqt] == 4 else "pk8", N, K, 1.0, 0, np.ascontiguousarray(sym).tobytes())
+        else:
+            blob, _ = encode_huf8(sym)
+            self.add(name, "huf4p" if SYMBITS[kqt] == 4 else "huf8", N, K, 1.0, 0, blob)
         self.add(name + ".kqs", "kq_" + KQ_NAME[kqt], N, side.shape[1], 1.0, 0, np.ascontiguousarray(side).tobytes())
 
     def close(self):
@@ -99,6 +104,16 @@ def read_tensor(path, t):
     with open(os.path.join(path, "weights.bin"), "rb") as f:
         f.seek(t["offset"])
         return np.frombuffer(f.read(t["nbytes"]), np.uint8)
+
+
+def write_packed_bundle(path, mats, threads=16):
+    """The packed twin of write_synthetic_bundle's matrices (the same seeded codes and side bytes), enc pk4 / pk8."""
+    w = Writer(str(path))
+    for name, kqt, N, K, H, seed in mats:
+        codes, side = synth_matrix(kqt, N, K, H, seed, threads)
+        w.add_kquant(name, kqt, codes, side, packed=True)
+    w.close()
+    return path
 
 
 def write_synthetic_bundle(path, mats, threads=16):

@@ -35,6 +35,8 @@ struct DevMat {
   // by the flat ring kernel from this list), the rest go through the whole-tile kernel
   const uint32_t* exc;
   int nexc, nexc32;
+  // 1: a packed (fixed-rate) matrix: words = the symbols as 16-byte chunks [T][16][64], lut4 = 256 symbol entries
+  int packed;
 };
 
 // Matrices of one grouped launch of the ring kernel (same K-quant type and ring size). Matrix i owns blocks
@@ -87,6 +89,11 @@ int split_stage_rows(const FlatPlan& plan);
 // K-quant types or ring sizes, or a matrix has no ring schedule).
 hipError_t launch_fused_group(const GroupPlan& plan, hipStream_t s);
 int group_waves_per_block(int ring_rows);
+// The packed (fixed-rate) twin over a plan of packed matrices of one K-quant type: blocks of 16 tile rows of one
+// tile column (block0 as for the ring kernel with 16 waves per block); partials as the ring kernel's.
+hipError_t launch_fused_packed(const GroupPlan& plan, hipStream_t s);
+// The packed twin for m = 1 over a flat plan (one tile per wave, W waves per block, every matrix whole; no lists).
+hipError_t launch_fused_packed_flat(const FlatPlan& plan, hipStream_t s);
 
 // Ordered reduction of several matrices in one launch: Y_i[j][n] = sum_tc P_i[tc][jj][n] (as launch_reduce).
 struct ReduceEntry {

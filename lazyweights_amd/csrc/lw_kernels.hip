@@ -396,25 +396,138 @@ struct XgRegs {
 // One tile's decode + dequant + dot products for both fronts of a wave (see k_fused_ring); `st` stages the ring,
 // `xgf(sub, j)` = sum of token j's x over sub-block `sub` of the tile column, `lutsel` = byte offset of the tile's
 // decode table within `lut4` (0 or 8192, OR-ed into the index).
-template <int KQ, int MT, bool COH = false, class Stager, class Xg>
-__device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint32_t lutsel, const uint32_t* xs,
-                                          const Xg& xgf, __attribute__((address_space(4))) const uint32_t* xcol,
-                                          const uint8_t* srow, uint32_t P, uint32_t rlb, int mt, int N, float* out) {
+// Symbol source of tile_gemv: the ring decoder. Window rows r, r + 1 in registers (A, B), row r + 2 (C) re-read
+// from the lane's ring column after every pair; P = bit position + 64 (bits 0-4: window offset, bits 5+: the row C
+// holds). pair() decodes the next two symbols and returns their table entries.
+template <class Stager>
+struct RingSrc {
+  static constexpr bool kFullUnroll = false, kPrefetchSide = false, kXLds = false;
+  static constexpr const uint32_t* xl = nullptr;
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  Stager& st;
+  uint32_t P, rlb, tsel, tmask, rmask, rbits, slot, A, B, C;
+  __device__ __forceinline__ RingSrc(Stager& s, const uint32_t* lut4, uint32_t lutsel, uint32_t P0, uint32_t rlb0)
+      : st(s), P(P0), rlb(rlb0) {
+    rmask = st.rmask;
+    rbits = rmask == 15u ? 4u : 5u;  // ring of 16 or 32 rows
+    // LDS byte address of the tile's table (a multiple of 8 KB: the tables are the kernels' only static LDS object)
+    tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4 + lutsel;
+    tmask = 0x1FFCu;
+    asm volatile("" : "+v"(tmask));
+    __builtin_amdgcn_s_setprio(3);
+    slot = __builtin_amdgcn_ubfe(P, 5, rbits);
+    A = *(LdsU32*)(rlb + (((slot - 2u) & rmask) << 7));
+    B = *(LdsU32*)(rlb + (((slot - 1u) & rmask) << 7));
+    C = *(LdsU32*)(rlb + (slot << 7));
+  }
+  // group g (16 symbols) begins: issue priority falls with progress (3 for the first quarter of the tile .. 0 for the
+  // last), so the waves sharing a SIMD keep pace instead of the oldest finishing first and the youngest running
+  // alone at the end; then the ring staging step
+  __device__ __forceinline__ void stage(int g) {
+    if (g == 4) __builtin_amdgcn_s_setprio(2);
+    if (g == 8) __builtin_amdgcn_s_setprio(1);
+    if (g == 12) __builtin_amdgcn_s_setprio(0);
+    st.stage(g);
+  }
+  __device__ __forceinline__ void pair(int, uint32_t& e1, uint32_t& e2) {
+    const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
+    e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
+    // the second symbol lies within w1: it starts len1 <= 11 bits further and its table index ends by bit 24
+    const uint32_t w2 = w1 >> (e1 & 31u);
+    e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
+    P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
+    // a pair advances at most 22 bits: the window slides by at most one row
+    const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, rbits);
+    const bool slide = nslot != slot;
+    A = slide ? B : A;
+    B = slide ? C : B;
+    slot = nslot;
+    C = *(LdsU32*)(rlb + (nslot << 7));
+  }
+};
+
+// Symbol source of tile_gemv: the packed (fixed-rate) twin. Lane L reads the 16 symbol bytes of group g of its
+// tile row as one 16-byte chunk (chunk g at src + 64 g, one group ahead in registers) and looks each symbol up in
+// the 256-entry symbol table, whose entries carry the same payload bits as the decode table's: the products, and
+// so the results, are those of the coded matrix with the same codes.
+// Q4_K needs no table: a symbol's grid bytes are its two nibbles, placed in bytes 2 and 3 of the entry with one
+// byte permute of the word's low and high nibbles.
+// The chunks stream through a per-wave LDS ring of PK_SLOTS 1 KB slots by direct-to-LDS loads, PK_DEPTH groups
+// ahead, so several KB per wave are in flight without holding registers. kFullUnroll: the pairs of a group are
+// unrolled (pair(p) selects its word by p).
+constexpr int PK_DEPTH = 3, PK_SLOTS = PK_DEPTH + 1;
+// m = 1 (kXLds): the tile column's x pairs are staged in LDS too (xl, 1 KB per wave), since without a decode chain
+// the scalar-cache latency of x per group would be exposed.
+template <int KQ>
+struct PackedSrc {
+  static constexpr bool kFullUnroll = true, kPrefetchSide = false, kXLds = true;
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  const uint4* src;  // this lane's chunk of group 0; group g at src + 64 g
+  uint4* ring;       // the wave's PK_SLOTS x 64 chunks
+  const uint32_t* xl;
+  uint4 cur;
+  uint32_t tsel, lo, hi, lane;
+  __device__ __forceinline__ void fetch(int g) {
+    __builtin_amdgcn_global_load_lds(src + 64 * g, (__attribute__((address_space(3))) void*)(ring + (g % PK_SLOTS) * 64),
+                                     16, 0, 0);
+  }
+  // x: the tile column's pairs (TW / 2 dwords) into xs, with direct-to-LDS loads (null: not staged)
+  __device__ __forceinline__ PackedSrc(const uint4* s, uint4* r, const uint32_t* tab, uint32_t l, const uint32_t* xcol,
+                                       uint32_t* xs)
+      : src(s), ring(r), xl(xs), lane(l) {
+    tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)tab;
+    if (xs) {
+      constexpr int NPAIR = (kq_symbits(KQ) == 4 ? 2 * TK : TK) / 2;
+#pragma unroll
+      for (int i = 0; i < NPAIR / 64; ++i)
+        __builtin_amdgcn_global_load_lds(xcol + 64 * i + l, (__attribute__((address_space(3))) void*)(xs + 64 * i), 4, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < PK_DEPTH; ++i) fetch(i);
+  }
+  // group g: fetch group g + PK_DEPTH (into the slot group g - 1 used), wait for group g's chunk (loads complete in
+  // order: at most PK_DEPTH younger ones may stay outstanding), read it
+  __device__ __forceinline__ void stage(int g) {
+    if (g + PK_DEPTH < 16) {
+      fetch(g + PK_DEPTH);
+      __builtin_amdgcn_s_waitcnt(PK_DEPTH == 3 ? 0x0F73 : 0x0F70);  // vmcnt(PK_DEPTH)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
+    // the read is opaque to the compiler, which would otherwise wait for every direct-to-LDS load before any LDS
+    // read (the explicit vmcnt above already orders this one)
+    const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint4*)(ring + (g % PK_SLOTS) * 64 + lane);
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(cur) : "v"(a));
+  }
+  __device__ __forceinline__ void pair(int p, uint32_t& e1, uint32_t& e2) {
+    const uint32_t w = p < 2 ? cur.x : p < 4 ? cur.y : p < 6 ? cur.z : cur.w;
+    if (KQ == KQ_Q4_K) {
+      if (!(p & 1)) {
+        lo = w & 0x0F0F0F0Fu;
+        hi = (w >> 4) & 0x0F0F0F0Fu;
+      }
+      const uint32_t k = 2 * (p & 1);  // symbols k, k + 1 of the word: entry bytes 2, 3 = their low, high nibble
+      e1 = __builtin_amdgcn_perm(hi, lo, 0x00000C0Cu | (k << 16) | ((4u + k) << 24));
+      e2 = __builtin_amdgcn_perm(hi, lo, 0x00000C0Cu | ((k + 1) << 16) | ((5u + k) << 24));
+    } else {
+      const uint32_t h = (p & 1) ? w >> 16 : w;
+      e1 = *(LdsU32*)(tsel + ((h & 255u) << 2));
+      e2 = *(LdsU32*)(tsel + (((h >> 8) & 255u) << 2));
+    }
+  }
+};
+
+// One tile's dequant + dot products for both fronts of a wave, from a symbol source (`src.stage(g)` at each
+// 16-symbol group, `src.pair(p, e1, e2)` for the table entries of the group's pair p: see decode_table4).
+// `xgf(sb, jj, j)` = sum of token j's x over sub-block jj of super-block sb of the tile column.
+template <int KQ, int MT, bool COH = false, class Src, class Xg>
+__device__ __forceinline__ void tile_gemv(Src& src, const uint32_t* xs, const Xg& xgf,
+                                          __attribute__((address_space(4))) const uint32_t* xcol,
+                                          const uint8_t* srow, int mt, int N, float* out) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
-  const uint32_t rmask = st.rmask, rbits = rmask == 15u ? 4u : 5u;  // ring of 16 or 32 rows
   constexpr bool XS_SGPR = MT == 1;
-  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
-  // LDS byte address of the tile's table (a multiple of 8 KB: the tables are the kernels' only static LDS object)
-  const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4 + lutsel;
-  uint32_t tmask = 0x1FFCu;
-  asm volatile("" : "+v"(tmask));
-  __builtin_amdgcn_s_setprio(3);
-  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, rbits);
-  uint32_t A = *(LdsU32*)(rlb + (((slot - 2u) & rmask) << 7));
-  uint32_t B = *(LdsU32*)(rlb + (((slot - 1u) & rmask) << 7));
-  uint32_t C = *(LdsU32*)(rlb + (slot << 7));
   constexpr int NSB = TW / 256;      // super-blocks per tile column
   constexpr int GPS = 16 / NSB;      // staging groups (16 symbols) per super-block
   constexpr int NSUB = 256 / GW;     // sub-blocks per super-block
@@ -435,11 +548,21 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
   for (int q = 0; q < NQ; ++q) accm[q] = f4v{0.f, 0.f, 0.f, 0.f};
   const uint32_t ltok = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 3u;
   uint32_t wprev = 0;
+  // sources without a decode chain (kPrefetchSide) load the next super-block's side words a super-block ahead, so
+  // their HBM latency hides behind a super-block of work; the ring decoder's registers are too tight for that
+  uint32_t swn[5] = {0, 0, 0, 0, 0};
+  if (Src::kPrefetchSide) side_load<KQ>(srow, swn);
 
 #pragma unroll 1
   for (int sb = 0; sb < NSB; ++sb) {
     uint32_t sw[5];
-    side_load<KQ>(srow + sb * (TN * SB), sw);
+    if (Src::kPrefetchSide) {
+#pragma unroll
+      for (int i = 0; i < 5; ++i) sw[i] = swn[i];
+      if (sb + 1 < NSB) side_load<KQ>(srow + (sb + 1) * (TN * SB), swn);
+    } else {
+      side_load<KQ>(srow + sb * (TN * SB), sw);
+    }
     float dA, dB;
     uint64_t scq, scq2;  // sub-block scales as bytes (signed for Q6_K / IQ4_XS), consumed low byte first
     side_packed<KQ>(sw, scq, scq2, dA, dB);
@@ -470,33 +593,18 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int g = sb * GPS + gg2 + h;
-        // issue priority falls with progress (3 for the first quarter of the tile .. 0 for the last), so the waves
-        // sharing a SIMD keep pace instead of the oldest finishing first and the youngest running alone at the end
-        if (g == 4) __builtin_amdgcn_s_setprio(2);
-        if (g == 8) __builtin_amdgcn_s_setprio(1);
-        if (g == 12) __builtin_amdgcn_s_setprio(0);
-        st.stage(g);
+        src.stage(g);
         // m = 1 unrolls the group fully; more tokens unroll less (their x operands come from LDS per pair)
-#pragma unroll MT == 1 ? 8 : (MMA && SYMB == 4 ? 1 : 2)
+#pragma unroll((MT == 1 || Src::kFullUnroll) ? 8 : (MMA && SYMB == 4 ? 1 : 2))
         for (int p = 0; p < 8; ++p) {
-          const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
-          const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
-          // the second symbol lies within w1: it starts len1 <= 11 bits further and its table index ends by bit 24
-          const uint32_t w2 = w1 >> (e1 & 31u);
-          const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
-          P = P + e1 + e2;  // lengths land in bits 0-15 exactly; entry values only disturb bits >= 16
-          // a pair advances at most 22 bits: the window slides by at most one row
-          const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, rbits);
-          const bool slide = nslot != slot;
-          A = slide ? B : A;
-          B = slide ? C : B;
-          slot = nslot;
-          C = *(LdsU32*)(rlb + (nslot << 7));
+          uint32_t e1, e2;
+          src.pair(p, e1, e2);
           if (SYMB == 4) {
             const uint32_t v1 = __builtin_amdgcn_perm(e1, e1, 0x0C030C02u), v2 = __builtin_amdgcn_perm(e2, e2, 0x0C030C02u);
             const int c = 16 * g + 2 * p;
             if (XS_SGPR) {
-              acc[0] = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc[0]));
+              if (Src::kXLds) acc[0] = dot2(v2, src.xl[c + 1], dot2(v1, src.xl[c], acc[0]));
+              else acc[0] = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc[0]));
             } else if (MMA) {
               const h4v wv = __builtin_bit_cast(h4v, make_uint2(v1, v2));
 #pragma unroll
@@ -513,7 +621,8 @@ __device__ __forceinline__ void ring_tile(Stager& st, const uint32_t* lut4, uint
             const uint32_t w = __builtin_amdgcn_perm(e2, e1, 0x07060302u);
             const int c = 8 * g + p;
             if (XS_SGPR) {
-              acc[0] = dot2(w, xcol[c], acc[0]);
+              if (Src::kXLds) acc[0] = dot2(w, src.xl[c], acc[0]);
+              else acc[0] = dot2(w, xcol[c], acc[0]);
             } else if (MMA) {  // one 4-weight product per two pairs (c odd: pairs c - 1, c)
               if (p & 1) {
                 const h4v wv = __builtin_bit_cast(h4v, make_uint2(wprev, w));
@@ -641,7 +750,8 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
     st.counts = sc.x;
     st.rmask = RS - 1;
     st.init((int)init0);
-    ring_tile<KQ, MT>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
+    RingSrc<RingStager<int, uint32_t>> src(st, lut4, 0u, P, rlb);
+    tile_gemv<KQ, MT>(src, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, mt, N, out);
   } else {
     RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
@@ -649,7 +759,8 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
     st.counts = f ? sc.y : sc.x;
     st.rmask = RS - 1;
     st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, MT>(st, lut4, 0u, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, P, rlb, mt, N, out);
+    RingSrc<RingStager<int, uint32_t>> src(st, lut4, 0u, P, rlb);
+    tile_gemv<KQ, MT>(src, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, mt, N, out);
   }
 }
 
@@ -710,6 +821,117 @@ __device__ __forceinline__ XgRegs column_xsums(const uint32_t* X2, int tc, int l
   return xgr;
 }
 
+// ── packed (fixed-rate) twin: decode-free fused GEMV / skinny GEMM ─────────────────────────────────────────
+// The control the reference keeps beside its coded bundles (enc pk4 / pk8, kernels/llmrt.cu:538-630, 1731-1777):
+// the same codes stored as plain bytes, so the kernel reads 4 (pk4) or 8 (pk8) bits per weight instead of the
+// Huffman stream and runs no decode chain. Block = 16 waves = 16 tile rows of one tile column (as k_fused_ring), x
+// staged in LDS for m > 1; tile_gemv with the packed source gives the coded path's bits.
+template <int KQ, int MT>
+__global__ void __launch_bounds__(1024, MT <= 2 ? 2 : 1) k_fused_packed(GroupPlan plan) {
+  constexpr int WPB = 16;
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), NG = TW / GW, SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  constexpr int NTHR = WPB * 64;
+  __shared__ uint32_t tab[256];
+  extern __shared__ __align__(16) uint32_t smem[];
+  uint32_t* xs = smem;                                    // [NPAIR][MT] fp16 pairs (xs_index)
+  float* xg = reinterpret_cast<float*>(xs + NPAIR * MT);  // [NG][MT] sub-block sums of x
+  uint4* rings = reinterpret_cast<uint4*>(smem + ((NPAIR + NG) * MT + 3) / 4 * 4);  // WPB x PK_SLOTS x 64 chunks
+  int mi = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < plan.n && (int)blockIdx.x >= plan.e[i].block0) mi = i;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const GroupEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  KEntry* ep = (KEntry*)(kbase + offsetof(GroupPlan, e) + (size_t)mi * sizeof(GroupEntry));
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const int mt = plan.mt;
+  const int bl = (int)blockIdx.x - E.block0;
+  const int KT = M.KT, NT = M.NT, K = M.K, N = M.N;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tc = bl % KT, tr = (bl / KT) * WPB + wave;
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 256) tab[threadIdx.x] = M.lut4[threadIdx.x];
+  if (MT > 1) {
+    for (int i = threadIdx.x; i < NPAIR * MT; i += NTHR) {
+      const int j = i / NPAIR, c = i - j * NPAIR;
+      xs[xs_index<MT>(c, j)] = j < mt ? E.X2[(size_t)j * (K / 2) + (size_t)tc * NPAIR + c] : 0u;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NG * MT; i += NTHR) {
+      const int g = i / MT, j = i - g * MT;
+      xg[g * MT + j] = xsum_sub<GW>([&](int c) { return xs[xs_index<MT>(g * (GW / 2) + c, j)]; });
+    }
+  }
+  __syncthreads();
+  if (tr >= NT) return;
+  const int t = tr * KT + tc;
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)(lane * SB);
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
+  float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
+  PackedSrc<KQ> src(reinterpret_cast<const uint4*>(M.words) + (size_t)t * 16 * 64 + (uint32_t)lane,
+                    rings + wave * PK_SLOTS * 64, tab, (uint32_t)lane, E.X2 + (size_t)tc * NPAIR,
+                    MT == 1 ? reinterpret_cast<uint32_t*>(rings + WPB * PK_SLOTS * 64) + wave * NPAIR : nullptr);
+  if (MT == 1)
+    tile_gemv<KQ, MT>(src, xs, column_xsums<KQ>(E.X2, tc, lane), xcol, srow, mt, N, out);
+  else
+    tile_gemv<KQ, MT>(src, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, mt, N, out);
+}
+
+// The packed twin for m = 1 over a flat tile list, as k_fused_flat: block b decodes tiles [b W, b W + W), one per
+// wave, x through the scalar cache, the reduction over tile columns in the launch. A block spans at most two
+// matrices: both symbol tables sit in LDS.
+template <int KQ>
+__global__ void __launch_bounds__(1024) k_fused_packed_flat(FlatPlan plan) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int SB = kq_sbytes(KQ), NPAIR = TW / 2;
+  __shared__ uint32_t tab[2 * 256];
+  extern __shared__ __align__(16) uint4 pk_rings[];  // W x PK_SLOTS x 64 chunks, then W x the column's x pairs
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * W, Tl = min(T0 + W, plan.ntiles) - 1;
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  if (threadIdx.x < 256) tab[threadIdx.x] = ea->M.lut4[threadIdx.x];
+  else if (threadIdx.x < 512 && mb != ma) tab[threadIdx.x] = eb->M.lut4[threadIdx.x - 256];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = T0 + wave;
+  if (T >= plan.ntiles) return;
+  const bool second = mb != ma && T >= eb->tile0;
+  KEntry* ep = second ? eb : ea;
+  const auto& E = *ep;
+  const auto& M = E.M;
+  const int KT = M.KT, NT = M.NT, N = M.N;
+  const int u = T - E.tile0;
+  const int t = (u % NT) * KT + u / NT;
+  const int tc = t % KT, tr = t / KT;
+  const int lane = threadIdx.x & 63;
+  const XgRegs xgr = column_xsums<KQ>(E.X2, tc, lane);
+  KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
+  const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)(lane * SB);
+  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
+  uint32_t* xw = reinterpret_cast<uint32_t*>(pk_rings + W * PK_SLOTS * 64) + wave * NPAIR;
+  PackedSrc<KQ> src(reinterpret_cast<const uint4*>(M.words) + (size_t)t * 16 * 64 + (uint32_t)lane,
+                    pk_rings + wave * PK_SLOTS * 64, tab + (second ? 256 : 0), (uint32_t)lane,
+                    E.X2 + (size_t)tc * NPAIR, xw);
+  tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
+  row_reduce(E, tr, KT, N, lane);
+}
+
 // ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
 // One tile of the flat kernel: lanes of front f stage into `ring` (RS rows of 32 words).
 template <int KQ, class KEntryRef>
@@ -740,7 +962,8 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.counts = sc.x;
     st.rmask = rmask;
     st.init((int)init0);
-    ring_tile<KQ, 1, true>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+    RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
+    tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
   } else {
     RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
@@ -748,7 +971,8 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.counts = f ? sc.y : sc.x;
     st.rmask = rmask;
     st.init((int)(f ? init1 : init0));
-    ring_tile<KQ, 1, true>(st, lut4, lutsel, nullptr, xgr, xcol, srow, P, rlb, 1, N, out);
+    RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
+    tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
   }
   row_reduce(E, tr, KT, N, lane);
 }
@@ -836,7 +1060,7 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
 // into 8 chains of 64 symbols at load-time offsets (Layout::split): wave w decodes symbols [64 w, 64 w + 64) of
 // both rows of every lane (lanes 0-31 row l, lanes 32-63 row l + 32, the same x columns), with the ring kernel's
 // register window reading the tile image directly. Each chain stores its sub-block dot products in LDS; wave 0
-// then forms each row's partial exactly as ring_tile does (same operations in the same order), so the result has
+// then forms each row's partial exactly as tile_gemv does (same operations in the same order), so the result has
 // the same bits as the ring kernels'. Exception tiles need nothing special: no staging schedule is involved.
 template <int KQ>
 __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_rows) {
@@ -939,7 +1163,7 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   __syncthreads();
   if (wave != 0) return;
 
-  // row partials, as ring_tile forms them: per super-block the min / bias term first, then d x the scaled sum of
+  // row partials, as tile_gemv forms them: per super-block the min / bias term first, then d x the scaled sum of
   // the sub-block dot products in order
   const float* accrow = accb + lane * NSUBT;
   float tot = 0.f;
@@ -1051,6 +1275,71 @@ hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
     case KQ_Q5_K: return rs == 16 ? flat_launch<KQ_Q5_K, 16>(p, s) : flat_launch<KQ_Q5_K, 32>(p, s);
     case KQ_Q6_K: return rs == 16 ? flat_launch<KQ_Q6_K, 16>(p, s) : flat_launch<KQ_Q6_K, 32>(p, s);
     case KQ_IQ4_XS: return rs == 16 ? flat_launch<KQ_IQ4_XS, 16>(p, s) : flat_launch<KQ_IQ4_XS, 32>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int KQ, int MT>
+static hipError_t packed_launch(const GroupPlan& p, hipStream_t s) {
+  constexpr int TW = kq_symbits(KQ) == 4 ? 2 * TK : TK;
+  const size_t smem = ((size_t)((TW / 2) + TW / kq_gw(KQ)) * MT + 3) / 4 * 16 + (size_t)16 * PK_SLOTS * 1024 +
+                      (MT == 1 ? (size_t)16 * (TW / 2) * 4 : 0);
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_packed<KQ, MT>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((k_fused_packed<KQ, MT>), dim3(p.blocks), dim3(1024), smem, s, p);
+  return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t packed_mt(const GroupPlan& p, hipStream_t s) {
+  if (p.mt <= 1) return packed_launch<KQ, 1>(p, s);
+  if (p.mt <= 2) return packed_launch<KQ, 2>(p, s);
+  if (p.mt <= 4) return packed_launch<KQ, 4>(p, s);
+  if (p.mt <= 8) return packed_launch<KQ, 8>(p, s);
+  return packed_launch<KQ, 16>(p, s);
+}
+
+hipError_t launch_fused_packed(const GroupPlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.mt < 1 || p.mt > 16 || p.blocks < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  for (int i = 0; i < p.n; ++i)
+    if (p.e[i].M.kqt != kqt || !p.e[i].M.packed || !p.e[i].M.lut4) return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return packed_mt<KQ_Q4_K>(p, s);
+    case KQ_Q5_K: return packed_mt<KQ_Q5_K>(p, s);
+    case KQ_Q6_K: return packed_mt<KQ_Q6_K>(p, s);
+    case KQ_IQ4_XS: return packed_mt<KQ_IQ4_XS>(p, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int KQ>
+static hipError_t packed_flat_launch(const FlatPlan& p, int blocks, size_t smem, hipStream_t s) {
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_packed_flat<KQ>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_fused_packed_flat<KQ>, dim3(blocks), dim3(p.W * 64), smem, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_packed_flat(const FlatPlan& p, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || p.ntiles < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (e.M.kqt != kqt || !e.M.packed || !e.M.lut4 || e.list || e.tile0 + e.ntile != end || e.ntile < p.W ||
+        e.ntile != e.M.NT * e.M.KT || (i == 0 && e.tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  const int blocks = (p.ntiles + p.W - 1) / p.W;
+  const size_t smem = (size_t)p.W * PK_SLOTS * 1024 + (size_t)p.W * (kq_symbits(kqt) == 4 ? TK : TK / 2) * 4;
+  switch (kqt) {
+    case KQ_Q4_K: return packed_flat_launch<KQ_Q4_K>(p, blocks, smem, s);
+    case KQ_Q5_K: return packed_flat_launch<KQ_Q5_K>(p, blocks, smem, s);
+    case KQ_Q6_K: return packed_flat_launch<KQ_Q6_K>(p, blocks, smem, s);
+    case KQ_IQ4_XS: return packed_flat_launch<KQ_IQ4_XS>(p, blocks, smem, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1213,7 +1502,39 @@ __global__ void __launch_bounds__(256) k_decode(DevMat M, uint8_t* __restrict__ 
   }
 }
 
+// codes of a packed matrix for tile rows [tr0, tr1): one thread per 16-symbol chunk (pk4: two codes per symbol,
+// low nibble first; pk8: one), rows relative to tr0
+template <int SYMB>
+__global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // chunk within the row range
+  const size_t n = (size_t)(tr1 - tr0) * M.KT * 16 * 64;
+  if (i >= n) return;
+  const int L = (int)(i & 63), g = (int)((i >> 6) & 15);
+  const size_t tt = i >> 10;  // tile within the range
+  const int tc = (int)(tt % M.KT), trr = (int)(tt / M.KT);
+  const uint4 c = reinterpret_cast<const uint4*>(M.words)[((size_t)(tr0 + trr) * M.KT + tc) * 1024 + (size_t)(g * 64 + L)];
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  uint8_t* o = out + (size_t)(trr * TN + L) * M.K + (size_t)(tc * TK + 16 * g) * (SYMB == 4 ? 2 : 1);
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    const uint32_t sym = (w[b >> 2] >> (8 * (b & 3))) & 255u;
+    if (SYMB == 4) {
+      o[2 * b] = (uint8_t)(sym & 15u);
+      o[2 * b + 1] = (uint8_t)(sym >> 4);
+    } else {
+      o[b] = (uint8_t)sym;
+    }
+  }
+}
+
 hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
+  if (M.packed) {
+    const size_t n = (size_t)(tr1 - tr0) * M.KT * 16 * 64;
+    if (!n) return hipSuccess;
+    if (M.symbits == 4) hipLaunchKernelGGL(k_unpack<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
+    else hipLaunchKernelGGL(k_unpack<8>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
+    return hipGetLastError();
+  }
   const size_t smem = (size_t)LUTN * 8 + (size_t)4 * 32 * (M.max_rows + 1) * 4;
   const int tiles = (tr1 - tr0) * M.KT, blocks = (tiles + 3) / 4;
   if (blocks <= 0) return hipSuccess;

@@ -91,6 +91,9 @@ struct Tensor {
   lw::DevMat dm{};
   std::vector<uint32_t> exc32;  // host copy of the exception tiles with a 32-row schedule (dm.exc[0, nexc32))
   bool coded() const { return enc == "huf8" || enc == "huf4p"; }
+  // the fixed-rate twin: the symbols stored as plain bytes (reference enc pk4 / pk8, kernels/llmrt.cu:1731-1750)
+  bool packed() const { return enc == "pk4" || enc == "pk8"; }
+  bool matrix() const { return coded() || packed(); }
   int KS() const { return (int)(symbits == 4 ? K / 2 : K); }
   int T() const { return (int)((N / lw::TN) * (KS() / lw::TK)); }
 };
@@ -191,7 +194,9 @@ bool validate(Model& M) {
   for (auto& t : M.ts) {
     if (t.off + t.nbytes > M.file_size)
       return fail(t.name + ": extends past the end of weights.bin");
-    if (!t.coded()) continue;
+    if (!t.matrix()) continue;
+    if (t.packed() && t.pre_il) return fail(t.name + ": " + t.enc + " has no pre-interleaved form");
+    if (t.packed() && t.nbytes < (uint64_t)t.N * t.KS()) return fail(t.name + ": packed blob shorter than N x K");
     if (t.N % lw::TN || t.K % (t.symbits == 4 ? 2 * lw::TK : lw::TK))
       return fail(t.name + ": shape " + std::to_string(t.N) + "x" + std::to_string(t.K) +
                   " is not a whole number of 64 x 256-symbol tiles");
@@ -206,10 +211,33 @@ bool validate(Model& M) {
     if (x.N != t.N || x.K != (t.K / 256) * lw::kq_sbytes(kqt) || x.nbytes < (uint64_t)x.N * x.K)
       return fail(t.name + ": side tensor " + x.name + " shape does not match the matrix");
     if (t.symbits != lw::kq_symbits(kqt))
-      return fail(t.name + ": " + x.enc + " needs enc " + (lw::kq_symbits(kqt) == 4 ? "huf4p" : "huf8"));
+      return fail(t.name + ": " + x.enc + " needs enc " + (lw::kq_symbits(kqt) == 4 ? "huf4p / pk4" : "huf8 / pk8"));
     t.kqt = kqt;
     t.side_idx = it->second;
   }
+  return true;
+}
+
+// Upload a K-quant matrix's side bytes in the kernels' tile-major record order (lw::side_record).
+bool upload_side(Model& M, Tensor& t) {
+  lw::DevMat& dm = t.dm;
+  const Tensor& x = M.ts[t.side_idx];
+  t.side_bytes = (size_t)x.N * x.K;
+  std::vector<uint8_t> raw(t.side_bytes), sb(t.side_bytes);
+  if (!pread_all(M.fd, raw.data(), t.side_bytes, x.off)) return fail(t.name + ": side read error");
+  // bundle order [N][K/256][SB] -> the kernels' tile-major record order (lw::side_record)
+  const int SB = lw::kq_sbytes(t.kqt), nb = (int)(t.K / 256), nsb = t.symbits == 4 ? 2 : 1;
+  for (int n = 0; n < (int)t.N; ++n)
+    for (int b = 0; b < nb; ++b)
+      memcpy(sb.data() + lw::side_record(n, b, dm.KT, nsb) * SB, raw.data() + ((size_t)n * nb + b) * SB, SB);
+  std::vector<uint8_t>().swap(raw);
+  if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(t.name + ": device allocation failed (side)");
+  }
+  if (hipMemcpy(t.dside, sb.data(), t.side_bytes, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(t.name + ": upload failed (side)");
+  dm.side = t.dside;
   return true;
 }
 
@@ -278,31 +306,69 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.KT = t.KS() / lw::TK;
   dm.NT = (int)(t.N / lw::TN);
   dm.max_rows = L.max_rows;
-  if (t.kqt) {
-    const Tensor& x = M.ts[t.side_idx];
-    t.side_bytes = (size_t)x.N * x.K;
-    std::vector<uint8_t> raw(t.side_bytes), sb(t.side_bytes);
-    if (!pread_all(M.fd, raw.data(), t.side_bytes, x.off)) return fail(t.name + ": side read error");
-    // bundle order [N][K/256][SB] -> the kernels' tile-major record order (lw::side_record)
-    const int SB = lw::kq_sbytes(t.kqt), nb = (int)(t.K / 256), nsb = t.symbits == 4 ? 2 : 1;
-    for (int n = 0; n < (int)t.N; ++n)
-      for (int b = 0; b < nb; ++b)
-        memcpy(sb.data() + lw::side_record(n, b, dm.KT, nsb) * SB, raw.data() + ((size_t)n * nb + b) * SB, SB);
-    std::vector<uint8_t>().swap(raw);
-    if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes) != hipSuccess) {
-      (void)hipGetLastError();
-      return fail(t.name + ": device allocation failed (side)");
-    }
-    if (hipMemcpy(t.dside, sb.data(), t.side_bytes, hipMemcpyHostToDevice) != hipSuccess)
-      return fail(t.name + ": upload failed (side)");
-    dm.side = t.dside;
-  }
+  if (t.kqt && !upload_side(M, t)) return false;
   t.resident = true;
   M.resident_bytes += bytes + t.side_bytes;
   M.device_bytes += bytes;
   M.coded_bytes += t.nbytes + t.side_bytes;
   const size_t blob_pay = (size_t)((t.payload_bits + 31) / 32) * 4;
   M.pad_bytes += bytes > blob_pay ? bytes - blob_pay : 0;
+  return true;
+}
+
+// Build and upload the device layout of a packed (fixed-rate) tensor: [symbol table 256 x 4 B, the payload bits of
+// decode_table4 for every symbol] padded to 256 B, then the symbols as 16-byte chunks [T][16 groups][64 rows]: chunk
+// (t, g, L) = symbols 16 g .. 16 g + 15 of tile row L, so a wave reads one group of its tile as 1 KB.
+bool make_resident_packed(Model& M, Tensor& t) {
+  const int KS = t.KS(), NT = (int)(t.N / lw::TN), KT = KS / lw::TK, T = NT * KT;
+  std::vector<uint8_t> blob((size_t)t.N * KS);
+  if (!pread_all(M.fd, blob.data(), blob.size(), t.off)) return fail(t.name + ": read error");
+  const size_t o_words = 256 * 4, bytes = o_words + (size_t)T * lw::TN * lw::TK + 8 * 128;
+  std::vector<uint8_t> host(bytes, 0);
+  if (t.kqt) {
+    std::vector<uint16_t> ident(lw::LUTN);
+    for (int i = 0; i < lw::LUTN; ++i) ident[i] = (uint16_t)(i & 255);
+    std::vector<uint32_t> tab(lw::LUTN);
+    lw::decode_table4(t.kqt, ident.data(), tab.data());
+    memcpy(host.data(), tab.data(), 256 * 4);
+  }
+  uint8_t* w = host.data() + o_words;
+  for (int tr = 0; tr < NT; ++tr)
+    for (int tc = 0; tc < KT; ++tc)
+      for (int g = 0; g < 16; ++g)
+        for (int L = 0; L < lw::TN; ++L)
+          memcpy(w + ((((size_t)tr * KT + tc) * 16 + g) * lw::TN + L) * 16,
+                 blob.data() + (size_t)(tr * lw::TN + L) * KS + tc * lw::TK + 16 * g, 16);
+  std::vector<uint8_t>().swap(blob);
+  void* d = nullptr;
+  if (hipMalloc(&d, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(t.name + ": device allocation failed");
+  }
+  if (hipMemcpy(d, host.data(), bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    (void)hipFree(d);
+    return fail(t.name + ": upload failed");
+  }
+  t.dev = d;
+  t.dev_bytes = bytes;
+  t.payload_bits = (uint64_t)t.N * KS * 8;
+  lw::DevMat& dm = t.dm;
+  dm = lw::DevMat{};
+  uint8_t* b = static_cast<uint8_t*>(d);
+  dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b) : nullptr;
+  dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
+  dm.packed = 1;
+  dm.N = (int)t.N;
+  dm.K = (int)t.K;
+  dm.kqt = t.kqt;
+  dm.symbits = t.symbits;
+  dm.KT = KT;
+  dm.NT = NT;
+  if (t.kqt && !upload_side(M, t)) return false;
+  t.resident = true;
+  M.resident_bytes += bytes + t.side_bytes;
+  M.device_bytes += bytes;
+  M.coded_bytes += t.nbytes + t.side_bytes;
   return true;
 }
 
@@ -435,6 +501,50 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   // are decoded in place in spare rings when those fit the LDS the launch's block width assumed.
   std::vector<char> done(count, 0), exc_in(count, 0), whole(count, 0);  // whole: every tile in a low-latency launch
   std::vector<lw::FlatPlan> flat_plans, split_plans;
+  // packed (fixed-rate) matrices: the decode-free kernels, one launch per K-quant type and MAX_GROUP matrices
+  // (m = 1: the flat one, which also reduces)
+  for (int i = 0; mt == 1 && i < count; ++i) {
+    if (done[i] || !ts[i]->dm.packed) continue;
+    lw::FlatPlan fp{};
+    int mintiles = 1 << 30;
+    for (int j = i; j < count && fp.n < lw::MAX_GROUP; ++j) {
+      const lw::DevMat& dm = ts[j]->dm;
+      if (done[j] || !dm.packed || dm.kqt != ts[i]->dm.kqt) continue;
+      lw::FlatEntry& e = fp.e[fp.n++];
+      e.M = dm;
+      e.X2 = static_cast<const uint32_t*>(X16[j]);
+      e.P = M.P + off[j];
+      e.tile0 = fp.ntiles;
+      e.ntile = dm.NT * dm.KT;
+      e.Y = Y[j];
+      e.cnt = M.cnt + coff[j];
+      fp.ntiles += e.ntile;
+      mintiles = std::min(mintiles, e.ntile);
+      reduced[j] = 1;
+      done[j] = 1;
+    }
+    fp.W = flat_width(fp.ntiles, 16, mintiles, 0);
+    HIPCHECK(lw::launch_fused_packed_flat(fp, s));
+    if (launches) ++*launches;
+  }
+  for (int i = 0; i < count; ++i) {
+    if (done[i] || !ts[i]->dm.packed) continue;
+    lw::GroupPlan pp{};
+    pp.mt = mt;
+    for (int j = i; j < count && pp.n < lw::MAX_GROUP; ++j) {
+      const lw::DevMat& dm = ts[j]->dm;
+      if (done[j] || !dm.packed || dm.kqt != ts[i]->dm.kqt) continue;
+      lw::GroupEntry& e = pp.e[pp.n++];
+      e.M = dm;
+      e.X2 = static_cast<const uint32_t*>(X16[j]);
+      e.P = M.P + off[j];
+      e.block0 = pp.blocks;
+      pp.blocks += dm.KT * ((dm.NT + 15) / 16);
+      done[j] = 1;
+    }
+    HIPCHECK(lw::launch_fused_packed(pp, s));
+    if (launches) ++*launches;
+  }
   for (int i = 0; flat && i < count; ++i) {
     if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
@@ -688,10 +798,10 @@ void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, 
     const long long floor_kb = (long long)floor_mb * 1024;
     size_t used = 0;
     for (auto& t : M->ts) {
-      if (!t.coded()) continue;
+      if (!t.matrix()) continue;
       if (budget_mb > 0 && used + t.nbytes > (size_t)budget_mb * 1048576ull) break;  // forward order: stop
       if (floor_mb > 0 && meminfo_kb("MemAvailable") - (long long)(t.nbytes >> 10) < floor_kb) break;
-      if (!make_resident(*M, t, threads)) {
+      if (!(t.packed() ? make_resident_packed(*M, t) : make_resident(*M, t, threads))) {
         release(M.release());
         return nullptr;
       }
@@ -833,6 +943,9 @@ int rt_test_cpu_decode(void* h, const char* name, int threads, uint8_t* out) {
   Model* M = static_cast<Model*>(h);
   if (!M || !out) return -1;
   Tensor* t = M->find(name);
+  if (t && t->packed()) {  // the stored bytes are the symbols (kernels/llmrt.cu:2547)
+    return pread_all(M->fd, out, (size_t)t->N * t->KS(), t->off) ? 0 : -1;
+  }
   if (!t || !t->coded() || t->pre_il) {
     g_err = std::string(name ? name : "(null)") + ": not a raw coded tensor";
     return -1;
@@ -915,7 +1028,7 @@ int lw_tensor_info(void* h, const char* name, int64_t* out) {
   out[4] = (int64_t)t->nbytes;
   out[5] = t->kqt ? (int64_t)M->ts[t->side_idx].nbytes : 0;
   out[6] = (int64_t)t->dev_bytes;
-  out[7] = t->coded() ? t->T() : 0;
+  out[7] = t->matrix() ? t->T() : 0;
   out[8] = t->resident ? 1 : 0;
   return 0;
 }

@@ -387,6 +387,47 @@ def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):
             assert torch.equal(a[0], b[0]), nm
 
 
+def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
+    """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices),
+    m = 5 and the fp32-x path; its GPU decode returns the codes."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    mats = [("m%d" % kqt, kqt, N, K, H, 20 + kqt) for kqt, N, K, H in
+            ((1, 128, 2048, 2.3), (2, 128, 1024, 3.4), (3, 64, 1024, 4.3), (4, 128, 2048, 2.6))]
+    bundle.write_synthetic_bundle(str(tmp_path / "coded"), mats, threads=4)
+    bundle.write_packed_bundle(str(tmp_path / "packed"), mats, threads=4)
+    with Runtime(tmp_path / "coded") as rc, Runtime(tmp_path / "packed") as rp:
+        names = [m[0] for m in mats]
+        xs = [torch.randn(1, m[3]).half().cuda() for m in mats]
+
+        def group(rt):
+            ys = [torch.zeros(1, m[2], device="cuda") for m in mats]
+            n = len(names)
+            assert rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                              (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                              (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None) == 0
+            torch.cuda.synchronize()
+            return [y.cpu() for y in ys]
+        for (name, kqt, N, K, H, seed), a, b in zip(mats, group(rc), group(rp)):
+            say("packed twin m=1", name)
+            assert torch.equal(a, b), name
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
+            assert np.array_equal(rp.test_decode(name), codes)
+            X5 = torch.randn(5, K).half().cuda()
+            y5c, y5p = torch.zeros(5, N, device="cuda"), torch.zeros(5, N, device="cuda")
+            rc.matmul_dev(name, X5, y5c)
+            rp.matmul_dev(name, X5, y5p)
+            torch.cuda.synchronize()
+            assert torch.equal(y5c, y5p), name
+            X3 = np.random.default_rng(kqt).standard_normal((3, K)).astype(np.float32)
+            yc, yp = rc.test_matmul(name, X3), rp.test_matmul(name, X3)
+            assert np.array_equal(yc, yp), name
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X3.astype(np.float64))
+            check_err(yp, y64, name + " packed fp32 m=3")
+
+
 def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
     """The m = 1 flat kernel: one launch over matrices of different sizes (blocks spanning two matrices and two
     tile columns) gives the same bits as one call per matrix and as the block-per-column ring kernel (mode 2),

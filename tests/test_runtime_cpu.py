@@ -136,3 +136,24 @@ def test_synthetic_bundle_writer(lib, tmp_path, orc):
         sym = orc.decode_lockstep(blob, N, ks)
         assert np.array_equal(orc.unpack_symbols(8 if ks == K else 4, sym), codes)
         assert np.array_equal(bundle.read_tensor(str(tmp_path), by[name + ".kqs"]).reshape(side.shape), side)
+
+
+def test_packed_twin_bundle(lib, tmp_path):
+    """The fixed-rate twin (enc pk4 / pk8, the reference bundler's --packed output): it opens, its CPU decode
+    returns the stored symbols (kernels/llmrt.cu:2547) and a packed blob shorter than N x K is rejected."""
+    from lazyweights_amd import Runtime, bundle
+    mats = [("p4", 1, 64, 1024, 2.3, 5), ("p8", 3, 64, 512, 4.3, 6)]
+    bundle.write_packed_bundle(str(tmp_path / "ok"), mats, threads=2)
+    cfg, ts = bundle.read_manifest(str(tmp_path / "ok"))
+    assert {t["name"]: t["enc"] for t in ts if not t["name"].endswith(".kqs")} == {"p4": "pk4", "p8": "pk8"}
+    with Runtime(tmp_path / "ok", budget_mb=0) as rt:
+        for name, kqt, N, K, H, seed in mats:
+            codes, _ = bundle.synth_matrix(kqt, N, K, H, seed)
+            assert np.array_equal(rt.test_cpu_decode(name, 2), bundle.form_symbols(kqt, codes))
+    w = bundle.Writer(str(tmp_path / "bad"))
+    codes, side = bundle.synth_matrix(1, 64, 1024, 2.3, 5)
+    w.add("p4", "pk4", 64, 1024, 1.0, 0, bundle.form_symbols(1, codes).tobytes()[:-1])
+    w.add("p4.kqs", "kq_Q4_K", 64, side.shape[1], 1.0, 0, side.tobytes())
+    w.close()
+    with pytest.raises(RuntimeError, match="packed blob shorter"):
+        Runtime(tmp_path / "bad", budget_mb=0)
