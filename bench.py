@@ -108,6 +108,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--no-packed", action="store_true", help="skip the packed-twin control")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-shape (m = 128) figure")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
@@ -215,6 +216,31 @@ def main():
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
 
+        # prefill shapes (m = 128, fp32 x resident): the decode-to-scratch path with its GEMM on the matrix cores,
+        # over layer 0's seven matrices (a reported figure, not the metric)
+        prefill = None
+        if not a.no_prefill:
+            pm = 128
+            XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
+            YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
+
+            def prefill_layer():
+                for i in range(7):
+                    if lib.lw_matmul_dev(rt.h, names[i], ctypes.c_void_p(XP[i].data_ptr()), 0, pm,
+                                         ctypes.c_void_p(YP[i].data_ptr()), infos[i]["N"], stream) != 0:
+                        raise RuntimeError(lib.lw_last_error().decode())
+            prefill_layer()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(5):
+                prefill_layer()
+            torch.cuda.synchronize()
+            fms = (time.perf_counter() - t0) * 1e3 / 5
+            flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos[:7])
+            prefill = {"m": pm, "ms_per_layer": round(fms, 3), "TFLOPs": round(flops / (fms * 1e-3) / 1e12, 1),
+                       "path": "decode to scratch + v_mfma_f32_32x32x8f16 GEMM (fp16 hi + lo x)"}
+            log("bench: prefill m=%d: %.3f ms per layer, %.1f TFLOP/s" % (pm, fms, prefill["TFLOPs"]))
+
         # packed-twin control: the same codes stored fixed-rate (pk4 / pk8), no decode chain; the achievable rate of
         # this access pattern and arithmetic without entropy decoding (the reference's pk4 baseline)
         packed = None
@@ -303,6 +329,7 @@ def main():
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
             "control_packed_twin": packed,
+            "prefill_path2": prefill,
         }
         print(json.dumps(res), flush=True)
         rt.close()

@@ -121,6 +121,9 @@ hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStr
 // simple K-quant GEMM from decoded codes (m > 8 or path 2): Y[m][N] = X[m][K] dequant(codes, side)^T
 hipError_t launch_gemm_codes(const DevMat& M, const uint8_t* codes, int row0, int nrows, const float* X, int m,
                              float* Y, int ldy, hipStream_t s);
+// the same on the matrix cores, with X16 = fp16 hi / lo rows [2m][K] (launch_split_x), rows [row0, row0 + nrows)
+hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row0, int nrows, const void* X16, int m,
+                                  float* Y, int ldy, hipStream_t s);
 // streaming read of n16 16-byte words (achievable HBM bandwidth control); out gets one value per block
 hipError_t launch_stream_read(const void* src, size_t n16, float* out, int blocks, hipStream_t s);
 

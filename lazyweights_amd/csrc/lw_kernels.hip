@@ -28,6 +28,7 @@ constexpr int GUARD_BITS = 2;
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f16x16 __attribute__((ext_vector_type(16)));
 
 // Activations of MT pseudo-tokens staged in LDS as fp16 pairs: pair c (weights 2c, 2c + 1) of token j. With
 // MT >= 4 (the MFMA path) the two pairs of one 4-weight step are adjacent per token, so a lane reads its token's
@@ -1591,6 +1592,91 @@ hipError_t launch_gemm_codes(const DevMat& M, const uint8_t* codes, int row0, in
     case KQ_Q5_K: hipLaunchKernelGGL(k_gemm_codes<KQ_Q5_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, X, m, Y, ldy); break;
     case KQ_Q6_K: hipLaunchKernelGGL(k_gemm_codes<KQ_Q6_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, X, m, Y, ldy); break;
     case KQ_IQ4_XS: hipLaunchKernelGGL(k_gemm_codes<KQ_IQ4_XS>, grid, dim3(256), 0, s, M, codes, row0, nrows, X, m, Y, ldy); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ── prefill GEMM on the matrix cores (path 2, m > 16): decoded codes x fp16 hi + lo activations ──────────
+// Y[t][n] = sum over sub-blocks of s_n (x_t . f(q_n)) - o_n (sum x_t), as k_gemm_codes, with both sums on
+// v_mfma_f32_32x32x8f16. Block = 4 waves = 64 rows x 64 tokens, wave = 32 x 32. In a block of 32 lanes the MFMA
+// takes A[i][k] (token i, 8 weights) from lane i + 32 (k / 4) and B[k][j] (row j) from lane j + 32 (k / 4), and
+// leaves D[i][j] in lane j + 32 h, register r, i = 8 (r / 4) + 4 h + r % 4 (checked on the GPU): every lane holds
+// one row (its scales) and 16 tokens. Products are exact (f(q) and the hi / lo halves of x are fp16, fp32 sums);
+// the activation sums come from a second MFMA with B = 1.
+template <int KQ>
+__global__ void __launch_bounds__(256) k_gemm_codes_mfma(DevMat M, const uint8_t* __restrict__ codes, int row0,
+                                                         int nrows, const uint16_t* __restrict__ X16, int m,
+                                                         float* __restrict__ Y, int ldy) {
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr bool MINS = KQ == KQ_Q4_K || KQ == KQ_Q5_K;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int nl = blockIdx.x * 64 + (wave & 1) * 32 + c;   // the lane's row (relative to row0)
+  const int t0 = blockIdx.y * 64 + (wave >> 1) * 32;       // the wave's first token
+  const int K = M.K;
+  const int nls = min(nl, nrows - 1);                      // rows past the end compute row nrows - 1, unstored
+  const int ta = min(t0 + c, m - 1);                       // the lane's token for A (clamped likewise)
+  const uint8_t* cr = codes + (size_t)nls * K + 4 * h;
+  const uint16_t* xh = X16 + (size_t)(2 * ta) * K + 4 * h;
+  const uint16_t* xl = X16 + (size_t)(2 * ta + 1) * K + 4 * h;
+  const h4v ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+  f16x16 tot = {};
+  for (int b = 0; b < K / 256; ++b) {
+    uint32_t sw[5];
+    side_load<KQ>(M.side + side_record(row0 + nls, b, M.KT, M.symbits == 4 ? 2 : 1) * SB, sw);
+    for (int jj = 0; jj < 256 / GW; ++jj) {
+      float sc, o;
+      side_scale<KQ>(sw, jj, sc, o);
+      f16x16 d1 = {}, d2 = {};
+#pragma unroll
+      for (int ks = 0; ks < GW / 8; ++ks) {
+        const int k = b * 256 + jj * GW + ks * 8;
+        const uint32_t q = *reinterpret_cast<const uint32_t*>(cr + k);
+        float w0 = (float)(q & 255u), w1 = (float)((q >> 8) & 255u);  // v_cvt_f32_ubyte0..3
+        float w2 = (float)((q >> 16) & 255u), w3 = (float)(q >> 24);
+        if (KQ == KQ_Q6_K) {
+          w0 -= 32.f;
+          w1 -= 32.f;
+          w2 -= 32.f;
+          w3 -= 32.f;
+        } else if (KQ == KQ_IQ4_XS) {
+          w0 = (float)IQ4_GRID[q & 15u];
+          w1 = (float)IQ4_GRID[(q >> 8) & 15u];
+          w2 = (float)IQ4_GRID[(q >> 16) & 15u];
+          w3 = (float)IQ4_GRID[(q >> 24) & 15u];
+        }
+        const h4v wv = {(_Float16)w0, (_Float16)w1, (_Float16)w2, (_Float16)w3};
+        const h4v ah = __builtin_bit_cast(h4v, *reinterpret_cast<const uint2*>(xh + k));
+        const h4v al = __builtin_bit_cast(h4v, *reinterpret_cast<const uint2*>(xl + k));
+        d1 = __builtin_amdgcn_mfma_f32_32x32x8f16(ah, wv, d1, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_32x32x8f16(al, wv, d1, 0, 0, 0);
+        if (MINS) {
+          d2 = __builtin_amdgcn_mfma_f32_32x32x8f16(ah, ones, d2, 0, 0, 0);
+          d2 = __builtin_amdgcn_mfma_f32_32x32x8f16(al, ones, d2, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tot[r] = MINS ? tot[r] + (sc * d1[r] - o * d2[r]) : tot[r] + sc * d1[r];
+    }
+  }
+  if (nl >= nrows) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int t = t0 + 8 * (r / 4) + 4 * h + (r % 4);
+    if (t < m) Y[(size_t)t * ldy + row0 + nl] = tot[r];
+  }
+}
+
+hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row0, int nrows, const void* X16, int m,
+                                  float* Y, int ldy, hipStream_t s) {
+  if (nrows < 1 || m < 1) return hipErrorInvalidValue;
+  const dim3 grid((nrows + 63) / 64, (m + 63) / 64);
+  const uint16_t* x = static_cast<const uint16_t*>(X16);
+  switch (M.kqt) {
+    case KQ_Q4_K: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_Q4_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
+    case KQ_Q5_K: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_Q5_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
+    case KQ_Q6_K: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_Q6_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
+    case KQ_IQ4_XS: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_IQ4_XS>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -730,15 +730,24 @@ int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, in
 }
 
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
+// (the GEMM on the matrix cores over fp16 hi + lo activations; kernel mode 1 keeps the SIMT GEMM)
 int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
   const size_t row_bytes = (size_t)lw::TN * t.K;
   const size_t cap = std::max(row_bytes, std::min<size_t>((size_t)t.N * t.K, (size_t)64 << 20));
   if (grow(M.codes, M.codes_cap, cap)) return -1;
+  const bool mfma = g_kernel_mode != 1;
+  if (mfma) {
+    if (grow(M.X16, M.X16_cap, (size_t)2 * m * t.K * 2)) return -1;
+    HIPCHECK(lw::launch_split_x(X, M.X16, m, (int)t.K, s));
+  }
   const int rows_fit = (int)std::max<size_t>(1, M.codes_cap / row_bytes);
   for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit) {
     const int tr1 = std::min(t.dm.NT, tr0 + rows_fit);
     HIPCHECK(lw::launch_decode(t.dm, M.codes, tr0, tr1, s));
-    HIPCHECK(lw::launch_gemm_codes(t.dm, M.codes, tr0 * lw::TN, (tr1 - tr0) * lw::TN, X, m, Y, ldy, s));
+    if (mfma)
+      HIPCHECK(lw::launch_gemm_codes_mfma(t.dm, M.codes, tr0 * lw::TN, (tr1 - tr0) * lw::TN, M.X16, m, Y, ldy, s));
+    else
+      HIPCHECK(lw::launch_gemm_codes(t.dm, M.codes, tr0 * lw::TN, (tr1 - tr0) * lw::TN, X, m, Y, ldy, s));
   }
   return 0;
 }
@@ -1049,10 +1058,11 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
     }
     return fused_dev(*M, *t, X, m, 1, Y, ldy, s);
   }
-  if (m < 1 || m > 8) {
-    g_err = "lw_matmul_dev: fp32 activations need 1 <= m <= 8";
+  if (m < 1) {
+    g_err = "lw_matmul_dev: m < 1";
     return -1;
   }
+  if (m > 8) return decode_gemm_dev(*M, *t, static_cast<const float*>(X), m, Y, ldy, s);  // prefill shapes
   if (grow(M->X16, M->X16_cap, (size_t)2 * m * t->K * 2)) return -1;
   HIPCHECK(lw::launch_split_x(static_cast<const float*>(X), M->X16, m, (int)t->K, s));
   return fused_dev(*M, *t, M->X16, m, 2, Y, ldy, s);

@@ -121,6 +121,26 @@ def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
 
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
+    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) on the matrix cores against fp64, and
+    against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
+    rt, mats = fmt_rt
+    mat = mats[fmt]
+    rng = np.random.default_rng(30 + kqt)
+    X = rng.uniform(-1, 1, (80, mat[3])).astype(np.float32)
+    _, y64 = reference_y(orc, mat, X.astype(np.float64))
+    say("prefill m=80", fmt)
+    Y = rt.test_matmul(fmt, X, path=2)
+    check_err(Y, y64, fmt + " prefill m=80")
+    assert rt.lib.lw_set_kernel_mode(1) == 0
+    try:
+        Ys = rt.test_matmul(fmt, X, path=2)
+    finally:
+        rt.lib.lw_set_kernel_mode(0)
+    assert np.abs(Y - Ys).max() <= 1e-5 * np.abs(Ys).max()
+
+
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_fused_fp16_x_device(fmt_rt, orc, kqt, fmt, H):
     """lw_matmul_dev with fp16 activations resident on the GPU (the bench path), m up to 16."""
     import torch
