@@ -95,6 +95,19 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
+/* Int8 activations for m = 1 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev and
+ * lw_group_matmul_dev quantize x per block of 32 (d = max|x| / 127, q = x / d rounded to nearest even, plus d sum q)
+ * and the fused kernels take integer dot products per sub-block, y += s d acc - o d sum q. Replaces the reference's
+ * act8 switch (kernels/llmrt.cu:2221, LLMRT_FP_ACT; kernels k_quant_x8 / k_gemvm_kq8 at kernels/llmrt.cu:1035-1169),
+ * which is on by default there and also covers 2 <= m <= 8; here m > 1 keeps fp16 activations. Needs kernel mode
+ * 0, 3, 4 or 5 (the flat kernels). Returns 0 or -1. */
+int lw_set_act8(int on);
+
+/* The int8 quantization of lw_set_act8 on host buffers (test entry, runs the device kernel): X [m, K] fp32 or fp16
+ * (x_f16) -> xq [m, K] int8, dx [m, K / 32] = max|x| / 127 per block, sx [m, K / 32] = dx * sum of the block's q
+ * (kernels/llmrt.cu:1035-1055). Returns 0 or -1. */
+int lw_test_quant_x8(const void* X, int x_f16, int m, int K, int8_t* xq, float* dx, float* sx);
+
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in
  * names/X/Y (group g has sizes[g] matrices), cycling through the groups, with HIP events on the launch stream.
  * out[0] = mean ms per pass over all groups, out[1] = mean ms per pass of the groups' kernels alone (events around

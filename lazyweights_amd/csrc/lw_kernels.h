@@ -18,6 +18,7 @@ namespace lw {
 struct DevMat {
   const uint16_t* lut;
   const uint32_t* lut4;  // the ring kernels' 4-byte table entries (decode_table4 in lw_layout.h); null if kqt == 0
+  const uint32_t* luti8; // the same with int8 grid values (decode_table_i8), for int8 activations
   const uint32_t* tbase;
   const uint16_t* mid;
   const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency kernel (Layout::split)
@@ -68,6 +69,10 @@ struct FlatEntry {
   // in the launch by the last wave of each tile row; cnt = NT zeroed counters (left zeroed)
   float* Y;
   uint32_t* cnt;
+  // int8 activations (plan.i8): x quantized per 32 weights (launch_quant_x8): XQ [K] int8, DX / SX [K / 32]
+  const int8_t* XQ;
+  const float* DX;
+  const float* SX;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];
@@ -77,11 +82,15 @@ struct FlatPlan {
   // 16-row launches: spare 16-row ring pairs per block for exception tiles with a 32-row schedule (>= the most
   // such tiles in any block); 0: exception tiles are skipped (decoded by an exception pass)
   int nspare;
+  int i8;  // 1: int8 activations (the entries' XQ / DX / SX), m = 1
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
 // The low-latency kernel over the same kind of plan (one tile per block of 4 waves, 8 chains per lane; W and
 // nspare are ignored; exception tiles included). Every matrix needs a K-quant table and the split offsets.
 hipError_t launch_fused_split(const FlatPlan& plan, hipStream_t s);
+// int8 activations as the reference's k_quant_x8 (kernels/llmrt.cu:1035-1055): X [m][K] (fp32, or fp16 when x_f16)
+// in blocks of 32: d = amax / 127, q = round-to-nearest-even(x / d) (0 when d = 0), XQ = q, DX = d, SX = d sum q.
+hipError_t launch_quant_x8(const void* X, int x_f16, int m, int K, int8_t* XQ, float* DX, float* SX, hipStream_t s);
 // LDS rows the low-latency kernel stages per tile for this plan (max over its matrices of max_rows + 2)
 int split_stage_rows(const FlatPlan& plan);
 

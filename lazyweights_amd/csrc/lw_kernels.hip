@@ -822,6 +822,94 @@ __device__ __forceinline__ XgRegs column_xsums(const uint32_t* X2, int tc, int l
   return xgr;
 }
 
+// ── int8 activations (m = 1), the reference's k_quant_x8 + k_gemvm_kq8 (kernels/llmrt.cu:1035-1169) ───────
+// Quantization: one block of 32 activations per half-wave.
+__global__ void __launch_bounds__(256) k_quant_x8(const void* __restrict__ X, int x_f16, int8_t* __restrict__ XQ,
+                                                  float* __restrict__ DX, float* __restrict__ SX, int nb) {
+  const int b = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  if (b >= nb) return;  // a half-wave's exchanges stay inside it (xor offsets < 32)
+  const size_t i = (size_t)b * 32 + l;
+  const float v = x_f16 ? h2f(static_cast<const uint16_t*>(X)[i]) : static_cast<const float*>(X)[i];
+  float a = fabsf(v);
+#pragma unroll
+  for (int o = 16; o; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+  const float d = a / 127.f;
+  const int q = d > 0.f ? (int)rintf(v / d) : 0;  // round to nearest even, as __float2int_rn
+  int sm = q;
+#pragma unroll
+  for (int o = 16; o; o >>= 1) sm += __shfl_xor(sm, o);
+  XQ[i] = (int8_t)q;
+  if (l == 0) {
+    DX[b] = d;
+    SX[b] = d * (float)sm;
+  }
+}
+
+hipError_t launch_quant_x8(const void* X, int x_f16, int m, int K, int8_t* XQ, float* DX, float* SX, hipStream_t s) {
+  if (m < 1 || K % 32) return hipErrorInvalidValue;
+  const int nb = m * K / 32;
+  hipLaunchKernelGGL(k_quant_x8, dim3((nb + 7) / 8), dim3(256), 0, s, X, x_f16, XQ, DX, SX, nb);
+  return hipGetLastError();
+}
+
+// One tile's int8-activation GEMV from a symbol source (table entries from decode_table_i8): per sub-block an
+// integer dot product of the int8 grid values with the quantized x (v_dot4_i32_i8, 4 weights per step), then
+// y += s d_x acc - o s_x with s = d sc, o = dmin m per sub-block and d_x, s_x of the sub-block's 32-block.
+// xq4 = the tile column's quantized x as 4-byte words, dx / sx its 32-block scales (scalar loads).
+template <int KQ, class Src>
+__device__ __forceinline__ void tile_gemv_i8(Src& src, __attribute__((address_space(4))) const uint32_t* xq4,
+                                             __attribute__((address_space(4))) const float* dx,
+                                             __attribute__((address_space(4))) const float* sx,
+                                             const uint8_t* srow, float* out) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr int NSB = TW / 256, GPS = 16 / NSB, NSUB = 256 / GW, GPSUB = GPS / NSUB;
+  float tot = 0.f;
+#pragma unroll 1
+  for (int sb = 0; sb < NSB; ++sb) {
+    uint32_t sw[5];
+    side_load<KQ>(srow + sb * (TN * SB), sw);
+    float dA, dB, mf[8];
+    uint64_t scq, scq2;
+    side_packed<KQ>(sw, scq, scq2, dA, dB);
+    if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw, mf);
+    int acc = 0;
+    uint32_t wprev = 0;
+#pragma unroll 1
+    for (int gg2 = 0; gg2 < GPS; gg2 += 2) {
+      if (KQ == KQ_Q6_K && gg2 == 8) scq = scq2;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int g = sb * GPS + gg2 + h;
+        src.stage(g);
+#pragma unroll 8
+        for (int p = 0; p < 8; ++p) {
+          uint32_t e1, e2;
+          src.pair(p, e1, e2);
+          if (SYMB == 4) {
+            acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2, e1, 0x07060302u), (int)xq4[8 * g + p], acc, false);
+          } else {
+            const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);  // f(q1), f(q2) in bytes 0, 1
+            if (p & 1) acc = __builtin_amdgcn_sdot4((int)(wprev | (w2 << 16)), (int)xq4[4 * g + p / 2], acc, false);
+            else wprev = w2;
+          }
+        }
+        if (GPSUB == 1 || h == 1) {  // sub-block end
+          const int jj = (gg2 + h) / GPSUB, xb = (sb * 256 + jj * GW) / 32;
+          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                               : (float)(uint32_t)(scq & 255u);
+          scq >>= 8;
+          tot = fmaf(dA * scv * dx[xb], (float)acc, tot);
+          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+          acc = 0;
+        }
+      }
+    }
+  }
+  __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ── packed (fixed-rate) twin: decode-free fused GEMV / skinny GEMM ─────────────────────────────────────────
 // The control the reference keeps beside its coded bundles (enc pk4 / pk8, kernels/llmrt.cu:538-630, 1731-1777):
 // the same codes stored as plain bytes, so the kernel reads 4 (pk4) or 8 (pk8) bits per weight instead of the
@@ -883,10 +971,26 @@ __global__ void __launch_bounds__(1024, MT <= 2 ? 2 : 1) k_fused_packed(GroupPla
     tile_gemv<KQ, MT>(src, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, mt, N, out);
 }
 
+// m = 1 tile of a flat launch: fp16 activations (tile_gemv) or int8 activations (tile_gemv_i8, the entry's XQ / DX /
+// SX for tile column tc)
+template <int KQ, bool I8, class Src, class KEntryRef>
+__device__ __forceinline__ void tile_body(Src& src, const KEntryRef& E, int tc, const XgRegs& xgr,
+                                          __attribute__((address_space(4))) const uint32_t* xcol, const uint8_t* srow,
+                                          int N, float* out) {
+  constexpr int TW = kq_symbits(KQ) == 4 ? 2 * TK : TK;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  typedef __attribute__((address_space(4))) const float KF32;
+  if (I8)
+    tile_gemv_i8<KQ>(src, (KU32*)(E.XQ + (size_t)tc * TW), (KF32*)(E.DX + (size_t)tc * (TW / 32)),
+                     (KF32*)(E.SX + (size_t)tc * (TW / 32)), srow, out);
+  else
+    tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
+}
+
 // The packed twin for m = 1 over a flat tile list, as k_fused_flat: block b decodes tiles [b W, b W + W), one per
 // wave, x through the scalar cache, the reduction over tile columns in the launch. A block spans at most two
 // matrices: both symbol tables sit in LDS.
-template <int KQ>
+template <int KQ, bool I8>
 __global__ void __launch_bounds__(1024) k_fused_packed_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -906,8 +1010,11 @@ __global__ void __launch_bounds__(1024) k_fused_packed_flat(FlatPlan plan) {
   }
   KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
-  if (threadIdx.x < 256) tab[threadIdx.x] = ea->M.lut4[threadIdx.x];
-  else if (threadIdx.x < 512 && mb != ma) tab[threadIdx.x] = eb->M.lut4[threadIdx.x - 256];
+  // the tables (blocks of W = 1..16 waves: any number of threads)
+  for (int i = threadIdx.x; i < 256; i += W * 64) {
+    tab[i] = (I8 ? ea->M.luti8 : ea->M.lut4)[i];
+    if (mb != ma) tab[256 + i] = (I8 ? eb->M.luti8 : eb->M.lut4)[i];
+  }
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int T = T0 + wave;
@@ -921,21 +1028,23 @@ __global__ void __launch_bounds__(1024) k_fused_packed_flat(FlatPlan plan) {
   const int t = (u % NT) * KT + u / NT;
   const int tc = t % KT, tr = t / KT;
   const int lane = threadIdx.x & 63;
-  const XgRegs xgr = column_xsums<KQ>(E.X2, tc, lane);
+  XgRegs xgr;
+  if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
   KU32* xcol = (KU32*)(E.X2 + (size_t)tc * NPAIR);
   const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * SB + (uint32_t)(lane * SB);
   float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
-  uint32_t* xw = reinterpret_cast<uint32_t*>(pk_rings + W * PK_SLOTS * 64) + wave * NPAIR;
+  // int8 activations: x through the scalar cache (tile_gemv_i8), nothing staged
+  uint32_t* xw = I8 ? nullptr : reinterpret_cast<uint32_t*>(pk_rings + W * PK_SLOTS * 64) + wave * NPAIR;
   PackedSrc<KQ> src(reinterpret_cast<const uint4*>(M.words) + (size_t)t * 16 * 64 + (uint32_t)lane,
                     pk_rings + wave * PK_SLOTS * 64, tab + (second ? 256 : 0), (uint32_t)lane,
                     E.X2 + (size_t)tc * NPAIR, xw);
-  tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
+  tile_body<KQ, I8>(src, E, tc, xgr, xcol, srow, N, out);
   row_reduce(E, tr, KT, N, lane);
 }
 
 // ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
 // One tile of the flat kernel: lanes of front f stage into `ring` (RS rows of 32 words).
-template <int KQ, class KEntryRef>
+template <int KQ, bool I8, class KEntryRef>
 __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4& sc, uint32_t* ring, uint32_t rmask,
                                           const uint32_t* lut4, uint32_t lutsel, const XgRegs& xgr, int lane) {
   constexpr int SYMB = kq_symbits(KQ);
@@ -964,7 +1073,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.rmask = rmask;
     st.init((int)init0);
     RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
-    tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
+    tile_body<KQ, I8>(src, E, tc, xgr, xcol, srow, N, out);
   } else {
     RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
@@ -973,7 +1082,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.rmask = rmask;
     st.init((int)(f ? init1 : init0));
     RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
-    tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
+    tile_body<KQ, I8>(src, E, tc, xgr, xcol, srow, N, out);
   }
   row_reduce(E, tr, KT, N, lane);
 }
@@ -987,7 +1096,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
 // Exception tiles (no 16-row schedule) are skipped, except with plan.nspare > 0 in a 16-row launch: then a tile
 // with a 32-row schedule is decoded in place, front 0 in the wave's own two rings (4 KB) and front 1 in spare ring
 // k of the block, k = the number of such tiles before it in the block (the host sizes nspare to the block maximum).
-template <int KQ, int RS, int NTAB>
+template <int KQ, int RS, int NTAB, bool I8>
 __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -1010,10 +1119,11 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
   const int NTHR = blockDim.x;
-  for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(ea->M.lut4)[i];
+  const uint4* ta = reinterpret_cast<const uint4*>(I8 ? ea->M.luti8 : ea->M.lut4);
+  const uint4* tb = reinterpret_cast<const uint4*>(I8 ? eb->M.luti8 : eb->M.lut4);
+  for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4)[i] = ta[i];
   if (NTAB > 1 && mb != ma)
-    for (int i = threadIdx.x; i < LUTN / 4; i += NTHR)
-      reinterpret_cast<uint4*>(lut4 + LUTN)[i] = reinterpret_cast<const uint4*>(eb->M.lut4)[i];
+    for (int i = threadIdx.x; i < LUTN / 4; i += NTHR) reinterpret_cast<uint4*>(lut4 + LUTN)[i] = tb[i];
   __syncthreads();
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1045,14 +1155,15 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
     if (spare >= plan.nspare) return;  // cannot happen with the host's sizing; never overrun the spare rings
   }
 
-  const XgRegs xgr = column_xsums<KQ>(E.X2, tc, lane);
+  XgRegs xgr;
+  if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
 
   // the ring of the lane's front: 16-row launches place a 32-row exception tile's front 0 in the wave's two rings
   // and its front 1 in spare ring pair `spare`
   const int f = lane >> 5;
   const bool x32 = RS == 16 && spare >= 0;
   uint32_t* ring = rings + (x32 ? (f ? 2 * W + 2 * spare : 2 * wave) : 2 * wave + f) * RING_WORDS;
-  flat_tile<KQ>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane);
+  flat_tile<KQ, I8>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane);
 }
 
 // ── low-latency kernel (m = 1): one tile per block, 8 chains per lane ───────────────────────────────────
@@ -1063,7 +1174,7 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
 // register window reading the tile image directly. Each chain stores its sub-block dot products in LDS; wave 0
 // then forms each row's partial exactly as tile_gemv does (same operations in the same order), so the result has
 // the same bits as the ring kernels'. Exception tiles need nothing special: no staging schedule is involved.
-template <int KQ>
+template <int KQ, bool I8>
 __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_rows) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -1097,7 +1208,8 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;
   const int tc = t % KT, tr = t / KT;
   const int R = min((int)M.rows[t] + 2, stage_rows);  // rows read: up to 2 past the longest lane's last row
-  for (int i = threadIdx.x; i < LUTN / 4; i += 256) reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
+  const uint4* tab = reinterpret_cast<const uint4*>(I8 ? M.luti8 : M.lut4);
+  for (int i = threadIdx.x; i < LUTN / 4; i += 256) reinterpret_cast<uint4*>(lut4)[i] = tab[i];
   const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
   for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
   __syncthreads();
@@ -1112,7 +1224,7 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   if (wave == 0) {
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
-    xgr = column_xsums<KQ>(E.X2, tc, lane);
+    if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
   }
   {
     // chain of lane front f: symbols [64 wave, 64 wave + 64) of row l + 32 f, i.e. stream symbols 256 f + 64 wave..
@@ -1124,12 +1236,15 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
     uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
     asm volatile("" : "+v"(rlb));
     KU32* xcol = (KU32*)(E.X2 + (size_t)tc * (TW / 2));
+    KU32* xq4 = (KU32*)(E.XQ + (size_t)tc * TW);
     uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
     uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
     uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
     uint32_t C = *(LdsU32*)(rlb + (slot << 7));
     float* accrow = accb + (f * 32 + l) * NSUBT;
     float acc = 0.f;
+    int iacc = 0;
+    uint32_t wprev = 0;
 #pragma unroll 1
     for (int gi = 0; gi < 4; ++gi) {
       const int g = 4 * wave + gi;  // 16-symbol group within the row
@@ -1146,7 +1261,15 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
         B = slide ? C : B;
         slot = nslot;
         C = *(LdsU32*)(rlb + (nslot << 7));
-        if (SYMB == 4) {
+        if (I8) {  // as tile_gemv_i8
+          if (SYMB == 4) {
+            iacc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2, e1, 0x07060302u), (int)xq4[8 * g + p], iacc, false);
+          } else {
+            const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);
+            if (p & 1) iacc = __builtin_amdgcn_sdot4((int)(wprev | (w2 << 16)), (int)xq4[4 * g + p / 2], iacc, false);
+            else wprev = w2;
+          }
+        } else if (SYMB == 4) {
           const uint32_t v1 = __builtin_amdgcn_perm(e1, e1, 0x0C030C02u), v2 = __builtin_amdgcn_perm(e2, e2, 0x0C030C02u);
           const int c = 16 * g + 2 * p;
           acc = dot2(v2, xcol[c + 1], dot2(v1, xcol[c], acc));
@@ -1156,8 +1279,9 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
         }
       }
       if (GPSUB == 1 || (gi & 1)) {
-        accrow[g / GPSUB] = acc;
+        accrow[g / GPSUB] = I8 ? (float)iacc : acc;  // |iacc| < 2^24: exact
         acc = 0.f;
+        iacc = 0;
       }
     }
   }
@@ -1168,8 +1292,30 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   // the sub-block dot products in order
   const float* accrow = accb + lane * NSUBT;
   float tot = 0.f;
+  if (I8) {  // tile_gemv_i8's order: per sub-block s d_x acc, then - o s_x
+    typedef __attribute__((address_space(4))) const float KF32;
+    KF32* dx = (KF32*)(E.DX + (size_t)tc * (TW / 32));
+    KF32* sx = (KF32*)(E.SX + (size_t)tc * (TW / 32));
 #pragma unroll
-  for (int sb = 0; sb < NSB; ++sb) {
+    for (int sb = 0; sb < NSB; ++sb) {
+      float dA, dB, mf[8];
+      uint64_t scq, scq2;
+      side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+      if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
+#pragma unroll
+      for (int jj = 0; jj < NSUB; ++jj) {
+        if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+        const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                             : (float)(uint32_t)(scq & 255u);
+        scq >>= 8;
+        const int xb = (sb * 256 + jj * GW) / 32;
+        tot = fmaf(dA * scv * dx[xb], accrow[sb * NSUB + jj], tot);
+        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+      }
+    }
+  }
+#pragma unroll
+  for (int sb = 0; !I8 && sb < NSB; ++sb) {
     float dA, dB;
     uint64_t scq, scq2;
     side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
@@ -1202,14 +1348,19 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   row_reduce(E, tr, KT, N, lane);
 }
 
-template <int KQ>
-static hipError_t split_launch(const FlatPlan& p, int stage_rows, hipStream_t s) {
+template <int KQ, bool I8>
+static hipError_t split_launch_t(const FlatPlan& p, int stage_rows, hipStream_t s) {
   const size_t smem = (size_t)stage_rows * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_split<KQ>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_split<KQ, I8>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_fused_split<KQ>, dim3(p.ntiles), dim3(256), smem, s, p, stage_rows);
+  hipLaunchKernelGGL((k_fused_split<KQ, I8>), dim3(p.ntiles), dim3(256), smem, s, p, stage_rows);
   return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t split_launch(const FlatPlan& p, int stage_rows, hipStream_t s) {
+  return p.i8 ? split_launch_t<KQ, true>(p, stage_rows, s) : split_launch_t<KQ, false>(p, stage_rows, s);
 }
 
 int split_stage_rows(const FlatPlan& p) {
@@ -1225,7 +1376,8 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
     if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || e.tile0 + e.ntile != end || e.ntile < 1 ||
-        (!e.list && e.ntile != e.M.NT * e.M.KT) || (i == 0 && e.tile0 != 0))
+        (!e.list && e.ntile != e.M.NT * e.M.KT) || (i == 0 && e.tile0 != 0) ||
+        (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
       return hipErrorInvalidValue;
   }
   const int rows = split_stage_rows(p);
@@ -1239,21 +1391,22 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
   }
 }
 
-template <int KQ, int RS, int NTAB>
+template <int KQ, int RS, int NTAB, bool I8>
 static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
   const size_t smem = (size_t)(p.W + p.nspare) * 2 * RS * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB, I8>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + p.W - 1) / p.W;
-  hipLaunchKernelGGL((k_fused_flat<KQ, RS, NTAB>), dim3(blocks), dim3(p.W * 64), smem, s, p);
+  hipLaunchKernelGGL((k_fused_flat<KQ, RS, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p);
   return hipGetLastError();
 }
 
 // one-wave blocks never span two matrices: one table
 template <int KQ, int RS>
 static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
-  return p.W == 1 ? flat_launch_t<KQ, RS, 1>(p, s) : flat_launch_t<KQ, RS, 2>(p, s);
+  if (p.i8) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true>(p, s) : flat_launch_t<KQ, RS, 2, true>(p, s);
+  return p.W == 1 ? flat_launch_t<KQ, RS, 1, false>(p, s) : flat_launch_t<KQ, RS, 2, false>(p, s);
 }
 
 hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
@@ -1264,7 +1417,8 @@ hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
     const DevMat& M = e.M;
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
     if (M.kqt != kqt || M.ring_rows != rs || !M.sched || !M.lut4 || e.tile0 + e.ntile != end || e.ntile < p.W ||
-        (!e.list && e.ntile != M.NT * M.KT) || (i == 0 && e.tile0 != 0))
+        (!e.list && e.ntile != M.NT * M.KT) || (i == 0 && e.tile0 != 0) ||
+        (p.i8 && (!M.luti8 || !e.XQ || !e.DX || !e.SX)))
       return hipErrorInvalidValue;
   }
   if (rs != 16 && rs != 32) return hipErrorInvalidValue;
@@ -1315,13 +1469,18 @@ hipError_t launch_fused_packed(const GroupPlan& p, hipStream_t s) {
   }
 }
 
-template <int KQ>
-static hipError_t packed_flat_launch(const FlatPlan& p, int blocks, size_t smem, hipStream_t s) {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_packed_flat<KQ>),
+template <int KQ, bool I8>
+static hipError_t packed_flat_launch_t(const FlatPlan& p, int blocks, size_t smem, hipStream_t s) {
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_packed_flat<KQ, I8>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_fused_packed_flat<KQ>, dim3(blocks), dim3(p.W * 64), smem, s, p);
+  hipLaunchKernelGGL((k_fused_packed_flat<KQ, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p);
   return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t packed_flat_launch(const FlatPlan& p, int blocks, size_t smem, hipStream_t s) {
+  return p.i8 ? packed_flat_launch_t<KQ, true>(p, blocks, smem, s) : packed_flat_launch_t<KQ, false>(p, blocks, smem, s);
 }
 
 hipError_t launch_fused_packed_flat(const FlatPlan& p, hipStream_t s) {
@@ -1331,7 +1490,7 @@ hipError_t launch_fused_packed_flat(const FlatPlan& p, hipStream_t s) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
     if (e.M.kqt != kqt || !e.M.packed || !e.M.lut4 || e.list || e.tile0 + e.ntile != end || e.ntile < p.W ||
-        e.ntile != e.M.NT * e.M.KT || (i == 0 && e.tile0 != 0))
+        e.ntile != e.M.NT * e.M.KT || (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
       return hipErrorInvalidValue;
   }
   const int blocks = (p.ntiles + p.W - 1) / p.W;

@@ -423,4 +423,18 @@ void decode_table4(int kqt, const uint16_t* lut, uint32_t* out) {
   }
 }
 
+void decode_table_i8(int kqt, const uint16_t* lut, uint32_t* out) {
+  auto f = [kqt](uint32_t q) -> uint32_t {
+    const int v = kqt == KQ_IQ4_XS ? IQ4_GRID[q & 15] : kqt == KQ_Q6_K ? (int)q - 32 : (int)q;
+    return (uint32_t)(uint8_t)(int8_t)v;
+  };
+  for (int i = 0; i < LUTN; ++i) {
+    const uint32_t sym = lut[i] & 255u, len = lut[i] >> 8;
+    uint32_t v = len;
+    if (kq_symbits(kqt) == 4) v |= f(sym & 15u) << 16 | f(sym >> 4) << 24;
+    else v |= f(sym) << 16;
+    out[i] = v;
+  }
+}
+
 }  // namespace lw

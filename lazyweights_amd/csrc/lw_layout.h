@@ -62,5 +62,8 @@ int default_threads();
 // symbols, the two grid bytes at bytes 2 and 3 (Q4_K: q; IQ4_XS: kv[q] + 128), for 8-bit symbols fp16(f(q)) in bits
 // 16-31 (Q5_K: q; Q6_K: q - 32).
 void decode_table4(int kqt, const uint16_t* lut, uint32_t* out);
+// The int8-activation kernels' table: as decode_table4, with the grid values as int8 bytes (4-bit symbols: bytes 2
+// and 3 = f(q) of the low and high code, Q4_K q, IQ4_XS kv[q]; 8-bit symbols: byte 2 = f(q), Q5_K q, Q6_K q - 32).
+void decode_table_i8(int kqt, const uint16_t* lut, uint32_t* out);
 
 }  // namespace lw

@@ -117,6 +117,8 @@ struct Model {
   size_t cnt_cap = 0;
   uint16_t* X16 = nullptr;
   size_t X16_cap = 0;
+  uint8_t* x8 = nullptr;  // int8 activations: per vector [K int8][K / 32 d][K / 32 d sum q], 256-B aligned parts
+  size_t x8_cap = 0;
   uint8_t* codes = nullptr;
   size_t codes_cap = 0;
   int verbose = 0;
@@ -252,17 +254,21 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][4-byte table 8192 B][tbase 4T][mid 64T][split 512T][rows 2T][sched 16T (16-aligned)]
-  // [exception tiles 4E] padded to 256 B, then the words
+  // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][tbase 4T][mid 64T][split 512T][rows 2T]
+  // [sched 16T (16-aligned)][exception tiles 4E] padded to 256 B, then the words
   const size_t nexc = L.exc.size();
-  const size_t o_lut4 = 2 * lw::LUTN, o_tb = o_lut4 + 4 * lw::LUTN, o_mid = o_tb + 4ull * T;
+  const size_t o_lut4 = 2 * lw::LUTN, o_luti8 = o_lut4 + 4 * lw::LUTN, o_tb = o_luti8 + 4 * lw::LUTN;
+  const size_t o_mid = o_tb + 4ull * T;
   const size_t o_split = o_mid + 64ull * T, o_rows = o_split + 64ull * lw::SPLITS * T;
   const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_exc = o_sched + 16ull * T;
   const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
   memcpy(host.data(), L.lut, 2 * lw::LUTN);
-  if (t.kqt) lw::decode_table4(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_lut4));
+  if (t.kqt) {
+    lw::decode_table4(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_lut4));
+    lw::decode_table_i8(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_luti8));
+  }
   memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
   memcpy(host.data() + o_split, L.split.data(), 64ull * lw::SPLITS * T);
@@ -287,6 +293,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   uint8_t* b = static_cast<uint8_t*>(d);
   dm.lut = reinterpret_cast<const uint16_t*>(b);
   dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_lut4) : nullptr;
+  dm.luti8 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_luti8) : nullptr;
   dm.tbase = reinterpret_cast<const uint32_t*>(b + o_tb);
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
   dm.split = reinterpret_cast<const uint16_t*>(b + o_split);
@@ -323,14 +330,16 @@ bool make_resident_packed(Model& M, Tensor& t) {
   const int KS = t.KS(), NT = (int)(t.N / lw::TN), KT = KS / lw::TK, T = NT * KT;
   std::vector<uint8_t> blob((size_t)t.N * KS);
   if (!pread_all(M.fd, blob.data(), blob.size(), t.off)) return fail(t.name + ": read error");
-  const size_t o_words = 256 * 4, bytes = o_words + (size_t)T * lw::TN * lw::TK + 8 * 128;
+  const size_t o_words = 2 * 256 * 4, bytes = o_words + (size_t)T * lw::TN * lw::TK + 8 * 128;
   std::vector<uint8_t> host(bytes, 0);
-  if (t.kqt) {
+  if (t.kqt) {  // [symbol table 256 x 4 B][int8 symbol table 256 x 4 B]
     std::vector<uint16_t> ident(lw::LUTN);
     for (int i = 0; i < lw::LUTN; ++i) ident[i] = (uint16_t)(i & 255);
     std::vector<uint32_t> tab(lw::LUTN);
     lw::decode_table4(t.kqt, ident.data(), tab.data());
     memcpy(host.data(), tab.data(), 256 * 4);
+    lw::decode_table_i8(t.kqt, ident.data(), tab.data());
+    memcpy(host.data() + 256 * 4, tab.data(), 256 * 4);
   }
   uint8_t* w = host.data() + o_words;
   for (int tr = 0; tr < NT; ++tr)
@@ -356,6 +365,7 @@ bool make_resident_packed(Model& M, Tensor& t) {
   dm = lw::DevMat{};
   uint8_t* b = static_cast<uint8_t*>(d);
   dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b) : nullptr;
+  dm.luti8 = t.kqt ? reinterpret_cast<const uint32_t*>(b + 256 * 4) : nullptr;
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
   dm.packed = 1;
   dm.N = (int)t.N;
@@ -381,6 +391,7 @@ void release(Model* M) {
   if (M->P) (void)hipFree(M->P);
   if (M->cnt) (void)hipFree(M->cnt);
   if (M->X16) (void)hipFree(M->X16);
+  if (M->x8) (void)hipFree(M->x8);
   if (M->codes) (void)hipFree(M->codes);
   if (M->stream) (void)hipStreamDestroy(M->stream);
   if (M->fd >= 0) close(M->fd);
@@ -468,14 +479,60 @@ long long split_cost(int total, int stage_rows, int kqt) {
   return full * std::max<long long>(4 * per_cu, 16) * 40 + (rest ? std::max<long long>(4 * rest, 16) * 40 : 0);
 }
 
+// Int8 activations for m = 1 GEMVs (the reference's default on sm_61+, off there with LLMRT_FP_ACT=1; off by
+// default here, where fp16 hi + lo activations are the default): x quantized per block of 32 (k_quant_x8), integer
+// dot products per sub-block (kernels/llmrt.cu:1035-1169, 1808-1813, 2221).
+int g_act8 = 0;
+
+struct X8 {
+  const int8_t* q;
+  const float* d;
+  const float* s;
+};
+
+// Quantize the m = 1 activation vector of each of `count` matrices (fp16 or fp32; a vector shared by several
+// matrices once) into the model's x8 scratch; x8[i] = matrix i's quantized x.
+int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, std::vector<X8>& x8,
+                 hipStream_t s) {
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  std::vector<size_t> off(count);
+  std::map<const void*, int> first;
+  size_t total = 0;
+  for (int i = 0; i < count; ++i) {
+    const size_t K = (size_t)ts[i]->K;
+    auto it = first.find(X[i]);
+    if (it != first.end() && ts[it->second]->K == ts[i]->K) {
+      off[i] = off[it->second];
+      continue;
+    }
+    first[X[i]] = i;
+    off[i] = total;
+    total += al(K) + 2 * al(K / 32 * 4);
+  }
+  if (grow(M.x8, M.x8_cap, total)) return -1;
+  x8.resize(count);
+  for (int i = 0; i < count; ++i) {
+    const size_t K = (size_t)ts[i]->K;
+    uint8_t* b = M.x8 + off[i];
+    x8[i] = X8{reinterpret_cast<const int8_t*>(b), reinterpret_cast<const float*>(b + al(K)),
+               reinterpret_cast<const float*>(b + al(K) + al(K / 32 * 4))};
+    if (first[X[i]] != i) continue;
+    HIPCHECK(lw::launch_quant_x8(X[i], x_f16, 1, (int)K, reinterpret_cast<int8_t*>(b),
+                                 reinterpret_cast<float*>(b + al(K)), reinterpret_cast<float*>(b + al(K) + al(K / 32 * 4)),
+                                 s));
+  }
+  return 0;
+}
+
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
 // others into whole-tile launches. The ordered reduction over tile columns runs inside the flat (m = 1) launch for
 // every matrix that launch decodes completely, else in one reduction launch per MAX_GROUP matrices. Partials of
 // all matrices live side by side in the model's P scratch; calls that overlap on one model race (P and counters).
-// `launches` (optional) counts the kernel launches.
+// `launches` (optional) counts the kernel launches. x8 (m = 1, flat kernels only): int8 activations (quant_x8_dev)
+// instead of X16.
 int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
-                    const int* ldy, hipStream_t s, int* launches = nullptr) {
+                    const int* ldy, hipStream_t s, int* launches = nullptr, const X8* x8 = nullptr) {
   const int mt = m * per;
   std::vector<size_t> off(count + 1, 0);
   for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
@@ -495,6 +552,17 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   };
   const bool ring_ok = g_kernel_mode != 1;
   const bool flat = ring_ok && mt == 1 && g_kernel_mode != 2;
+  if (x8 && !flat) {
+    g_err = "int8 activations: m = 1 and a flat kernel mode (0, 3, 4 or 5) only";
+    return -1;
+  }
+  auto set8 = [&](lw::FlatPlan& fp, lw::FlatEntry& e, int j) {
+    if (!x8) return;
+    fp.i8 = 1;
+    e.XQ = x8[j].q;
+    e.DX = x8[j].d;
+    e.SX = x8[j].s;
+  };
   // m = 1 (fp16 x): one flat launch (balanced blocks) per (K-quant type, ring size) and batch of MAX_GROUP
   // matrices, whatever their order: the ring kernel, or the low-latency kernel when the cost model favours it (few
   // tiles per CU) or a matrix has no ring schedule. In a 16-row ring launch, exception tiles with a 32-row schedule
@@ -513,6 +581,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       lw::FlatEntry& e = fp.e[fp.n++];
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
+      set8(fp, e, j);
       e.P = M.P + off[j];
       e.tile0 = fp.ntiles;
       e.ntile = dm.NT * dm.KT;
@@ -558,6 +627,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       lw::FlatEntry& e = fp.e[fp.n++];
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
+      set8(fp, e, j);
       e.P = M.P + off[j];
       e.list = nullptr;
       e.tile0 = total;
@@ -629,6 +699,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         e.M = dm;
         e.M.ring_rows = 32;  // these tiles' schedules are for a 32-row ring
         e.X2 = static_cast<const uint32_t*>(X16[j]);
+        set8(fp, e, j);
         e.P = M.P + off[j];
         e.list = dm.exc;
         e.tile0 = fp.ntiles;
@@ -654,6 +725,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         lw::FlatEntry& e = fp.e[fp.n++];
         e.M = dm;
         e.X2 = static_cast<const uint32_t*>(X16[i]);
+        set8(fp, e, i);
         e.P = M.P + off[i];
         e.list = rest.exc;
         e.ntile = fp.ntiles = rest.nexc;
@@ -850,7 +922,20 @@ int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, i
     g_err = "rt_test_matmul: device allocation failed";
     return -1;
   }
-  if (m <= 8 && path != 2) {
+  if (g_act8 && m == 1 && path != 2) {  // int8 activations quantized on the device from the fp32 x
+    std::vector<X8> x8;
+    if (hipMalloc(reinterpret_cast<void**>(&dx), K * 4) != hipSuccess ||
+        hipMemcpy(dx, X, K * 4, hipMemcpyHostToDevice) != hipSuccess) {
+      cleanup();
+      g_err = "rt_test_matmul: upload failed";
+      return -1;
+    }
+    const void* xp = dx;
+    float* yp = dy;
+    const int ld = (int)N;
+    rc = quant_x8_dev(*M, &t, &xp, 0, 1, x8, M->stream);
+    if (!rc) rc = fused_group_dev(*M, &t, &xp, 1, 1, 1, &yp, &ld, M->stream, nullptr, x8.data());
+  } else if (m <= 8 && path != 2) {
     // fp32 activations as fp16 hi + lo pseudo-tokens (x = hi + lo to 2^-22 relative)
     std::vector<uint16_t> x16((size_t)2 * m * K);
     for (int j = 0; j < m; ++j)
@@ -884,6 +969,32 @@ int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, i
     }
   }
   cleanup();
+  return rc;
+}
+
+int lw_test_quant_x8(const void* X, int x_f16, int m, int K, int8_t* xq, float* dx, float* sx) {
+  if (!X || !xq || !dx || !sx || m < 1 || K < 32 || K % 32) {
+    g_err = "lw_test_quant_x8: bad arguments";
+    return -1;
+  }
+  const size_t n = (size_t)m * K, nb = n / 32, xb = n * (x_f16 ? 2 : 4);
+  uint8_t* d = nullptr;
+  if (hipMalloc(reinterpret_cast<void**>(&d), xb + n + 8 * nb) != hipSuccess) {
+    g_err = "lw_test_quant_x8: device allocation failed";
+    return -1;
+  }
+  int8_t* q = reinterpret_cast<int8_t*>(d + xb);
+  float* fd = reinterpret_cast<float*>(d + xb + n);
+  int rc = 0;
+  if (hipMemcpy(d, X, xb, hipMemcpyHostToDevice) != hipSuccess ||
+      lw::launch_quant_x8(d, x_f16, m, K, q, fd, fd + nb, nullptr) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess || hipMemcpy(xq, q, n, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(dx, fd, nb * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(sx, fd + nb, nb * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+    g_err = std::string("lw_test_quant_x8: ") + hipGetErrorString(hipGetLastError());
+    rc = -1;
+  }
+  (void)hipFree(d);
   return rc;
 }
 
@@ -1051,6 +1162,11 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
   Tensor* t = M->find(name);
   if (check_matmul(t, name)) return -1;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g_act8 && m == 1) {
+    std::vector<X8> x8;
+    if (quant_x8_dev(*M, &t, &X, x_f16, 1, x8, s)) return -1;
+    return fused_group_dev(*M, &t, &X, 1, 1, 1, &Y, &ldy, s, nullptr, x8.data());
+  }
   if (x_f16) {
     if (m < 1 || m > 16) {
       g_err = "lw_matmul_dev: fp16 activations need 1 <= m <= 16";
@@ -1086,7 +1202,19 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
     }
     ldy[i] = (int)ts[i]->N;
   }
-  return fused_group_dev(*M, ts.data(), X, count, m, 1, Y, ldy.data(), static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g_act8 && m == 1) {
+    std::vector<X8> x8;
+    if (quant_x8_dev(*M, ts.data(), X, 1, count, x8, s)) return -1;
+    return fused_group_dev(*M, ts.data(), X, count, 1, 1, Y, ldy.data(), s, nullptr, x8.data());
+  }
+  return fused_group_dev(*M, ts.data(), X, count, m, 1, Y, ldy.data(), s);
+}
+
+int lw_set_act8(int on) {
+  if (on != 0 && on != 1) return -1;
+  g_act8 = on;
+  return 0;
 }
 
 int lw_set_kernel_mode(int mode) {

@@ -136,3 +136,59 @@ def rel_err(y, y64):
     y = np.asarray(y, np.float64)
     y64 = np.asarray(y64, np.float64)
     return float(np.max(np.abs(y - y64)) / max(np.max(np.abs(y64)), 1e-300))
+
+
+# ── int8 activations (the reference's act8 path) ────────────────────────────────────────────────────────────
+# IQ4_XS grid (llama.cpp kvalues_iq4nl, the table the reference dequantizes with: kernels/llmrt.cu:1057-1065)
+IQ4_GRID = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.int32)
+
+
+def quant_x8(x):
+    """x [m, K] (fp32; K a multiple of 32) -> (q int8 [m, K], d fp32 [m, K / 32], sx fp32 [m, K / 32]).
+
+    Follows k_quant_x8 (kernels/llmrt.cu:1035-1055): per block of 32, d = max|x| / 127 in fp32, q = x / d (fp32
+    quotient) rounded to nearest even (__float2int_rn), 0 where d = 0, and sx = d * (sum of q) in fp32.
+    """
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    m, K = x.shape
+    if K % 32:
+        raise ValueError("K must be a multiple of 32")
+    b = x.reshape(m, K // 32, 32)
+    d = (np.abs(b).max(axis=2) / np.float32(127)).astype(np.float32)
+    safe = np.where(d > 0, d, np.float32(1))
+    q = np.where(d[..., None] > 0, np.rint(b / safe[..., None]), np.float32(0)).astype(np.int32)
+    sx = (d * q.sum(axis=2).astype(np.float32)).astype(np.float32)
+    return q.reshape(m, K).astype(np.int8), d, sx
+
+
+def grid_i8(kqt, codes):
+    """The integer each code contributes to the int8 dot products (kernels/llmrt.cu:1134-1146): Q4_K / Q5_K q,
+    Q6_K q - 32, IQ4_XS the grid value kv[q]."""
+    c = np.asarray(codes).astype(np.int32)
+    if kqt == 4:
+        return IQ4_GRID[c & 15]
+    if kqt == 3:
+        return c - 32
+    return c
+
+
+def gemv_act8_f64(kqt, codes, side, q, d, sx):
+    """y [m, N] that the int8-activation kernels approximate, in fp64 (kernels/llmrt.cu:1127-1160): per sub-block g
+    of GW weights (32; 16 for Q6_K), y += s_ng d_b acc_ng - o_ng sx_b, with acc_ng = sum over g of grid_i8 x q
+    (an exact integer), b = g's 32-block and (s, o) the sub-block scale and offset of sub_scales."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    N, K = codes.shape
+    q = np.atleast_2d(q).astype(np.float64)
+    d = np.atleast_2d(d).astype(np.float64)
+    sx = np.atleast_2d(sx).astype(np.float64)
+    m = q.shape[0]
+    G = 16 if kqt == 3 else 8
+    GW = 256 // G
+    s, o = sub_scales(kqt, np.ascontiguousarray(side, np.uint8).reshape(N * (K // 256), -1))
+    s = s.astype(np.float64).reshape(N, K // GW)
+    o = o.astype(np.float64).reshape(N, K // GW)
+    v = grid_i8(kqt, codes).astype(np.float64).reshape(N, K // GW, GW)
+    acc = np.einsum("ngk,mgk->mng", v, q.reshape(m, K // GW, GW))  # integers below 2^53: exact
+    blk = (np.arange(K // GW) * GW) // 32
+    y = np.einsum("ng,mg,mng->mn", s, d[:, blk], acc)
+    return y - np.einsum("ng,mg->mn", o, sx[:, blk])

@@ -408,14 +408,16 @@ def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):
 
 
 def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
-    """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices),
-    m = 5 and the fp32-x path; its GPU decode returns the codes."""
+    """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices,
+    with a one-tile IQ4_XS matrix so the flat launch runs one-wave blocks that use all 256 table entries), m = 5 and
+    the fp32-x path; its GPU decode returns the codes."""
     import ctypes
 
     import torch
     from lazyweights_amd import Runtime, bundle
     mats = [("m%d" % kqt, kqt, N, K, H, 20 + kqt) for kqt, N, K, H in
             ((1, 128, 2048, 2.3), (2, 128, 1024, 3.4), (3, 64, 1024, 4.3), (4, 128, 2048, 2.6))]
+    mats.append(("m4s", 4, 64, 512, 2.6, 30))
     bundle.write_synthetic_bundle(str(tmp_path / "coded"), mats, threads=4)
     bundle.write_packed_bundle(str(tmp_path / "packed"), mats, threads=4)
     with Runtime(tmp_path / "coded") as rc, Runtime(tmp_path / "packed") as rp:

@@ -5,7 +5,10 @@
 - comparator tables: against the LUT over all 2048 windows (brute force);
 - sub-scale extraction: against the reference's field *packing* (scripts/kq_quant.py:204-221), restated here as
   the inverse function, and against hand-computed known answers;
-- GEMV: against numpy's fp64 matmul.
+- GEMV: against numpy's fp64 matmul;
+- int8 activations: the quantizer against hand-built blocks (exact scale, ties to even, zero blocks, the error
+  bound), and the int8 GEMV against the identity it must satisfy: the sum of s d acc - o sx over sub-blocks equals
+  the fp64 product of the dequantized weights with the dequantized activations d q.
 """
 import os
 import subprocess
@@ -161,3 +164,54 @@ def test_reference_cpp_decoder_reads_our_bundles(tmp_path):
         assert p.returncode == 0, p.stderr
         assert '"mismatch": 0' in p.stdout and '"mismatch": 1' not in p.stdout
         assert np.array_equal(np.fromfile(dump, np.uint8).reshape(sym.shape), sym)
+
+
+def test_quant_x8_known_blocks(orc):
+    # block 0: max |x| = 127 -> d = 1 exactly; halves round to even (2.5 -> 2, 3.5 -> 4, -2.5 -> -2)
+    b0 = np.zeros(32, np.float32)
+    b0[:6] = [127, 2.5, 3.5, -2.5, 0.5, -1.49]
+    b1 = np.zeros(32, np.float32)                        # all zero: d = 0, q = 0, sx = 0
+    b2 = np.zeros(32, np.float32)
+    b2[7] = -3.0                                         # one value: q = -127 there
+    b3 = np.linspace(-1, 2, 32).astype(np.float32)       # max at the end: q = 127 there
+    q, d, sx = orc.quant_x8(np.concatenate([b0, b1, b2, b3])[None])
+    q = q.reshape(4, 32).astype(int)
+    assert d[0, 0] == 1.0 and list(q[0, :6]) == [127, 2, 4, -2, 0, -1] and sx[0, 0] == 130.0
+    assert d[0, 1] == 0 and not q[1].any() and sx[0, 1] == 0
+    assert d[0, 2] == np.float32(3.0) / np.float32(127) and q[2, 7] == -127 and q[2].sum() == -127
+    assert q[3, 31] == 127 and q[3, 0] == round(-1 / (2 / 127))
+
+
+def test_quant_x8_bounds(orc):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((4, 4096)) * rng.uniform(1e-3, 1e3, (4, 1))).astype(np.float32)
+    q, d, sx = orc.quant_x8(x)
+    qb = q.astype(np.int64).reshape(4, 128, 32)
+    xb = x.astype(np.float64).reshape(4, 128, 32)
+    assert np.abs(qb).max() <= 127 and (np.abs(qb).max(axis=2) == 127).all()
+    assert (np.abs(xb - d[..., None] * qb) <= d[..., None] * (0.5 + 1e-5)).all()
+    assert np.allclose(sx, d * qb.sum(axis=2), rtol=1e-7, atol=0)
+
+
+@pytest.mark.parametrize("kqt", [1, 2, 3, 4])
+def test_act8_gemv_identity(orc, kqt, monkeypatch):
+    """gemv_act8_f64 (sub-block integer sums, scales applied per sub-block) == fp64 product of dequant(W) with the
+    dequantized activations: pins the per-sub-block scale, the 32-block index, the offset term and the grid."""
+    from lazyweights_amd import bundle
+    codes, side = bundle.synth_matrix(kqt, 64, 1024, 3.0, 5)
+    x = np.random.default_rng(kqt).standard_normal((3, 1024)).astype(np.float32)
+    q, d, sx = orc.quant_x8(x)
+    y8 = orc.gemv_act8_f64(kqt, codes, side, q, d, sx)
+    xh = (q.astype(np.float64).reshape(3, 32, 32) * d[..., None]).reshape(3, 1024)
+    W = orc.dequant(kqt, codes, side)
+    assert orc.rel_err(y8, orc.gemv_f64(W, xh)) < 1e-7
+    # the int8 result stays near the fp32-x product (quantization error only)
+    assert orc.rel_err(y8, orc.gemv_f64(W, x.astype(np.float64))) < 2e-2
+    # planted mistakes the identity catches: the offset term dropped, the grid off by one, the wrong 32-block
+    ref = orc.gemv_f64(W, xh)
+    if kqt in (1, 2):
+        assert orc.rel_err(y8 - orc.gemv_act8_f64(kqt, codes, side, 0 * q, d, sx), ref) > 1e-3
+    assert orc.rel_err(orc.gemv_act8_f64(kqt, codes, side, q, np.roll(d, 1, axis=1), sx), ref) > 1e-3
+    if kqt in (3, 4):
+        monkeypatch.setattr(orc, "grid_i8", lambda k, c: np.asarray(c).astype(np.int32))
+        assert orc.rel_err(orc.gemv_act8_f64(kqt, codes, side, q, d, sx), ref) > 1e-3
