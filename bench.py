@@ -216,6 +216,30 @@ def main():
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
 
+        # int8 activations (the reference's default act8 mode; m = 1 only): the same step with x quantized per block
+        # of 32 on the device (one quantization launch per distinct x) and integer sub-block dot products
+        act8 = None
+        if m == 1:
+            lib.lw_set_act8(1)
+            try:
+                step()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(a.steps):
+                    step()
+                torch.cuda.synchronize()
+                ams = (time.perf_counter() - t0) * 1e3 / a.steps
+                out8 = (ctypes.c_double * 3)()
+                if lib.lw_bench_groups(rt.h, a.layers, sizes, names, xp, m, yp, 1, max(3, a.steps // 2), out8) != 0:
+                    raise RuntimeError(lib.lw_last_error().decode())
+            finally:
+                lib.lw_set_act8(0)
+            act8 = {"ms_per_step": round(ams, 4), "GBps_coded": round(bytes_per_step / (ams * 1e-3) / 1e9, 1),
+                    "kernel_ms_per_pass": round(out8[1], 4), "launches_per_pass": int(out8[2]),
+                    "speed_vs_fp16_x": round(ms_per_step / ams, 3)}
+            log("bench: int8 activations %.3f ms per step (%.1f GB/s coded; kernels %.3f ms per pass, %d launches)"
+                % (ams, act8["GBps_coded"], out8[1], int(out8[2])))
+
         # prefill shapes (m = 128, fp32 x resident): the decode-to-scratch path with its GEMM on the matrix cores,
         # over layer 0's seven matrices (a reported figure, not the metric)
         prefill = None
@@ -329,6 +353,7 @@ def main():
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
             "control_packed_twin": packed,
+            "act8": act8,
             "prefill_path2": prefill,
         }
         print(json.dumps(res), flush=True)

@@ -91,6 +91,17 @@ hipError_t launch_fused_split(const FlatPlan& plan, hipStream_t s);
 // int8 activations as the reference's k_quant_x8 (kernels/llmrt.cu:1035-1055): X [m][K] (fp32, or fp16 when x_f16)
 // in blocks of 32: d = amax / 127, q = round-to-nearest-even(x / d) (0 when d = 0), XQ = q, DX = d, SX = d sum q.
 hipError_t launch_quant_x8(const void* X, int x_f16, int m, int K, int8_t* XQ, float* DX, float* SX, hipStream_t s);
+// up to MAX_GROUP vectors in one launch: job i quantizes nb[i] blocks of 32 from X[i]
+struct QuantJobs {
+  const void* X[MAX_GROUP];
+  int8_t* XQ[MAX_GROUP];
+  float* DX[MAX_GROUP];
+  float* SX[MAX_GROUP];
+  int nb[MAX_GROUP];
+  int b0[MAX_GROUP];  // first block-of-8 index of each job in the launch
+  int n, x_f16;
+};
+hipError_t launch_quant_x8_group(const QuantJobs& q, hipStream_t s);
 // LDS rows the low-latency kernel stages per tile for this plan (max over its matrices of max_rows + 2)
 int split_stage_rows(const FlatPlan& plan);
 

@@ -824,10 +824,8 @@ __device__ __forceinline__ XgRegs column_xsums(const uint32_t* X2, int tc, int l
 
 // ── int8 activations (m = 1), the reference's k_quant_x8 + k_gemvm_kq8 (kernels/llmrt.cu:1035-1169) ───────
 // Quantization: one block of 32 activations per half-wave.
-__global__ void __launch_bounds__(256) k_quant_x8(const void* __restrict__ X, int x_f16, int8_t* __restrict__ XQ,
-                                                  float* __restrict__ DX, float* __restrict__ SX, int nb) {
-  const int b = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
-  if (b >= nb) return;  // a half-wave's exchanges stay inside it (xor offsets < 32)
+__device__ __forceinline__ void quant_x8_block(const void* __restrict__ X, int x_f16, int8_t* __restrict__ XQ,
+                                               float* __restrict__ DX, float* __restrict__ SX, int b, int l) {
   const size_t i = (size_t)b * 32 + l;
   const float v = x_f16 ? h2f(static_cast<const uint16_t*>(X)[i]) : static_cast<const float*>(X)[i];
   float a = fabsf(v);
@@ -845,10 +843,39 @@ __global__ void __launch_bounds__(256) k_quant_x8(const void* __restrict__ X, in
   }
 }
 
+__global__ void __launch_bounds__(256) k_quant_x8(const void* __restrict__ X, int x_f16, int8_t* __restrict__ XQ,
+                                                  float* __restrict__ DX, float* __restrict__ SX, int nb) {
+  const int b = blockIdx.x * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  if (b >= nb) return;  // a half-wave's exchanges stay inside it (xor offsets < 32)
+  quant_x8_block(X, x_f16, XQ, DX, SX, b, l);
+}
+
+// several vectors in one launch (the distinct activation vectors of a grouped call)
+__global__ void __launch_bounds__(256) k_quant_x8_group(QuantJobs q) {
+  int j = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < q.n && (int)blockIdx.x >= q.b0[i]) j = i;
+  const int b = ((int)blockIdx.x - q.b0[j]) * 8 + (threadIdx.x >> 5), l = threadIdx.x & 31;
+  if (b >= q.nb[j]) return;
+  quant_x8_block(q.X[j], q.x_f16, q.XQ[j], q.DX[j], q.SX[j], b, l);
+}
+
 hipError_t launch_quant_x8(const void* X, int x_f16, int m, int K, int8_t* XQ, float* DX, float* SX, hipStream_t s) {
   if (m < 1 || K % 32) return hipErrorInvalidValue;
   const int nb = m * K / 32;
   hipLaunchKernelGGL(k_quant_x8, dim3((nb + 7) / 8), dim3(256), 0, s, X, x_f16, XQ, DX, SX, nb);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_x8_group(const QuantJobs& q, hipStream_t s) {
+  if (q.n < 1 || q.n > MAX_GROUP) return hipErrorInvalidValue;
+  int blocks = 0;
+  for (int i = 0; i < q.n; ++i) {
+    if (q.nb[i] < 1 || q.b0[i] != blocks) return hipErrorInvalidValue;
+    blocks += (q.nb[i] + 7) / 8;
+  }
+  hipLaunchKernelGGL(k_quant_x8_group, dim3(blocks), dim3(256), 0, s, q);
   return hipGetLastError();
 }
 

@@ -511,16 +511,30 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
   }
   if (grow(M.x8, M.x8_cap, total)) return -1;
   x8.resize(count);
+  lw::QuantJobs q{};
+  q.x_f16 = x_f16;
+  int blocks = 0;
   for (int i = 0; i < count; ++i) {
     const size_t K = (size_t)ts[i]->K;
     uint8_t* b = M.x8 + off[i];
     x8[i] = X8{reinterpret_cast<const int8_t*>(b), reinterpret_cast<const float*>(b + al(K)),
                reinterpret_cast<const float*>(b + al(K) + al(K / 32 * 4))};
     if (first[X[i]] != i) continue;
-    HIPCHECK(lw::launch_quant_x8(X[i], x_f16, 1, (int)K, reinterpret_cast<int8_t*>(b),
-                                 reinterpret_cast<float*>(b + al(K)), reinterpret_cast<float*>(b + al(K) + al(K / 32 * 4)),
-                                 s));
+    if (q.n == lw::MAX_GROUP) {
+      HIPCHECK(lw::launch_quant_x8_group(q, s));
+      q.n = 0;
+      blocks = 0;
+    }
+    q.X[q.n] = X[i];
+    q.XQ[q.n] = reinterpret_cast<int8_t*>(b);
+    q.DX[q.n] = reinterpret_cast<float*>(b + al(K));
+    q.SX[q.n] = reinterpret_cast<float*>(b + al(K) + al(K / 32 * 4));
+    q.nb[q.n] = (int)(K / 32);
+    q.b0[q.n] = blocks;
+    blocks += (int)(K / 32 + 7) / 8;
+    ++q.n;
   }
+  if (q.n) HIPCHECK(lw::launch_quant_x8_group(q, s));
   return 0;
 }
 
@@ -794,6 +808,19 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     if (launches) ++*launches;
   }
   return 0;
+}
+
+// lw_group_matmul_dev's work (fp16 x [m][K_i] per matrix): the fused path, after the quantization launch when int8
+// activations are on (m = 1)
+int group_matmul(Model& M, Tensor* const* ts, const void* const* X, int count, int m, float* const* Y, const int* ldy,
+                 hipStream_t s, int* launches = nullptr) {
+  if (g_act8 && m == 1) {
+    std::vector<X8> x8;
+    if (quant_x8_dev(M, ts, X, 1, count, x8, s)) return -1;
+    if (launches) ++*launches;
+    return fused_group_dev(M, ts, X, count, 1, 1, Y, ldy, s, launches, x8.data());
+  }
+  return fused_group_dev(M, ts, X, count, m, 1, Y, ldy, s, launches);
 }
 
 int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, int ldy, hipStream_t s) {
@@ -1202,13 +1229,7 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
     }
     ldy[i] = (int)ts[i]->N;
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (g_act8 && m == 1) {
-    std::vector<X8> x8;
-    if (quant_x8_dev(*M, ts.data(), X, 1, count, x8, s)) return -1;
-    return fused_group_dev(*M, ts.data(), X, count, 1, 1, Y, ldy.data(), s, nullptr, x8.data());
-  }
-  return fused_group_dev(*M, ts.data(), X, count, m, 1, Y, ldy.data(), s);
+  return group_matmul(*M, ts.data(), X, count, m, Y, ldy.data(), static_cast<hipStream_t>(stream));
 }
 
 int lw_set_act8(int on) {
@@ -1269,7 +1290,7 @@ int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* n
       for (int i = first[g]; i < first[g + 1]; ++i) ts.push_back(M->find(names[i]));
       HIPCHECK(hipEventRecord(ev[2 * g], s));
       int nl = 0;
-      if (fused_group_dev(*M, ts.data(), X + first[g], sizes[g], m, 1, Y + first[g], ldys.data() + first[g], s, &nl))
+      if (group_matmul(*M, ts.data(), X + first[g], sizes[g], m, Y + first[g], ldys.data() + first[g], s, &nl))
         return -1;
       if (it == 0) launches += nl;
       HIPCHECK(hipEventRecord(ev[2 * g + 1], s));
