@@ -109,6 +109,7 @@ def main():
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--no-packed", action="store_true", help="skip the packed-twin control")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-shape (m = 128) figure")
+    ap.add_argument("--kernel-mode", type=int, default=0, help="lw_set_kernel_mode for the whole run (0 = auto)")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
@@ -125,6 +126,8 @@ def main():
     from lazyweights_amd.configs import config2_layer
 
     lib = load_library()
+    if lib.lw_set_kernel_mode(a.kernel_mode) != 0:
+        raise SystemExit("bench.py: unknown kernel mode %d" % a.kernel_mode)
     work = a.workdir or tempfile.mkdtemp(prefix="lw_bench_")
     os.makedirs(work, exist_ok=True)
     try:

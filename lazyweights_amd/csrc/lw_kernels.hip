@@ -1418,6 +1418,279 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
   }
 }
 
+// ── whole-tile kernel for flat launches (m = 1): a tile per wave, 4 chains per lane ───────────────────────
+// Block = W waves sharing the decode tables; the block decodes tiles [T0, T0 + W R) (spanning at most two
+// matrices), wave w first tile T0 + w, then the next undecoded one from a counter in LDS: the waves of a block do
+// not share a SIMD evenly (13 waves: 4 on one SIMD, 3 on the others), so each SIMD takes tiles at its own rate.
+// A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
+// lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 4 chains of 64 symbols that start at the
+// load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
+// chain reads its two window words straight from the buffer for every pair (one ds_read2), no register window.
+// There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here. The lane keeps its row's sub-block dot products in registers and forms the row
+// partial in tile_gemv's order (tile_gemv_i8's for int8 activations), the bits of the other kernels.
+template <int KQ, int NTAB, bool I8>
+__global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr int NSUBT = TW / GW;                          // sub-blocks per tile row
+  constexpr int NSB = TW / 256;                           // super-blocks per tile row
+  constexpr int NSUB = 256 / GW;                          // sub-blocks per super-block
+  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
+  constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
+  constexpr int NC = 4;                                   // chains per lane
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  typedef __attribute__((address_space(4))) const float KF32;
+  // one static LDS object at address 0, so the tables sit at 0 and 8 KB (table_addr ORs its base into the index);
+  // the block's tile counter after them
+  __shared__ uint32_t lut4[NTAB * LUTN + 4];
+  extern __shared__ __align__(16) uint32_t tbuf[];  // W x buf_rows word rows of 32 words
+
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * W * R, Tl = min(T0 + W * R, plan.ntiles) - 1;
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  {
+    const uint4* ta = reinterpret_cast<const uint4*>(I8 ? ea->M.luti8 : ea->M.lut4);
+    const uint4* tb = reinterpret_cast<const uint4*>(I8 ? eb->M.luti8 : eb->M.lut4);
+    for (int i = threadIdx.x; i < LUTN / 4; i += W * 64) {
+      reinterpret_cast<uint4*>(lut4)[i] = ta[i];
+      if (NTAB > 1 && mb != ma) reinterpret_cast<uint4*>(lut4 + LUTN)[i] = tb[i];
+    }
+  }
+  uint32_t* next = lut4 + NTAB * LUTN;
+  if (threadIdx.x == 0) *next = (uint32_t)W;
+  __syncthreads();
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
+  uint32_t* buf = tbuf + (size_t)wave * buf_rows * 32;
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+#pragma unroll 1
+  for (int n = wave;;) {
+    const int T = T0 + n;
+    if (n >= W * R || T >= plan.ntiles) break;
+    const bool second = NTAB > 1 && mb != ma && T >= eb->tile0;
+    KEntry* ep = second ? eb : ea;
+    const auto& E = *ep;
+    const auto& M = E.M;
+    const int KT = M.KT, NT = M.NT, N = M.N;
+    const int u = T - E.tile0;
+    const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;
+    const int tc = t % KT, tr = t / KT;
+    // the tile's rows (and the 2 the last windows read past the longest lane), 8 rows per copy instruction; the
+    // previous tile's reads of the buffer have completed (each chain waited for its last reads)
+    {
+      const int nrow = (int)M.rows[t] + 2;
+      const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]) + lane;
+      for (int i = 0; i < (nrow + 7) / 8; ++i)
+        __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+    }
+    // side records, x sums and chain starts while the copy is in flight
+    const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+    uint32_t sw[NSB][5];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+    XgRegs xgr;
+    if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
+    uint32_t P[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + 4 * f + j) * 32 + (uint32_t)s] - GUARD_BITS;
+    const uint32_t tsel = second ? 4u * LUTN : 0u;
+    // the tile column's activations in VGPRs (lane l holds dwords l, l + 64, ..), read back wave-uniform with
+    // v_readlane: no scalar loads inside the decode loop, whose waits would drain every chain's LDS reads
+    constexpr int XV = I8 ? TW / 4 / 64 : TW / 2 / 64;
+    uint32_t xv[XV];
+    {
+      const uint32_t* xs = I8 ? reinterpret_cast<const uint32_t*>(E.XQ) + (size_t)tc * (TW / 4) : E.X2 + (size_t)tc * (TW / 2);
+#pragma unroll
+      for (int k = 0; k < XV; ++k) xv[k] = xs[64 * k + lane];
+    }
+    auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS
+    float sub[NSUBT];
+    float acc[NC];
+    int iacc[NC];
+    uint32_t wprev[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      acc[j] = 0.f;
+      iacc[j] = 0;
+      wprev[j] = 0;
+    }
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
+        // (the reads return in order: a chain waits only for its own)
+        // the window: word rows P / 32 and P / 32 + 1 of the lane (bits 0-4 of P: the offset; bits >= 16 carry
+        // table-entry payload and are ignored)
+        uint32_t w1[NC], e1[NC], e2[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          LdsU32* wp = (LdsU32*)(rlb + (__builtin_amdgcn_ubfe(P[j], 5, 8) << 7));
+          w1[j] = __builtin_amdgcn_alignbit(wp[32], wp[0], P[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NC; ++j) e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) P[j] = P[j] + e1[j] + e2[j];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int g = 4 * j + gi;  // 16-symbol group within the row
+          if (I8) {  // as tile_gemv_i8
+            if (SYMB == 4) {
+              iacc[j] = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u),
+                                               (int)xw(8 * g + p), iacc[j], false);
+            } else {
+              const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e1[j], 0x0C0C0602u);
+              if (p & 1) iacc[j] = __builtin_amdgcn_sdot4((int)(wprev[j] | (v2 << 16)), (int)xw(4 * g + p / 2), iacc[j], false);
+              else wprev[j] = v2;
+            }
+          } else if (SYMB == 4) {
+            const uint32_t v1 = __builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u);
+            const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u);
+            const int c = 16 * g + 2 * p;
+            acc[j] = dot2(v2, xw(c + 1), dot2(v1, xw(c), acc[j]));
+          } else {
+            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
+            acc[j] = dot2(v, xw(8 * g + p), acc[j]);
+          }
+        }
+      }
+      if (GPSUB == 1 || (gi & 1)) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          sub[(4 * j + gi) / GPSUB] = I8 ? (float)iacc[j] : acc[j];  // |iacc| < 2^24: exact
+          acc[j] = 0.f;
+          iacc[j] = 0;
+        }
+      }
+    }
+
+    // the row partial in tile_gemv's order (tile_gemv_i8's for int8 activations)
+    float tot = 0.f;
+    if (I8) {
+      KF32* dx = (KF32*)(E.DX + (size_t)tc * (TW / 32));
+      KF32* sx = (KF32*)(E.SX + (size_t)tc * (TW / 32));
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) {
+        float dA, dB, mf[8];
+        uint64_t scq, scq2;
+        side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
+#pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj) {
+          if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                               : (float)(uint32_t)(scq & 255u);
+          scq >>= 8;
+          const int xb = (sb * 256 + jj * GW) / 32;
+          tot = fmaf(dA * scv * dx[xb], sub[sb * NSUB + jj], tot);
+          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) {
+        float dA, dB;
+        uint64_t scq, scq2;
+        side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
+          float mf[8], msum = 0.f;
+          side_mins(sw[sb], mf);
+#pragma unroll
+          for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xgr(sb, jj, 0), msum);
+          tot = fmaf(-dB, msum, tot);
+        }
+        if (KQ == KQ_IQ4_XS) {
+          float csum = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < NSUB; ++jj) csum = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgr(sb, jj, 0), csum);
+          tot = fmaf(-128.f * dA, csum, tot);
+        }
+        float tsum = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj) {
+          if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                               : (float)(uint32_t)(scq & 255u);
+          scq >>= 8;
+          tsum = fmaf(scv, sub[sb * NSUB + jj], tsum);
+        }
+        tot = fmaf(dA * VSCALE, tsum, tot);
+      }
+    }
+    float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
+    __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    row_reduce(E, tr, KT, N, lane);
+    uint32_t nx = 0;
+    if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    n = __builtin_amdgcn_readfirstlane((int)nx);
+  }
+}
+
+template <int KQ, int NTAB, bool I8>
+static hipError_t tiles_launch_t(const FlatPlan& p, int rounds, int buf_rows, hipStream_t s) {
+  const size_t smem = (size_t)p.W * buf_rows * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  const int per = p.W * rounds, blocks = (p.ntiles + per - 1) / per;
+  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p, rounds, buf_rows);
+  return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t tiles_launch(const FlatPlan& p, int rounds, int buf_rows, hipStream_t s) {
+  const bool one = p.n == 1;  // one matrix: one table
+  if (p.i8) return one ? tiles_launch_t<KQ, 1, true>(p, rounds, buf_rows, s) : tiles_launch_t<KQ, 2, true>(p, rounds, buf_rows, s);
+  return one ? tiles_launch_t<KQ, 1, false>(p, rounds, buf_rows, s) : tiles_launch_t<KQ, 2, false>(p, rounds, buf_rows, s);
+}
+
+int tiles_buf_rows(const FlatPlan& p) {
+  int r = 0;
+  for (int i = 0; i < p.n; ++i) r = std::max(r, p.e[i].M.max_rows + 2);
+  return (r + 7) / 8 * 8;
+}
+
+hipError_t launch_fused_tiles(const FlatPlan& p, int rounds, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || rounds < 1 || p.ntiles < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt, per = p.W * rounds;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    // a block (W x rounds consecutive tiles) spans at most two matrices
+    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
+        e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
+        (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
+      return hipErrorInvalidValue;
+  }
+  const int rows = tiles_buf_rows(p);
+  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return tiles_launch<KQ_Q4_K>(p, rounds, rows, s);
+    case KQ_Q5_K: return tiles_launch<KQ_Q5_K>(p, rounds, rows, s);
+    case KQ_Q6_K: return tiles_launch<KQ_Q6_K>(p, rounds, rows, s);
+    case KQ_IQ4_XS: return tiles_launch<KQ_IQ4_XS>(p, rounds, rows, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <int KQ, int RS, int NTAB, bool I8>
 static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
   const size_t smem = (size_t)(p.W + p.nspare) * 2 * RS * 128;

@@ -11,8 +11,9 @@ namespace lw {
 // Every lane stream starts with GUARD zero bits in the device layout, so the window of the symbol at stream bit p is
 // read at q = p - GUARD and the byte offset of its 4-byte table entry is (window & 0x1FFC): one AND per symbol.
 constexpr int GUARD = 2;
-// Zero rows appended after the last tile (read-ahead of the staging copies and of the 64-bit windows).
-constexpr int TAIL_ROWS = 8;
+// Zero rows appended after the last tile (read-ahead of the staging copies and of the 64-bit windows; the
+// whole-tile kernel copies rows + 2 rounded up to 8).
+constexpr int TAIL_ROWS = 16;
 // Symbols per staging group (one sub-block of the 4-bit formats) and groups per chain (256 symbols).
 constexpr int GROUP_SYMS = 16;
 constexpr int GROUPS = 16;

@@ -538,6 +538,30 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
   return 0;
 }
 
+// Waves per block and rounds (tiles per wave) of the whole-tile kernel for a flat plan: one tile buffer per wave
+// (tiles_buf_rows) next to one or two 8 KB tables in 160 KB of LDS; rounds = the tiles per wave that spread the
+// plan over every CU once; a block's W x rounds tiles may span at most two matrices (<= the smallest matrix's tile
+// count). Returns 0 if no width fits.
+int tiles_width(const lw::FlatPlan& fp, int mintiles, int& rounds) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+  }
+  const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
+  if (rows > 256) return 0;
+  const int wmax = std::min(16, (160 * 1024 - tables) / (rows * 128));
+  if (wmax < 1) return 0;
+  rounds = (fp.ntiles + cus * wmax - 1) / (cus * wmax);
+  int w = std::min(wmax, (fp.ntiles + cus * rounds - 1) / (cus * rounds));
+  if (fp.n > 1)
+    while (w > 1 && w * rounds > mintiles) --w;
+  if (fp.n > 1 && w * rounds > mintiles) rounds = std::max(1, mintiles / w);
+  return w;
+}
+
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
 // ring-capable matrices go into grouped launches (same K-quant type and ring size, up to MAX_GROUP per launch), the
 // others into whole-tile launches. The ordered reduction over tile columns runs inside the flat (m = 1) launch for
@@ -583,6 +607,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   // are decoded in place in spare rings when those fit the LDS the launch's block width assumed.
   std::vector<char> done(count, 0), exc_in(count, 0), whole(count, 0);  // whole: every tile in a low-latency launch
   std::vector<lw::FlatPlan> flat_plans, split_plans;
+  std::vector<std::pair<lw::FlatPlan, int>> tile_plans;  // whole-tile kernel launches and their rounds
   // packed (fixed-rate) matrices: the decode-free kernels, one launch per K-quant type and MAX_GROUP matrices
   // (m = 1: the flat one, which also reduces)
   for (int i = 0; mt == 1 && i < count; ++i) {
@@ -652,6 +677,19 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       done[j] = 1;
     }
     fp.ntiles = total;
+    if (g_kernel_mode == 6) {  // the whole-tile kernel: every tile, the reduction in the launch
+      int rounds = 0;
+      fp.W = tiles_width(fp, mintiles, rounds);
+      if (fp.W > 0) {
+        for (int k = 0; k < fp.n; ++k) {
+          fp.e[k].Y = Y[sel[k]];
+          fp.e[k].cnt = M.cnt + coff[sel[k]];
+          reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
+        }
+        tile_plans.emplace_back(fp, rounds);
+        continue;
+      }
+    }
     bool split = !di.ring_rows || g_kernel_mode == 4;
     if (!split && g_kernel_mode != 5) {
       const int w = flat_width(total, di.ring_rows, mintiles, 0);
@@ -756,6 +794,10 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   }
   for (const lw::FlatPlan& fp : split_plans) {
     HIPCHECK(lw::launch_fused_split(fp, s));
+    if (launches) ++*launches;
+  }
+  for (const auto& tp : tile_plans) {
+    HIPCHECK(lw::launch_fused_tiles(tp.first, tp.second, s));
     if (launches) ++*launches;
   }
   for (int i = 0; i < count; ++i) {
@@ -1239,7 +1281,7 @@ int lw_set_act8(int on) {
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 5) return -1;
+  if (mode < 0 || mode > 6) return -1;
   g_kernel_mode = mode;
   return 0;
 }

@@ -138,7 +138,8 @@ def group(rt, names, xs):
 
 def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
     """One grouped m = 1 call over matrices of every size (one shared x, quantized once, and distinct ones): the
-    ring kernels (mode 5), the low-latency kernel (mode 4) and the packed twin give the same bits, within
+    ring kernels (mode 5), the low-latency kernel (mode 4), the whole-tile kernel (mode 6) and the packed twin give the
+    same bits, within
     tolerance of the oracle."""
     import torch
     rc, rp, mats = a8_rt
@@ -147,24 +148,24 @@ def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
         shared = torch.randn(1, mats[fmt][3]).half().cuda()
         xs = [shared, torch.randn(1, 512).half().cuda(), shared, torch.randn(1, 512).half().cuda()]
         runs = {}
-        for mode in (0, 4, 5):
+        for mode in (0, 4, 5, 6):
             assert lib.lw_set_kernel_mode(mode) == 0
             runs[mode] = group(rc, names, xs)
         lib.lw_set_kernel_mode(0)
         runs["packed"] = group(rp, names, xs)
         say("act8 kernels same bits", fmt)
-        for k in (0, 4, 5, "packed"):
+        for k in (0, 4, 5, 6, "packed"):
             for nm, x, y in zip(names, xs, runs[k]):
                 y8, _ = y_act8(orc, mats[nm], x.float().cpu().numpy())
                 check(y, y8, TOL_ACT8, "%s act8 grouped (%s)" % (nm, k))
-        for k in (4, 5, "packed"):
+        for k in (4, 5, 6, "packed"):
             for a, b in zip(runs[0], runs[k]):
                 assert np.array_equal(a, b), (fmt, k)
 
 
 def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
     """Matrices with exception tiles (32-row schedules decoded in place or by the one-wave pass; tiles without a
-    ring schedule by the low-latency kernel): modes 0, 3, 4 and 5 the same bits, within tolerance of the oracle."""
+    ring schedule by the low-latency kernel; every tile by the whole-tile kernel): modes 0, 3-6 the same bits, within tolerance of the oracle."""
     import torch
     from lazyweights_amd import Runtime
     from lazyweights_amd.bundle import Writer
@@ -178,12 +179,12 @@ def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
         x = torch.randn(1, 8192).half().cuda()
         for nm, (codes, side) in cases.items():
             runs = {}
-            for mode in (0, 3, 4, 5):
+            for mode in (0, 3, 4, 5, 6):
                 assert lib.lw_set_kernel_mode(mode) == 0
                 runs[mode] = group(rt, [nm], [x])[0]
             lib.lw_set_kernel_mode(0)
             say("act8 exception tiles", nm)
-            for mode in (3, 4, 5):
+            for mode in (3, 4, 5, 6):
                 assert np.array_equal(runs[0], runs[mode]), (nm, mode)
             q, d, s = orc.quant_x8(x.float().cpu().numpy())
             check(runs[0], orc.gemv_act8_f64(2, codes, side, q, d, s), TOL_ACT8, nm + " act8")

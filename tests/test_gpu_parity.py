@@ -407,6 +407,56 @@ def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):
             assert torch.equal(a[0], b[0]), nm
 
 
+def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
+    """The whole-tile flat kernel (a tile per wave in LDS, 4 chains per lane; mode 6) gives the ring kernels' bits
+    (mode 5) for every format, for single matrices and groups spanning several matrices (blocks over two tables),
+    and for matrices with exception tiles, which it decodes like any other tile."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer
+    from test_layout import mild_skew_codes, skewed_tile_codes
+
+    def run(rt, names, xs, mode):
+        assert rt.lib.lw_set_kernel_mode(mode) == 0
+        try:
+            ys = [torch.zeros(1, rt.info(nm)["N"], device="cuda") for nm in names]
+            n = len(names)
+            rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                            (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                            (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+            assert rc == 0, rt.lib.lw_last_error()
+            torch.cuda.synchronize()
+            return [y.cpu() for y in ys]
+        finally:
+            rt.lib.lw_set_kernel_mode(0)
+
+    rt, mats = fmt_rt
+    for kqt, fmt, H in FORMATS:
+        for names in ([fmt], [fmt + "_small"], [fmt + "_small", fmt, fmt + "_small"]):
+            X = [torch.randn(1, mats[nm][3]).half() for nm in names]
+            xs = [x.cuda() for x in X]
+            a, b = run(rt, names, xs, 6), run(rt, names, xs, 5)
+            say("whole-tile flat kernel", fmt, len(names))
+            for nm, x, ya, yb in zip(names, X, a, b):
+                assert torch.equal(ya, yb), nm
+                _, y64 = reference_y(orc, mats[nm], x.double().numpy())
+                check_err(ya.numpy(), y64, "%s whole-tile kernel" % nm)
+    w = Writer(str(tmp_path))
+    cases = {"mskew": mild_skew_codes(), "skew": skewed_tile_codes()}
+    for nm, (codes, side) in cases.items():
+        w.add_kquant(nm, 2, codes, side)
+    w.close()
+    with Runtime(tmp_path) as rt2:
+        x = torch.randn(1, 8192).half()
+        for nm, (codes, side) in cases.items():
+            a, b = run(rt2, [nm], [x.cuda()], 6), run(rt2, [nm], [x.cuda()], 5)
+            say("whole-tile flat kernel, exception tiles", nm)
+            assert torch.equal(a[0], b[0]), nm
+            check_err(a[0].numpy(), orc.gemv_f64(orc.dequant(2, codes, side), x.double().numpy()), nm)
+
+
 def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
     """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices,
     with a one-tile IQ4_XS matrix so the flat launch runs one-wave blocks that use all 256 table entries), m = 5 and
