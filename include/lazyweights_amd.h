@@ -135,8 +135,8 @@ int lw_write_bundle(const char* dir, int count, const char* const* names, const 
 int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L);
 
 /* The device layout this library builds from a blob at load time (host-side, for inspection and tests): fills tbase
- * [T], mid [T * 32], split [T * 8 * 32] (bit offsets of symbols 64 k per lane, the low-latency kernel's chain
- * starts), rows [T], sched [2 T] (ring staging schedule), *ring_rows and, when words_cap is large enough, words;
+ * [T], mid [T * 32], split [T * 16 * 32] (bit offsets of symbols 32 k per lane: the chain starts of the
+ * low-latency and whole-tile kernels), rows [T], sched [2 T] (ring staging schedule), *ring_rows and, when words_cap is large enough, words;
  * returns the word count (-1 on a bad or corrupt blob). Any output pointer may be NULL. pre_il / compact select the
  * reference's pre-interleaved export formats (_il / _ilc). */
 long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,

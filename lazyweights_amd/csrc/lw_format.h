@@ -21,7 +21,8 @@ constexpr int LMAX = 11;           // maximum code length
 constexpr int LUTN = 1 << LMAX;    // bundle LUT entries
 constexpr int LANES = 32;          // lanes per tile
 constexpr int LANE_SYMS = 2 * TK;  // symbols per lane (two rows)
-constexpr int SPLITS = 8;          // chains per lane in the low-latency kernel (64 symbols each)
+constexpr int SPLITS = 16;         // chain starts per lane stream, every 32 symbols (the low-latency kernel uses
+                                   // every second one, the whole-tile kernel all)
 
 // K-quant type ids, numbered as the reference's Tensor::kqt (kernels/llmrt.cu:113-116)
 enum : int { KQ_NONE = 0, KQ_Q4_K = 1, KQ_Q5_K = 2, KQ_Q6_K = 3, KQ_IQ4_XS = 4 };

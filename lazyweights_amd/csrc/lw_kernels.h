@@ -21,7 +21,7 @@ struct DevMat {
   const uint32_t* luti8; // the same with int8 grid values (decode_table_i8), for int8 activations
   const uint32_t* tbase;
   const uint16_t* mid;
-  const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency kernel (Layout::split)
+  const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency and whole-tile kernels (Layout::split)
   const uint16_t* rows;
   const uint32_t* words;
   const uint8_t* side;

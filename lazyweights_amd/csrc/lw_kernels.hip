@@ -770,6 +770,24 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 // before the wave counts its tile in its tile row; the wave that counts the row's last tile resets the counter and
 // sums the row's partials in tile-column order (the order of k_reduce_group, so the bits are the same) with
 // device-coherent loads. No-op when the entry has no Y (the partials are reduced by a separate launch).
+// The sum of tile row tr's partials by the wave that counted the row's last tile (resets the counter).
+template <class KEntryRef>
+__device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane) {
+  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
+  float a = 0.f;
+  for (int c0 = 0; c0 < KT; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c0 + c < KT) a += v[c];
+  }
+  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
+}
+
 template <class KEntryRef>
 __device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane) {
   if (!E.Y) return;
@@ -1256,7 +1274,7 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   {
     // chain of lane front f: symbols [64 wave, 64 wave + 64) of row l + 32 f, i.e. stream symbols 256 f + 64 wave..
     const int k = 4 * f + wave;
-    uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+    uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k * (SPLITS / 8)) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
     const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
     uint32_t tmask = 0x1FFCu;
     asm volatile("" : "+v"(tmask));
@@ -1423,13 +1441,16 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
 // matrices), wave w first tile T0 + w, then the next undecoded one from a counter in LDS: the waves of a block do
 // not share a SIMD evenly (13 waves: 4 on one SIMD, 3 on the others), so each SIMD takes tiles at its own rate.
 // A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
-// lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 4 chains of 64 symbols that start at the
+// lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 8 chains of 32 symbols that start at the
 // load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
 // chain reads its two window words straight from the buffer for every pair (one ds_read2), no register window.
 // There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here. The lane keeps its row's sub-block dot products in registers and forms the row
 // partial in tile_gemv's order (tile_gemv_i8's for int8 activations), the bits of the other kernels.
+// (at most 16 waves per CU by the LDS of the tile buffers: 4 per SIMD, so the scheduler may spend up to 128 VGPRs on
+// keeping the 8 chains' reads in flight)
 template <int KQ, int NTAB, bool I8>
-__global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
+__global__ void __launch_bounds__(1024, 1)
+k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
@@ -1438,12 +1459,14 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
   constexpr int NSUB = 256 / GW;                          // sub-blocks per super-block
   constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
   constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
-  constexpr int NC = 4;                                   // chains per lane
+  constexpr int NC = 8;                                   // chains per lane (32 symbols each)
+  constexpr int NG = 16 / NC;                             // 16-symbol groups per chain
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   typedef __attribute__((address_space(4))) const char KChar;
   typedef __attribute__((address_space(4))) const FlatEntry KEntry;
   typedef __attribute__((address_space(4))) const uint32_t KU32;
   typedef __attribute__((address_space(4))) const float KF32;
+  typedef __attribute__((address_space(4))) const uint16_t KU16;
   // one static LDS object at address 0, so the tables sit at 0 and 8 KB (table_addr ORs its base into the index);
   // the block's tile counter after them
   __shared__ uint32_t lut4[NTAB * LUTN + 4];
@@ -1477,26 +1500,50 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
   const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
   uint32_t tmask = 0x1FFCu;
   asm volatile("" : "+v"(tmask));
-#pragma unroll 1
-  for (int n = wave;;) {
+  // tile n of the block: the second entry or not, and the tile index (wave-uniform values)
+  auto tile_of = [&](int n, int& sec, int& t) {
     const int T = T0 + n;
-    if (n >= W * R || T >= plan.ntiles) break;
-    const bool second = NTAB > 1 && mb != ma && T >= eb->tile0;
+    sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
+    KEntry* e = sec ? eb : ea;
+    const int u = T - e->tile0, NT = e->M.NT, KT = e->M.KT;
+    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : (u % NT) * KT + u / NT);
+  };
+  // the tile's rows (and the 2 the last windows read past the longest lane) into the wave's buffer, 8 rows per
+  // copy instruction; the per-tile words are read through the scalar cache (read-only during the launch)
+  auto copy_tile = [&](KEntry* e, int t) {
+    const int nrow = (int)((KU16*)e->M.rows)[t] + 2;
+    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+    for (int i = 0; i < (nrow + 7) / 8; ++i)
+      __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+  };
+  // The in-launch reduction of a tile's row is deferred behind the next tile's copy and decode: its partial is
+  // stored, and after the next copy's wait (which also covers the store) the row counter is incremented; the
+  // counter's old value is read after the next decode, and the row's last tile sums the row. The next copy is
+  // issued as soon as a decode ends, so its latency hides behind the combine and the reduction.
+  int pend = -1;  // the pending tile's entry: 0 = first, 1 = second, -1 = none
+  int ptr = 0, pKT = 0, pN = 0;
+  uint32_t pold = 0;
+  auto finish_pending = [&]() {
+    if (pend < 0) return;
+    const uint32_t old = (uint32_t)__builtin_amdgcn_readlane((int)pold, 0);
+    if (old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
+    pend = -1;
+  };
+  int n = wave;
+  bool have = n < W * R && T0 + n < plan.ntiles;
+  int sec = 0, t = 0;
+  if (have) {
+    tile_of(n, sec, t);
+    copy_tile(sec ? eb : ea, t);
+  }
+#pragma unroll 1
+  while (have) {
+    const bool second = sec != 0;
     KEntry* ep = second ? eb : ea;
     const auto& E = *ep;
     const auto& M = E.M;
-    const int KT = M.KT, NT = M.NT, N = M.N;
-    const int u = T - E.tile0;
-    const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;
+    const int KT = M.KT, N = M.N;
     const int tc = t % KT, tr = t / KT;
-    // the tile's rows (and the 2 the last windows read past the longest lane), 8 rows per copy instruction; the
-    // previous tile's reads of the buffer have completed (each chain waited for its last reads)
-    {
-      const int nrow = (int)M.rows[t] + 2;
-      const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]) + lane;
-      for (int i = 0; i < (nrow + 7) / 8; ++i)
-        __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
-    }
     // side records, x sums and chain starts while the copy is in flight
     const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
     uint32_t sw[NSB][5];
@@ -1506,7 +1553,7 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
     if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
     uint32_t P[NC];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + 4 * f + j) * 32 + (uint32_t)s] - GUARD_BITS;
+    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS;
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // the tile column's activations in VGPRs (lane l holds dwords l, l + 64, ..), read back wave-uniform with
     // v_readlane: no scalar loads inside the decode loop, whose waits would drain every chain's LDS reads
@@ -1518,7 +1565,9 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
       for (int k = 0; k < XV; ++k) xv[k] = xs[64 * k + lane];
     }
     auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
+    if (pend >= 0 && lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float sub[NSUBT];
     float acc[NC];
     int iacc[NC];
@@ -1530,28 +1579,37 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
       wprev[j] = 0;
     }
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi) {
+    for (int gi = 0; gi < NG; ++gi) {
 #pragma unroll
       for (int p = 0; p < 8; ++p) {
         // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
         // (the reads return in order: a chain waits only for its own)
         // the window: word rows P / 32 and P / 32 + 1 of the lane (bits 0-4 of P: the offset; bits >= 16 carry
         // table-entry payload and are ignored)
-        uint32_t w1[NC], e1[NC], e2[NC];
+        // (scheduling barriers keep the stages apart, so every chain's read is issued before the first result is
+        // waited for)
+        uint32_t w1[NC], e1[NC], e2[NC], lo[NC], hi[NC];
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
           LdsU32* wp = (LdsU32*)(rlb + (__builtin_amdgcn_ubfe(P[j], 5, 8) << 7));
-          w1[j] = __builtin_amdgcn_alignbit(wp[32], wp[0], P[j]);
+          lo[j] = wp[0];
+          hi[j] = wp[32];
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+        for (int j = 0; j < NC; ++j) {
+          w1[j] = __builtin_amdgcn_alignbit(hi[j], lo[j], P[j]);
+          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NC; ++j) P[j] = P[j] + e1[j] + e2[j];
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
-          const int g = 4 * j + gi;  // 16-symbol group within the row
+          const int g = NG * j + gi;  // 16-symbol group within the row
           if (I8) {  // as tile_gemv_i8
             if (SYMB == 4) {
               iacc[j] = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u),
@@ -1575,7 +1633,7 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
       if (GPSUB == 1 || (gi & 1)) {
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
-          sub[(4 * j + gi) / GPSUB] = I8 ? (float)iacc[j] : acc[j];  // |iacc| < 2^24: exact
+          sub[(NG * j + gi) / GPSUB] = I8 ? (float)iacc[j] : acc[j];  // |iacc| < 2^24: exact
           acc[j] = 0.f;
           iacc[j] = 0;
         }
@@ -1637,10 +1695,28 @@ __global__ void __launch_bounds__(1024, 1) k_fused_tiles(FlatPlan plan, int R, i
     }
     float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
     __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    row_reduce(E, tr, KT, N, lane);
+    finish_pending();  // the counter's old value has arrived during the decode
+    if (E.Y) {
+      pend = sec;
+      ptr = tr;
+      pKT = KT;
+      pN = N;
+    }
+    // the next tile's copy into the buffer (free: every read of the decode has returned)
     uint32_t nx = 0;
     if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     n = __builtin_amdgcn_readfirstlane((int)nx);
+    have = n < W * R && T0 + n < plan.ntiles;
+    if (have) {
+      tile_of(n, sec, t);
+      copy_tile(sec ? eb : ea, t);
+    }
+  }
+  if (pend >= 0) {  // the last tile's reduction
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finish_pending();
   }
 }
 

@@ -26,8 +26,8 @@ struct Layout {
   uint16_t lut[2048];
   std::vector<uint32_t> tbase;  // [T]
   std::vector<uint16_t> mid;    // [T][32] device bit offset of symbol 256 (guard included)
-  // [T][8][32] device bit offsets of symbols 64 k, k = 0..7 (guard included; k = 4 is mid): the starts of the
-  // low-latency kernel's 8 chains per lane
+  // [T][16][32] device bit offsets of symbols 32 k, k = 0..15 (guard included; k = 8 is mid): the chain starts
+  // of the low-latency kernel (every second one) and the whole-tile kernel
   std::vector<uint16_t> split;
   std::vector<uint16_t> rows;   // [T]
   std::vector<uint32_t> words;  // tiles' word rows + zero tail

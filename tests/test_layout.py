@@ -19,7 +19,7 @@ def build_layout(lib, blob, N, KS, pre_il=0, compact=0, extra=False, splits=Fals
     T = (N // 64) * (KS // 256)
     tbase = np.zeros(T, np.uint32)
     mid = np.zeros(T * 32, np.uint16)
-    split = np.zeros(T * 8 * 32, np.uint16)
+    split = np.zeros(T * 16 * 32, np.uint16)
     rows = np.zeros(T, np.uint16)
     sched = np.zeros(2 * T, np.uint64)
     rr = ctypes.c_int(0)
@@ -31,7 +31,7 @@ def build_layout(lib, blob, N, KS, pre_il=0, compact=0, extra=False, splits=Fals
     lib.lw_build_layout(b.ctypes.data, len(b), N, KS, pre_il, compact, None, None, None, None, None, None,
                         words.ctypes.data, n)
     if splits:
-        return tbase, split.reshape(T, 8, 32), rows, words
+        return tbase, split.reshape(T, 16, 32), rows, words
     if extra:
         return tbase, mid.reshape(T, 32), rows, words, sched, rr.value
     return tbase, mid.reshape(T, 32), rows, words
@@ -241,7 +241,7 @@ def emulate_split(lut, tbase, split, rows, words, N, KS):
             return img[r, l]
         for f in range(2):
             for w in range(4):
-                P = split[t, 4 * f + w].astype(np.int64) - GUARD + 64
+                P = split[t, 2 * (4 * f + w)].astype(np.int64) - GUARD + 64
                 slot = P >> 5
                 A, B, C = row(slot - 2), row(slot - 1), row(slot)
                 col = 64 * w
@@ -263,15 +263,48 @@ def emulate_split(lut, tbase, split, rows, words, N, KS):
     return out
 
 
+def emulate_tiles(lut, tbase, split, rows, words, N, KS):
+    """The whole-tile kernel's decode (k_fused_tiles): lane l of a tile decodes row l (lane stream l % 32, front
+    l / 32) as 8 chains of 32 symbols from the load-time split offsets, each pair's window read straight from rows
+    P / 32 and P / 32 + 1 of the tile image (rows[t] + 2 rows, every read asserted inside it)."""
+    KT = KS // 256
+    lut = lut.astype(np.uint64)
+    out = np.zeros((N, KS), np.uint8)
+    l = np.arange(32)
+    M32 = np.uint64(0xFFFFFFFF)
+    for t in range(len(tbase)):
+        tr, tc = divmod(t, KT)
+        R = int(rows[t]) + 2
+        img = words[int(tbase[t]):int(tbase[t]) + 32 * R].astype(np.uint64).reshape(R, 32)
+        for f in range(2):
+            for j in range(8):
+                P = split[t, 8 * f + j].astype(np.int64) - GUARD
+                col = 32 * j
+                for p in range(16):
+                    r = P >> 5
+                    assert np.all(r >= 0) and np.all(r + 1 < R), (t, "row outside the tile image")
+                    w1 = (((img[r + 1, l] << np.uint64(32)) | img[r, l]) >> (P & 31).astype(np.uint64)) & M32
+                    e1 = lut[(w1 >> np.uint64(GUARD)) & np.uint64(2047)]
+                    w2 = w1 >> (e1 >> np.uint64(8))
+                    e2 = lut[(w2 >> np.uint64(GUARD)) & np.uint64(2047)]
+                    rr = tr * 64 + 32 * f + l
+                    out[rr, tc * 256 + col] = (e1 & np.uint64(255)).astype(np.uint8)
+                    out[rr, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
+                    col += 2
+                    P = P + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+    return out
+
+
 @pytest.mark.parametrize("case", golden_cases())
 def test_split_chain_emulation(lib, case):
-    """The 8 chain starts per lane reproduce the golden decode (k = 0 is the guard, k = 4 is mid)."""
+    """The chain starts per lane reproduce the golden decode (k = 0 is the guard, k = 8 is mid)."""
     g = load_golden(case)
     N, KS = g["sym"].shape
     tbase, split, rows, words = build_layout(lib, g["blob"], N, KS, splits=True)
     _, mid, _, _ = build_layout(lib, g["blob"], N, KS)
-    assert np.all(split[:, 0] == GUARD) and np.array_equal(split[:, 4], mid)
+    assert np.all(split[:, 0] == GUARD) and np.array_equal(split[:, 8], mid)
     assert np.array_equal(emulate_split(g["lut"], tbase, split, rows, words, N, KS), g["decoded"])
+    assert np.array_equal(emulate_tiles(g["lut"], tbase, split, rows, words, N, KS), g["decoded"])
 
 
 def test_split_chain_emulation_exception_tiles(lib):
@@ -284,6 +317,7 @@ def test_split_chain_emulation_exception_tiles(lib):
         tbase, split, rows, words = build_layout(lib, blob, 128, 8192, splits=True)
         lut = np.frombuffer(blob, np.uint16, 2048, 0)
         assert np.array_equal(emulate_split(lut, tbase, split, rows, words, 128, 8192), sym)
+        assert np.array_equal(emulate_tiles(lut, tbase, split, rows, words, 128, 8192), sym)
 
 
 @pytest.mark.parametrize("case", golden_cases())
