@@ -104,10 +104,10 @@ struct QuantJobs {
 hipError_t launch_quant_x8_group(const QuantJobs& q, hipStream_t s);
 // LDS rows the low-latency kernel stages per tile for this plan (max over its matrices of max_rows + 2)
 int split_stage_rows(const FlatPlan& plan);
-// whole-tile kernel for flat launches (m = 1): block = plan.W waves, `rounds` tiles per wave, a tile per wave in
-// LDS at a time (tiles_buf_rows rows), 4 chains per lane; every tile of the entries (exceptions included) and the
-// in-launch reduction for entries with Y
-hipError_t launch_fused_tiles(const FlatPlan& plan, int rounds, hipStream_t s);
+// whole-tile kernel for flat launches (m = 1): block = plan.W waves over `per` consecutive tiles (>= W), a tile per
+// wave in LDS at a time (tiles_buf_rows rows), 8 chains per lane; every tile of the entries (exceptions included)
+// and the in-launch reduction for entries with Y
+hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
 int tiles_buf_rows(const FlatPlan& plan);
 
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes

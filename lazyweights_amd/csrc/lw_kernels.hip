@@ -1436,10 +1436,39 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
   }
 }
 
+// acc += dot2(x, w) with x = lane k of the lane's 16-lane row of xrow (DPP row_newbcast: x held the same in every
+// row, so the broadcast costs no v_readlane); xrow is only ever written by loads, so no VALU-to-DPP hazard arises
+template <int K>
+__device__ __forceinline__ void dot2_bcast(float& acc, uint32_t xrow, uint32_t w) {
+  asm("v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+      : "+v"(acc)
+      : "v"(xrow), "v"(w), "n"(K));
+}
+__device__ __forceinline__ void dot2_row(float& acc, uint32_t xrow, int k, uint32_t w) {
+  switch (k) {  // k is a constant after unrolling
+    case 0: dot2_bcast<0>(acc, xrow, w); break;
+    case 1: dot2_bcast<1>(acc, xrow, w); break;
+    case 2: dot2_bcast<2>(acc, xrow, w); break;
+    case 3: dot2_bcast<3>(acc, xrow, w); break;
+    case 4: dot2_bcast<4>(acc, xrow, w); break;
+    case 5: dot2_bcast<5>(acc, xrow, w); break;
+    case 6: dot2_bcast<6>(acc, xrow, w); break;
+    case 7: dot2_bcast<7>(acc, xrow, w); break;
+    case 8: dot2_bcast<8>(acc, xrow, w); break;
+    case 9: dot2_bcast<9>(acc, xrow, w); break;
+    case 10: dot2_bcast<10>(acc, xrow, w); break;
+    case 11: dot2_bcast<11>(acc, xrow, w); break;
+    case 12: dot2_bcast<12>(acc, xrow, w); break;
+    case 13: dot2_bcast<13>(acc, xrow, w); break;
+    case 14: dot2_bcast<14>(acc, xrow, w); break;
+    default: dot2_bcast<15>(acc, xrow, w); break;
+  }
+}
+
 // ── whole-tile kernel for flat launches (m = 1): a tile per wave, 4 chains per lane ───────────────────────
-// Block = W waves sharing the decode tables; the block decodes tiles [T0, T0 + W R) (spanning at most two
-// matrices), wave w first tile T0 + w, then the next undecoded one from a counter in LDS: the waves of a block do
-// not share a SIMD evenly (13 waves: 4 on one SIMD, 3 on the others), so each SIMD takes tiles at its own rate.
+// Block = W waves sharing the decode tables; the block decodes tiles [T0, T0 + per) (spanning at most two
+// matrices), wave w first tile T0 + w, then the next undecoded one from a counter in LDS, so each SIMD takes
+// tiles at its own rate.
 // A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
 // lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 8 chains of 32 symbols that start at the
 // load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
@@ -1450,7 +1479,7 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
 // keeping the 8 chains' reads in flight)
 template <int KQ, int NTAB, bool I8>
 __global__ void __launch_bounds__(1024, 1)
-k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
+k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
@@ -1473,7 +1502,7 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
   extern __shared__ __align__(16) uint32_t tbuf[];  // W x buf_rows word rows of 32 words
 
   KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
-  const int W = plan.W, T0 = (int)blockIdx.x * W * R, Tl = min(T0 + W * R, plan.ntiles) - 1;
+  const int W = plan.W, T0 = (int)blockIdx.x * per, Tl = min(T0 + per, plan.ntiles) - 1;
   int ma = 0, mb = 0;
 #pragma unroll
   for (int i = 1; i < MAX_GROUP; ++i) {
@@ -1530,7 +1559,7 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
     pend = -1;
   };
   int n = wave;
-  bool have = n < W * R && T0 + n < plan.ntiles;
+  bool have = n < per && T0 + n < plan.ntiles;
   int sec = 0, t = 0;
   if (have) {
     tile_of(n, sec, t);
@@ -1555,14 +1584,19 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
 #pragma unroll
     for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS;
     const uint32_t tsel = second ? 4u * LUTN : 0u;
-    // the tile column's activations in VGPRs (lane l holds dwords l, l + 64, ..), read back wave-uniform with
-    // v_readlane: no scalar loads inside the decode loop, whose waits would drain every chain's LDS reads
-    constexpr int XV = I8 ? TW / 4 / 64 : TW / 2 / 64;
-    uint32_t xv[XV];
-    {
-      const uint32_t* xs = I8 ? reinterpret_cast<const uint32_t*>(E.XQ) + (size_t)tc * (TW / 4) : E.X2 + (size_t)tc * (TW / 2);
+    // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
+    // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
+    // used through DPP broadcasts), int8 x as dwords l, l + 64, .. read back with v_readlane
+    constexpr int XV = I8 ? TW / 4 / 64 : 1, XR = I8 ? 1 : TW / 2 / 16;
+    uint32_t xv[XV], xr[XR];
+    if (I8) {
+      const uint32_t* xs = reinterpret_cast<const uint32_t*>(E.XQ) + (size_t)tc * (TW / 4);
 #pragma unroll
       for (int k = 0; k < XV; ++k) xv[k] = xs[64 * k + lane];
+    } else {
+      const uint32_t* xs = E.X2 + (size_t)tc * (TW / 2) + (lane & 15);
+#pragma unroll
+      for (int m = 0; m < XR; ++m) xr[m] = xs[16 * m];
     }
     auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
@@ -1623,10 +1657,12 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
             const uint32_t v1 = __builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u);
             const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u);
             const int c = 16 * g + 2 * p;
-            acc[j] = dot2(v2, xw(c + 1), dot2(v1, xw(c), acc[j]));
+            dot2_row(acc[j], xr[c >> 4], c & 15, v1);
+            dot2_row(acc[j], xr[(c + 1) >> 4], (c + 1) & 15, v2);
           } else {
             const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
-            acc[j] = dot2(v, xw(8 * g + p), acc[j]);
+            const int c = 8 * g + p;
+            dot2_row(acc[j], xr[c >> 4], c & 15, v);
           }
         }
       }
@@ -1706,7 +1742,7 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
     uint32_t nx = 0;
     if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     n = __builtin_amdgcn_readfirstlane((int)nx);
-    have = n < W * R && T0 + n < plan.ntiles;
+    have = n < per && T0 + n < plan.ntiles;
     if (have) {
       tile_of(n, sec, t);
       copy_tile(sec ? eb : ea, t);
@@ -1721,21 +1757,21 @@ k_fused_tiles(FlatPlan plan, int R, int buf_rows) {
 }
 
 template <int KQ, int NTAB, bool I8>
-static hipError_t tiles_launch_t(const FlatPlan& p, int rounds, int buf_rows, hipStream_t s) {
+static hipError_t tiles_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  const int per = p.W * rounds, blocks = (p.ntiles + per - 1) / per;
-  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p, rounds, buf_rows);
+  const int blocks = (p.ntiles + per - 1) / per;
+  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
   return hipGetLastError();
 }
 
 template <int KQ>
-static hipError_t tiles_launch(const FlatPlan& p, int rounds, int buf_rows, hipStream_t s) {
+static hipError_t tiles_launch(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const bool one = p.n == 1;  // one matrix: one table
-  if (p.i8) return one ? tiles_launch_t<KQ, 1, true>(p, rounds, buf_rows, s) : tiles_launch_t<KQ, 2, true>(p, rounds, buf_rows, s);
-  return one ? tiles_launch_t<KQ, 1, false>(p, rounds, buf_rows, s) : tiles_launch_t<KQ, 2, false>(p, rounds, buf_rows, s);
+  if (p.i8) return one ? tiles_launch_t<KQ, 1, true>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, true>(p, per, buf_rows, s);
+  return one ? tiles_launch_t<KQ, 1, false>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, false>(p, per, buf_rows, s);
 }
 
 int tiles_buf_rows(const FlatPlan& p) {
@@ -1744,13 +1780,13 @@ int tiles_buf_rows(const FlatPlan& p) {
   return (r + 7) / 8 * 8;
 }
 
-hipError_t launch_fused_tiles(const FlatPlan& p, int rounds, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || rounds < 1 || p.ntiles < 1) return hipErrorInvalidValue;
-  const int kqt = p.e[0].M.kqt, per = p.W * rounds;
+hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || per < p.W || p.ntiles < 1) return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
-    // a block (W x rounds consecutive tiles) spans at most two matrices
+    // a block (`per` consecutive tiles) spans at most two matrices
     if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
         (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
@@ -1759,10 +1795,10 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int rounds, hipStream_t s) {
   const int rows = tiles_buf_rows(p);
   if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
   switch (kqt) {
-    case KQ_Q4_K: return tiles_launch<KQ_Q4_K>(p, rounds, rows, s);
-    case KQ_Q5_K: return tiles_launch<KQ_Q5_K>(p, rounds, rows, s);
-    case KQ_Q6_K: return tiles_launch<KQ_Q6_K>(p, rounds, rows, s);
-    case KQ_IQ4_XS: return tiles_launch<KQ_IQ4_XS>(p, rounds, rows, s);
+    case KQ_Q4_K: return tiles_launch<KQ_Q4_K>(p, per, rows, s);
+    case KQ_Q5_K: return tiles_launch<KQ_Q5_K>(p, per, rows, s);
+    case KQ_Q6_K: return tiles_launch<KQ_Q6_K>(p, per, rows, s);
+    case KQ_IQ4_XS: return tiles_launch<KQ_IQ4_XS>(p, per, rows, s);
     default: return hipErrorInvalidValue;
   }
 }

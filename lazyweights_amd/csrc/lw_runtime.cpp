@@ -538,11 +538,11 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
   return 0;
 }
 
-// Waves per block and rounds (tiles per wave) of the whole-tile kernel for a flat plan: one tile buffer per wave
-// (tiles_buf_rows) next to one or two 8 KB tables in 160 KB of LDS; rounds = the tiles per wave that spread the
-// plan over every CU once; a block's W x rounds tiles may span at most two matrices (<= the smallest matrix's tile
-// count). Returns 0 if no width fits.
-int tiles_width(const lw::FlatPlan& fp, int mintiles, int& rounds) {
+// Waves per block and tiles per block of the whole-tile kernel for a flat plan: one tile buffer per wave
+// (tiles_buf_rows) next to one or two 8 KB tables in 160 KB of LDS, at most 16 waves, a multiple of 4 when it can be
+// (the waves of a block then share the 4 SIMDs evenly); `per` = the tiles that spread the plan over every CU once,
+// at most the smallest matrix's tile count (a block spans at most two matrices). Returns 0 if no width fits.
+int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
@@ -552,13 +552,12 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& rounds) {
   }
   const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
   if (rows > 256) return 0;
-  const int wmax = std::min(16, (160 * 1024 - tables) / (rows * 128));
-  if (wmax < 1) return 0;
-  rounds = (fp.ntiles + cus * wmax - 1) / (cus * wmax);
-  int w = std::min(wmax, (fp.ntiles + cus * rounds - 1) / (cus * rounds));
-  if (fp.n > 1)
-    while (w > 1 && w * rounds > mintiles) --w;
-  if (fp.n > 1 && w * rounds > mintiles) rounds = std::max(1, mintiles / w);
+  int w = std::min(16, (160 * 1024 - tables) / (rows * 128));
+  if (w < 1) return 0;
+  if (w >= 4) w &= ~3;
+  per = (fp.ntiles + cus - 1) / cus;
+  if (fp.n > 1) per = std::min(per, mintiles);
+  w = std::min(w, per);
   return w;
 }
 
@@ -607,7 +606,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   // are decoded in place in spare rings when those fit the LDS the launch's block width assumed.
   std::vector<char> done(count, 0), exc_in(count, 0), whole(count, 0);  // whole: every tile in a low-latency launch
   std::vector<lw::FlatPlan> flat_plans, split_plans;
-  std::vector<std::pair<lw::FlatPlan, int>> tile_plans;  // whole-tile kernel launches and their rounds
+  std::vector<std::pair<lw::FlatPlan, int>> tile_plans;  // whole-tile kernel launches and their tiles per block
   // packed (fixed-rate) matrices: the decode-free kernels, one launch per K-quant type and MAX_GROUP matrices
   // (m = 1: the flat one, which also reduces)
   for (int i = 0; mt == 1 && i < count; ++i) {
@@ -678,7 +677,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     fp.ntiles = total;
     if (g_kernel_mode == 6) {  // the whole-tile kernel: every tile, the reduction in the launch
-      int rounds = 0;
+      int rounds = 0;  // tiles per block
       fp.W = tiles_width(fp, mintiles, rounds);
       if (fp.W > 0) {
         for (int k = 0; k < fp.n; ++k) {
