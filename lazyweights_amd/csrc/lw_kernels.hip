@@ -1472,7 +1472,8 @@ __device__ __forceinline__ void dot2_row(float& acc, uint32_t xrow, int k, uint3
 // A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
 // lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 8 chains of 32 symbols that start at the
 // load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
-// chain reads its two window words straight from the buffer for every pair (one ds_read2), no register window.
+// chain keeps its window rows in registers and reads one new row word per pair (LDS instruction issue, about 4
+// cycles per wave-wide read, is what a tile costs: 2 table gathers and 1 row read per pair).
 // There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here. The lane keeps its row's sub-block dot products in registers and forms the row
 // partial in tile_gemv's order (tile_gemv_i8's for int8 activations), the bits of the other kernels.
 // (at most 16 waves per CU by the LDS of the tile buffers: 4 per SIMD, so the scheduler may spend up to 128 VGPRs on
@@ -1582,7 +1583,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
     uint32_t P[NC];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS;
+    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS + 64u;
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
     // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
@@ -1602,6 +1603,16 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
     if (pend >= 0 && lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // register windows: rows r, r + 1 (A, B) of each chain, row r + 2 (C) read after every pair (P = bit
+    // position + 64: bits 5+ give the row C holds)
+    uint32_t slot[NC], A[NC], B[NC], C[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+      C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+    }
     float sub[NSUBT];
     float acc[NC];
     int iacc[NC];
@@ -1618,21 +1629,12 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       for (int p = 0; p < 8; ++p) {
         // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
         // (the reads return in order: a chain waits only for its own)
-        // the window: word rows P / 32 and P / 32 + 1 of the lane (bits 0-4 of P: the offset; bits >= 16 carry
-        // table-entry payload and are ignored)
         // (scheduling barriers keep the stages apart, so every chain's read is issued before the first result is
-        // waited for)
-        uint32_t w1[NC], e1[NC], e2[NC], lo[NC], hi[NC];
+        // waited for; bits >= 16 of P carry table-entry payload and are ignored)
+        uint32_t w1[NC], e1[NC], e2[NC];
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
-          LdsU32* wp = (LdsU32*)(rlb + (__builtin_amdgcn_ubfe(P[j], 5, 8) << 7));
-          lo[j] = wp[0];
-          hi[j] = wp[32];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          w1[j] = __builtin_amdgcn_alignbit(hi[j], lo[j], P[j]);
+          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
           e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1640,7 +1642,15 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
         for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) P[j] = P[j] + e1[j] + e2[j];
+        for (int j = 0; j < NC; ++j) {
+          P[j] = P[j] + e1[j] + e2[j];
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+          const bool slide = nslot != slot[j];  // a pair advances at most 22 bits: at most one row
+          A[j] = slide ? B[j] : A[j];
+          B[j] = slide ? C[j] : B[j];
+          slot[j] = nslot;
+          C[j] = *(LdsU32*)(rlb + (nslot << 7));
+        }
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
           const int g = NG * j + gi;  // 16-symbol group within the row

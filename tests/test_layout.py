@@ -265,8 +265,8 @@ def emulate_split(lut, tbase, split, rows, words, N, KS):
 
 def emulate_tiles(lut, tbase, split, rows, words, N, KS):
     """The whole-tile kernel's decode (k_fused_tiles): lane l of a tile decodes row l (lane stream l % 32, front
-    l / 32) as 8 chains of 32 symbols from the load-time split offsets, each pair's window read straight from rows
-    P / 32 and P / 32 + 1 of the tile image (rows[t] + 2 rows, every read asserted inside it)."""
+    l / 32) as 8 chains of 32 symbols from the load-time split offsets, each with the register window (rows r, r + 1,
+    then row r + 2 after every pair) over the tile image of rows[t] + 2 rows, every read asserted inside it."""
     KT = KS // 256
     lut = lut.astype(np.uint64)
     out = np.zeros((N, KS), np.uint8)
@@ -276,14 +276,18 @@ def emulate_tiles(lut, tbase, split, rows, words, N, KS):
         tr, tc = divmod(t, KT)
         R = int(rows[t]) + 2
         img = words[int(tbase[t]):int(tbase[t]) + 32 * R].astype(np.uint64).reshape(R, 32)
+
+        def row(r):
+            assert np.all(r >= 0) and np.all(r < R), (t, "row outside the tile image")
+            return img[r, l]
         for f in range(2):
             for j in range(8):
-                P = split[t, 8 * f + j].astype(np.int64) - GUARD
+                P = split[t, 8 * f + j].astype(np.int64) - GUARD + 64
+                slot = P >> 5
+                A, B, C = row(slot - 2), row(slot - 1), row(slot)
                 col = 32 * j
                 for p in range(16):
-                    r = P >> 5
-                    assert np.all(r >= 0) and np.all(r + 1 < R), (t, "row outside the tile image")
-                    w1 = (((img[r + 1, l] << np.uint64(32)) | img[r, l]) >> (P & 31).astype(np.uint64)) & M32
+                    w1 = (((B << np.uint64(32)) | A) >> (P & 31).astype(np.uint64)) & M32
                     e1 = lut[(w1 >> np.uint64(GUARD)) & np.uint64(2047)]
                     w2 = w1 >> (e1 >> np.uint64(8))
                     e2 = lut[(w2 >> np.uint64(GUARD)) & np.uint64(2047)]
@@ -292,6 +296,11 @@ def emulate_tiles(lut, tbase, split, rows, words, N, KS):
                     out[rr, tc * 256 + col + 1] = (e2 & np.uint64(255)).astype(np.uint8)
                     col += 2
                     P = P + (e1 >> np.uint64(8)).astype(np.int64) + (e2 >> np.uint64(8)).astype(np.int64)
+                    nslot = P >> 5
+                    slide = nslot != slot
+                    A, B = np.where(slide, B, A), np.where(slide, C, B)
+                    slot = nslot
+                    C = row(slot)
     return out
 
 
