@@ -91,16 +91,18 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * schedule (the flat, load-balanced kernel for m = 1; the block-per-column kernel otherwise); 1 = the whole-tile
  * kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m; 3 = as 0, but exception
  * tiles are never decoded inside the flat launch (always by the separate exception pass); 4 = as 0, with the
- * low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 0, never the low-latency kernel.
- * Returns 0 or -1. */
+ * low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 0, never the low-latency kernel; 6 = as 0,
+ * with the whole-tile-per-wave flat kernel (each tile copied to LDS, 8 chains per lane, every tile including
+ * exception tiles) for every m = 1 launch. Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
-/* Int8 activations for m = 1 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev and
- * lw_group_matmul_dev quantize x per block of 32 (d = max|x| / 127, q = x / d rounded to nearest even, plus d sum q)
- * and the fused kernels take integer dot products per sub-block, y += s d acc - o d sum q. Replaces the reference's
- * act8 switch (kernels/llmrt.cu:2221, LLMRT_FP_ACT; kernels k_quant_x8 / k_gemvm_kq8 at kernels/llmrt.cu:1035-1169),
- * which is on by default there and also covers 2 <= m <= 8; here m > 1 keeps fp16 activations. Needs kernel mode
- * 0, 3, 4 or 5 (the flat kernels). Returns 0 or -1. */
+/* Int8 activations for 1 <= m <= 8 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev
+ * and lw_group_matmul_dev quantize x per block of 32 (d = max|x| / 127, q = x / d rounded to nearest even, plus
+ * d sum q) and the fused kernels take integer dot products per sub-block, y += s d acc - o d sum q. Replaces the
+ * reference's act8 switch (kernels/llmrt.cu:2221, LLMRT_FP_ACT; kernels k_quant_x8 / k_gemvm_kq8 at
+ * kernels/llmrt.cu:1035-1169), which is on by default there. Here m > 1 runs one m = 1 pass per token (the same bits
+ * per token as an m = 1 call; the weights are read once per token). Needs kernel mode 0, 3, 4, 5 or 6 (the flat
+ * kernels). Returns 0 or -1. */
 int lw_set_act8(int on);
 
 /* The int8 quantization of lw_set_act8 on host buffers (test entry, runs the device kernel): X [m, K] fp32 or fp16

@@ -853,14 +853,29 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
 
 // lw_group_matmul_dev's work (fp16 x [m][K_i] per matrix): the fused path, after the quantization launch when int8
 // activations are on (m = 1)
+// Int8-activation matmuls of `count` matrices for m tokens (x [m][K_i], fp16 or fp32, rows K_i apart; y rows ldy
+// apart): one quantization launch and one m = 1 fused pass per token, so every token gets the bits of an m = 1 call
+// (the reference's int8 kernel covers m <= 8 in one pass over the weights; here the weights are read once per token).
+int act8_tokens(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, int m, float* const* Y,
+                const int* ldy, hipStream_t s, int* launches) {
+  std::vector<const void*> xj(count);
+  std::vector<float*> yj(count);
+  std::vector<X8> x8;
+  for (int j = 0; j < m; ++j) {
+    for (int i = 0; i < count; ++i) {
+      xj[i] = static_cast<const char*>(X[i]) + (size_t)j * ts[i]->K * (x_f16 ? 2 : 4);
+      yj[i] = Y[i] + (size_t)j * ldy[i];
+    }
+    if (quant_x8_dev(M, ts, xj.data(), x_f16, count, x8, s)) return -1;
+    if (launches) ++*launches;
+    if (fused_group_dev(M, ts, xj.data(), count, 1, 1, yj.data(), ldy, s, launches, x8.data())) return -1;
+  }
+  return 0;
+}
+
 int group_matmul(Model& M, Tensor* const* ts, const void* const* X, int count, int m, float* const* Y, const int* ldy,
                  hipStream_t s, int* launches = nullptr) {
-  if (g_act8 && m == 1) {
-    std::vector<X8> x8;
-    if (quant_x8_dev(M, ts, X, 1, count, x8, s)) return -1;
-    if (launches) ++*launches;
-    return fused_group_dev(M, ts, X, count, 1, 1, Y, ldy, s, launches, x8.data());
-  }
+  if (g_act8 && m <= 8) return act8_tokens(M, ts, X, 1, count, m, Y, ldy, s, launches);
   return fused_group_dev(M, ts, X, count, m, 1, Y, ldy, s, launches);
 }
 
@@ -990,10 +1005,9 @@ int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, i
     g_err = "rt_test_matmul: device allocation failed";
     return -1;
   }
-  if (g_act8 && m == 1 && path != 2) {  // int8 activations quantized on the device from the fp32 x
-    std::vector<X8> x8;
-    if (hipMalloc(reinterpret_cast<void**>(&dx), K * 4) != hipSuccess ||
-        hipMemcpy(dx, X, K * 4, hipMemcpyHostToDevice) != hipSuccess) {
+  if (g_act8 && m <= 8 && path != 2) {  // int8 activations quantized on the device from the fp32 x
+    if (hipMalloc(reinterpret_cast<void**>(&dx), (size_t)m * K * 4) != hipSuccess ||
+        hipMemcpy(dx, X, (size_t)m * K * 4, hipMemcpyHostToDevice) != hipSuccess) {
       cleanup();
       g_err = "rt_test_matmul: upload failed";
       return -1;
@@ -1001,8 +1015,7 @@ int rt_test_matmul(void* h, const char* name, const float* X, int m, float* Y, i
     const void* xp = dx;
     float* yp = dy;
     const int ld = (int)N;
-    rc = quant_x8_dev(*M, &t, &xp, 0, 1, x8, M->stream);
-    if (!rc) rc = fused_group_dev(*M, &t, &xp, 1, 1, 1, &yp, &ld, M->stream, nullptr, x8.data());
+    rc = act8_tokens(*M, &t, &xp, 0, 1, m, &yp, &ld, M->stream, nullptr);
   } else if (m <= 8 && path != 2) {
     // fp32 activations as fp16 hi + lo pseudo-tokens (x = hi + lo to 2^-22 relative)
     std::vector<uint16_t> x16((size_t)2 * m * K);
@@ -1230,11 +1243,7 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
   Tensor* t = M->find(name);
   if (check_matmul(t, name)) return -1;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (g_act8 && m == 1) {
-    std::vector<X8> x8;
-    if (quant_x8_dev(*M, &t, &X, x_f16, 1, x8, s)) return -1;
-    return fused_group_dev(*M, &t, &X, 1, 1, 1, &Y, &ldy, s, nullptr, x8.data());
-  }
+  if (g_act8 && m >= 1 && m <= 8) return act8_tokens(*M, &t, &X, x_f16, 1, m, &Y, &ldy, s, nullptr);
   if (x_f16) {
     if (m < 1 || m > 16) {
       g_err = "lw_matmul_dev: fp16 activations need 1 <= m <= 16";

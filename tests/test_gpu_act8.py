@@ -94,7 +94,8 @@ def check(y, ref, tol, what):
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_act8_gemv(a8_rt, orc, lib, act8, kqt, fmt, H):
     """rt_test_matmul (fp32 host x) and lw_matmul_dev (fp16 and fp32 device x) at m = 1 against the oracle's int8
-    GEMV; m = 3 keeps the fp16 path (within the contract tolerance of fp64)."""
+    GEMV; m = 3 (one pass per token): every token against the oracle and equal to its own m = 1 call; m = 12 (beyond
+    the int8 range) keeps fp32 activations on the prefill path (within 2e-5 of fp64)."""
     import torch
     rc, rp, mats = a8_rt
     rng = np.random.default_rng(kqt)
@@ -120,8 +121,14 @@ def test_gpu_act8_gemv(a8_rt, orc, lib, act8, kqt, fmt, H):
         y8h, _ = y_act8(orc, mat, x16.float().numpy())
         check(Yh.cpu().numpy(), y8h, TOL_ACT8, nm + " act8 fp16 device")
         X3 = rng.standard_normal((3, K)).astype(np.float32)
-        _, y64_3 = y_act8(orc, mat, X3)
-        check(rc.test_matmul(nm, X3), y64_3, 2e-5, nm + " m=3 stays fp16 hi + lo")
+        y8_3, _ = y_act8(orc, mat, X3)
+        Y3 = rc.test_matmul(nm, X3)
+        check(Y3, y8_3, TOL_ACT8, nm + " act8 m=3")
+        for j in range(3):
+            assert np.array_equal(Y3[j], rc.test_matmul(nm, X3[j:j + 1])[0]), (nm, j)
+        X12 = rng.standard_normal((12, K)).astype(np.float32)
+        _, y64_12 = y_act8(orc, mat, X12)
+        check(rc.test_matmul(nm, X12), y64_12, 2e-5, nm + " m=12 stays fp32 (prefill path)")
 
 
 def group(rt, names, xs):
