@@ -56,7 +56,8 @@ struct GroupPlan {
   int mt;
   int blocks;
 };
-// Matrices of one launch of the flat ring kernel (m = 1; same K-quant type and ring size). Their tiles form one list:
+// Matrices of one launch of the flat ring kernel (m = 1, or up to 8 tokens of int8 activations; same K-quant type and
+// ring size). Their tiles form one list:
 // matrix i owns tiles [tile0, tile0 + NT * KT), column-major; block b decodes tiles [b W, b W + W). Every matrix must
 // have at least W tiles, so a block spans at most two matrices.
 struct FlatEntry {
@@ -69,10 +70,12 @@ struct FlatEntry {
   // in the launch by the last wave of each tile row; cnt = NT zeroed counters (left zeroed)
   float* Y;
   uint32_t* cnt;
-  // int8 activations (plan.i8): x quantized per 32 weights (launch_quant_x8): XQ [K] int8, DX / SX [K / 32]
+  // int8 activations (plan.i8): x quantized per 32 weights (launch_quant_x8): XQ [mt][K] int8, DX / SX [mt][K / 32]
   const int8_t* XQ;
   const float* DX;
   const float* SX;
+  // plan.mt > 1: P is [KT][mt][N] and token j's Y row starts at Y + j ldy
+  int ldy;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];
@@ -82,9 +85,12 @@ struct FlatPlan {
   // 16-row launches: spare 16-row ring pairs per block for exception tiles with a 32-row schedule (>= the most
   // such tiles in any block); 0: exception tiles are skipped (decoded by an exception pass)
   int nspare;
-  int i8;  // 1: int8 activations (the entries' XQ / DX / SX), m = 1
+  int i8;  // 1: int8 activations (the entries' XQ / DX / SX)
+  int mt;  // tokens: 0 or 1, or 2..8 with int8 activations (the flat ring and low-latency kernels, one pass)
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
+// waves of the flat kernel one CU holds at once (its register use) for int8 activations, mt tokens (1, or 2..8)
+int flat_waves_per_cu(int kqt, int rs, int mt);
 // The low-latency kernel over the same kind of plan (one tile per block of 4 waves, 8 chains per lane; W and
 // nspare are ignored; exception tiles included). Every matrix needs a K-quant table and the split offsets.
 hipError_t launch_fused_split(const FlatPlan& plan, hipStream_t s);

@@ -772,43 +772,36 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 // device-coherent loads. No-op when the entry has no Y (the partials are reduced by a separate launch).
 // The sum of tile row tr's partials by the wave that counted the row's last tile (resets the counter).
 template <class KEntryRef>
-__device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane) {
+__device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
   if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
-  float a = 0.f;
-  for (int c0 = 0; c0 < KT; c0 += 16) {
-    float v[16];
+  // P is [KT][mt][N]: token j's partial of tile column c at P + (c mt + j) N
+  for (int j = 0; j < mt; ++j) {
+    const float* pr = E.P + (size_t)j * N + (size_t)tr * TN + (uint32_t)lane;
+    const size_t cs = (size_t)mt * N;
+    float a = 0.f;
+    for (int c0 = 0; c0 < KT; c0 += 16) {
+      float v[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      for (int c = 0; c < 16; ++c)
+        v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * cs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.f;
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c0 + c < KT) a += v[c];
+      for (int c = 0; c < 16; ++c)
+        if (c0 + c < KT) a += v[c];
+    }
+    E.Y[(size_t)j * (mt > 1 ? E.ldy : 0) + (size_t)tr * TN + (uint32_t)lane] = a;
   }
-  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
 }
 
 template <class KEntryRef>
-__device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane) {
+__device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
   if (!E.Y) return;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   uint32_t old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __builtin_amdgcn_readlane(old, 0);
   if (old != (uint32_t)(KT - 1)) return;
-  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const float* pr = E.P + (size_t)tr * TN + (uint32_t)lane;
-  float a = 0.f;
-  for (int c0 = 0; c0 < KT; c0 += 16) {
-    float v[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c0 + c < KT) a += v[c];
-  }
-  E.Y[(size_t)tr * TN + (uint32_t)lane] = a;
+  row_sum(E, tr, KT, N, lane, mt);
 }
 
 // One tile column's x sums per sub-block (m = 1), as wave-uniform values: lane 4 g + k sums quarter k of sub-block
@@ -901,16 +894,25 @@ hipError_t launch_quant_x8_group(const QuantJobs& q, hipStream_t s) {
 // integer dot product of the int8 grid values with the quantized x (v_dot4_i32_i8, 4 weights per step), then
 // y += s d_x acc - o s_x with s = d sc, o = dmin m per sub-block and d_x, s_x of the sub-block's 32-block.
 // xq4 = the tile column's quantized x as 4-byte words, dx / sx its 32-block scales (scalar loads).
-template <int KQ, class Src>
+// MT > 1 (the reference's MT-token kernel, kernels/llmrt.cu:1057-1169): tokens j < mt in one pass over the codes;
+// token j's x lies xw words (xq4) and xb blocks (dx, sx) after token 0's and its partial at out + j ostride. A
+// group's 8 pairs are decoded into 8 (4-bit formats) or 4 (8-bit formats) words of 4 grid bytes, then each token
+// takes them in pair order: every token gets the operations, in the same order, of an m = 1 pass.
+template <int KQ, int MT = 1, class Src>
 __device__ __forceinline__ void tile_gemv_i8(Src& src, __attribute__((address_space(4))) const uint32_t* xq4,
                                              __attribute__((address_space(4))) const float* dx,
                                              __attribute__((address_space(4))) const float* sx,
-                                             const uint8_t* srow, float* out) {
+                                             const uint8_t* srow, float* out, int mt = 1, int xw = 0, int xb = 0,
+                                             int ostride = 0) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
   constexpr int NSB = TW / 256, GPS = 16 / NSB, NSUB = 256 / GW, GPSUB = GPS / NSUB;
-  float tot = 0.f;
+  constexpr int NW = SYMB == 4 ? 8 : 4;  // words of 4 grid bytes per 16-symbol group
+  float tot[MT];
+  int acc[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) tot[j] = 0.f;
 #pragma unroll 1
   for (int sb = 0; sb < NSB; ++sb) {
     uint32_t sw[5];
@@ -919,7 +921,8 @@ __device__ __forceinline__ void tile_gemv_i8(Src& src, __attribute__((address_sp
     uint64_t scq, scq2;
     side_packed<KQ>(sw, scq, scq2, dA, dB);
     if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw, mf);
-    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[j] = 0;
     uint32_t wprev = 0;
 #pragma unroll 1
     for (int gg2 = 0; gg2 < GPS; gg2 += 2) {
@@ -928,31 +931,73 @@ __device__ __forceinline__ void tile_gemv_i8(Src& src, __attribute__((address_sp
       for (int h = 0; h < 2; ++h) {
         const int g = sb * GPS + gg2 + h;
         src.stage(g);
+        if (MT == 1) {
 #pragma unroll 8
-        for (int p = 0; p < 8; ++p) {
-          uint32_t e1, e2;
-          src.pair(p, e1, e2);
-          if (SYMB == 4) {
-            acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2, e1, 0x07060302u), (int)xq4[8 * g + p], acc, false);
-          } else {
-            const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);  // f(q1), f(q2) in bytes 0, 1
-            if (p & 1) acc = __builtin_amdgcn_sdot4((int)(wprev | (w2 << 16)), (int)xq4[4 * g + p / 2], acc, false);
-            else wprev = w2;
+          for (int p = 0; p < 8; ++p) {
+            uint32_t e1, e2;
+            src.pair(p, e1, e2);
+            if (SYMB == 4) {
+              acc[0] = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2, e1, 0x07060302u), (int)xq4[8 * g + p],
+                                              acc[0], false);
+            } else {
+              const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);  // f(q1), f(q2) in bytes 0, 1
+              if (p & 1) acc[0] = __builtin_amdgcn_sdot4((int)(wprev | (w2 << 16)), (int)xq4[4 * g + p / 2], acc[0], false);
+              else wprev = w2;
+            }
+          }
+        } else {
+          uint32_t wv[NW];
+#pragma unroll
+          for (int p = 0; p < 8; ++p) {
+            uint32_t e1, e2;
+            src.pair(p, e1, e2);
+            if (SYMB == 4) {
+              wv[p] = __builtin_amdgcn_perm(e2, e1, 0x07060302u);
+            } else {
+              const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);
+              if (p & 1) wv[p / 2] = wprev | (w2 << 16);
+              else wprev = w2;
+            }
+          }
+          // the tokens' x walk from token 0's by xw words; the stride is made opaque here so that the compiler does
+          // not keep MT precomputed addresses live across the loop (they would not fit the scalar registers)
+          int xws = xw;
+          asm volatile("" : "+s"(xws));
+          __attribute__((address_space(4))) const uint32_t* xj = xq4 + NW * g;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            if (j < mt) {
+#pragma unroll
+              for (int q = 0; q < NW; ++q) acc[j] = __builtin_amdgcn_sdot4((int)wv[q], (int)xj[q], acc[j], false);
+            }
+            xj += xws;
           }
         }
         if (GPSUB == 1 || h == 1) {  // sub-block end
-          const int jj = (gg2 + h) / GPSUB, xb = (sb * 256 + jj * GW) / 32;
+          const int jj = (gg2 + h) / GPSUB, b = (sb * 256 + jj * GW) / 32;
           const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
                                                                : (float)(uint32_t)(scq & 255u);
           scq >>= 8;
-          tot = fmaf(dA * scv * dx[xb], (float)acc, tot);
-          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
-          acc = 0;
+          int xbs = xb;
+          if (MT > 1) asm volatile("" : "+s"(xbs));
+          __attribute__((address_space(4))) const float *dj = dx + b, *sj = sx + b;
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            if (j < mt) {
+              tot[j] = fmaf(dA * scv * dj[0], (float)acc[j], tot[j]);
+              if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot[j] = fmaf(-(dB * mf[jj]), sj[0], tot[j]);
+              acc[j] = 0;
+            }
+            dj += xbs;
+            sj += xbs;
+          }
         }
       }
     }
   }
-  __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int j = 0; j < MT; ++j)
+    if (j < mt) __hip_atomic_store(out + (size_t)j * ostride, tot[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ── packed (fixed-rate) twin: decode-free fused GEMV / skinny GEMM ─────────────────────────────────────────
@@ -1016,19 +1061,21 @@ __global__ void __launch_bounds__(1024, MT <= 2 ? 2 : 1) k_fused_packed(GroupPla
     tile_gemv<KQ, MT>(src, xs, XgLds{xg, MT, 256 / GW}, xcol, srow, mt, N, out);
 }
 
-// m = 1 tile of a flat launch: fp16 activations (tile_gemv) or int8 activations (tile_gemv_i8, the entry's XQ / DX /
-// SX for tile column tc)
-template <int KQ, bool I8, class Src, class KEntryRef>
+// One tile of a flat launch: fp16 activations, m = 1 (tile_gemv) or int8 activations (tile_gemv_i8, the entry's XQ /
+// DX / SX for tile column tc; MT > 1: tokens j < mt, partials N apart)
+template <int KQ, bool I8, int MT = 1, class Src, class KEntryRef>
 __device__ __forceinline__ void tile_body(Src& src, const KEntryRef& E, int tc, const XgRegs& xgr,
                                           __attribute__((address_space(4))) const uint32_t* xcol, const uint8_t* srow,
-                                          int N, float* out) {
+                                          int N, float* out, int mt = 1) {
   constexpr int TW = kq_symbits(KQ) == 4 ? 2 * TK : TK;
   typedef __attribute__((address_space(4))) const uint32_t KU32;
   typedef __attribute__((address_space(4))) const float KF32;
-  if (I8)
-    tile_gemv_i8<KQ>(src, (KU32*)(E.XQ + (size_t)tc * TW), (KF32*)(E.DX + (size_t)tc * (TW / 32)),
-                     (KF32*)(E.SX + (size_t)tc * (TW / 32)), srow, out);
-  else
+  if (I8) {
+    // tc and K are wave-uniform: said so, the tokens' x addresses stay in scalar registers
+    const int tcu = __builtin_amdgcn_readfirstlane(tc), K = MT > 1 ? __builtin_amdgcn_readfirstlane(E.M.K) : 0;
+    tile_gemv_i8<KQ, MT>(src, (KU32*)(E.XQ + (size_t)tcu * TW), (KF32*)(E.DX + (size_t)tcu * (TW / 32)),
+                         (KF32*)(E.SX + (size_t)tcu * (TW / 32)), srow, out, mt, K / 4, K / 32, N);
+  } else
     tile_gemv<KQ, 1, true>(src, nullptr, xgr, xcol, srow, 1, N, out);
 }
 
@@ -1089,9 +1136,10 @@ __global__ void __launch_bounds__(1024) k_fused_packed_flat(FlatPlan plan) {
 
 // ── ring kernel over a flat tile list (m = 1): balanced blocks ───────────────────────────────────────────
 // One tile of the flat kernel: lanes of front f stage into `ring` (RS rows of 32 words).
-template <int KQ, bool I8, class KEntryRef>
+template <int KQ, bool I8, int MT, class KEntryRef>
 __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4& sc, uint32_t* ring, uint32_t rmask,
-                                          const uint32_t* lut4, uint32_t lutsel, const XgRegs& xgr, int lane) {
+                                          const uint32_t* lut4, uint32_t lutsel, const XgRegs& xgr, int lane,
+                                          int mt) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int NPAIR = TW / 2;
@@ -1108,7 +1156,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
   asm volatile("" : "+v"(rlb));
   const uint8_t* srow = M.side + side_record(tr * TN, tc * (TW / 256), KT, TW / 256) * kq_sbytes(KQ) +
                         (uint32_t)((f * 32 + l) * kq_sbytes(KQ));
-  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
+  float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)(f * 32 + l);
   const uint32_t init0 = (sc.z >> 8) & 255u, init1 = (sc.z >> 16) & 255u;
   if (sc.x == sc.y && init0 == init1) {  // one schedule for both fronts: scalar staging
     RingStager<int, uint32_t> st;
@@ -1118,7 +1166,7 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.rmask = rmask;
     st.init((int)init0);
     RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
-    tile_body<KQ, I8>(src, E, tc, xgr, xcol, srow, N, out);
+    tile_body<KQ, I8, MT>(src, E, tc, xgr, xcol, srow, N, out, mt);
   } else {
     RingStager<int, uint32_t> st;
     st.lane_slot = lane_slot;
@@ -1127,9 +1175,9 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
     st.rmask = rmask;
     st.init((int)(f ? init1 : init0));
     RingSrc<RingStager<int, uint32_t>> src(st, lut4, lutsel, P, rlb);
-    tile_body<KQ, I8>(src, E, tc, xgr, xcol, srow, N, out);
+    tile_body<KQ, I8, MT>(src, E, tc, xgr, xcol, srow, N, out, mt);
   }
-  row_reduce(E, tr, KT, N, lane);
+  row_reduce(E, tr, KT, N, lane, mt);
 }
 
 // The tiles of the plan's matrices form one list (matrix by matrix, each column-major: tile rows of one tile
@@ -1141,8 +1189,9 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
 // Exception tiles (no 16-row schedule) are skipped, except with plan.nspare > 0 in a 16-row launch: then a tile
 // with a 32-row schedule is decoded in place, front 0 in the wave's own two rings (4 KB) and front 1 in spare ring
 // k of the block, k = the number of such tiles before it in the block (the host sizes nspare to the block maximum).
-template <int KQ, int RS, int NTAB, bool I8>
-__global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
+// MT > 1 (int8 activations only): tokens j < plan.mt in one pass, partials [KT][mt][N].
+template <int KQ, int RS, int NTAB, bool I8, int MT = 1>
+__global__ void __launch_bounds__(1024, MT == 1 ? 2 : 1) k_fused_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ);
@@ -1182,10 +1231,13 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   const uint32_t lutsel = second ? (uint32_t)(LUTN * 4) : 0u;
   const int KT = M.KT, NT = M.NT;
   const int u = T - E.tile0;
-  const int t = E.list ? (int)E.list[u] : (u % NT) * KT + u / NT;  // column-major order, or the exception list
+  // wave-uniform (one tile per wave): said so, the tile's addresses and schedule stay in scalar registers
+  const int t = __builtin_amdgcn_readfirstlane(E.list ? (int)E.list[u] : (u % NT) * KT + u / NT);
   const int tc = t % KT;
   const int lane = threadIdx.x & 63;
-  const uint4 sc = M.sched[t];
+  const uint4 sc0 = M.sched[t];
+  const uint4 sc = make_uint4(__builtin_amdgcn_readfirstlane(sc0.x), __builtin_amdgcn_readfirstlane(sc0.y),
+                              __builtin_amdgcn_readfirstlane(sc0.z), __builtin_amdgcn_readfirstlane(sc0.w));
   int spare = -1;
   if (!E.list && (sc.w & 1u)) {  // exception tile
     if (RS != 16 || !plan.nspare || !(sc.w & 2u)) return;  // decoded by the exception pass
@@ -1208,7 +1260,7 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
   const int f = lane >> 5;
   const bool x32 = RS == 16 && spare >= 0;
   uint32_t* ring = rings + (x32 ? (f ? 2 * W + 2 * spare : 2 * wave) : 2 * wave + f) * RING_WORDS;
-  flat_tile<KQ, I8>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane);
+  flat_tile<KQ, I8, MT>(E, t, sc, ring, x32 ? 31u : (uint32_t)(RS - 1), lut4, lutsel, xgr, lane, MT == 1 ? 1 : plan.mt);
 }
 
 // ── low-latency kernel (m = 1): one tile per block, 8 chains per lane ───────────────────────────────────
@@ -1219,7 +1271,9 @@ __global__ void __launch_bounds__(1024, 2) k_fused_flat(FlatPlan plan) {
 // register window reading the tile image directly. Each chain stores its sub-block dot products in LDS; wave 0
 // then forms each row's partial exactly as tile_gemv does (same operations in the same order), so the result has
 // the same bits as the ring kernels'. Exception tiles need nothing special: no staging schedule is involved.
-template <int KQ, bool I8>
+// MT > 1 (int8 activations only): tokens j < plan.mt in one pass (chain dot products per token), partials
+// [KT][mt][N].
+template <int KQ, bool I8, int MT = 1>
 __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_rows) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -1231,9 +1285,10 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
   constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   // one static LDS object, so the table sits at LDS address 0 (table_addr ORs its base into the index bits)
-  __shared__ uint32_t lds_static[LUTN + TN * NSUBT];
+  __shared__ uint32_t lds_static[LUTN + TN * NSUBT * MT];
   uint32_t* lut4 = lds_static;
-  float* accb = reinterpret_cast<float*>(lds_static + LUTN);  // [row][sub-block] dot products of the chains
+  float* accb = reinterpret_cast<float*>(lds_static + LUTN);  // [row][sub-block][token] dot products of the chains
+  const int mt = MT == 1 ? 1 : plan.mt;
   extern __shared__ __align__(16) uint32_t tw[];              // the tile's word rows [stage_rows][32]
 
   typedef __attribute__((address_space(4))) const char KChar;
@@ -1281,15 +1336,18 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
     uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
     asm volatile("" : "+v"(rlb));
     KU32* xcol = (KU32*)(E.X2 + (size_t)tc * (TW / 2));
-    KU32* xq4 = (KU32*)(E.XQ + (size_t)tc * TW);
+    KU32* xq4 = (KU32*)(E.XQ + (size_t)__builtin_amdgcn_readfirstlane(tc) * TW);
     uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
     uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
     uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
     uint32_t C = *(LdsU32*)(rlb + (slot << 7));
-    float* accrow = accb + (f * 32 + l) * NSUBT;
+    float* accrow = accb + (f * 32 + l) * NSUBT * MT;
     float acc = 0.f;
-    int iacc = 0;
-    uint32_t wprev = 0;
+    int iacc = 0, iaccm[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) iaccm[j] = 0;
+    constexpr int NW = SYMB == 4 ? 8 : 4;  // MT > 1: words of 4 grid bytes per group, as tile_gemv_i8
+    uint32_t wprev = 0, wv[NW];
 #pragma unroll 1
     for (int gi = 0; gi < 4; ++gi) {
       const int g = 4 * wave + gi;  // 16-symbol group within the row
@@ -1306,7 +1364,15 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
         B = slide ? C : B;
         slot = nslot;
         C = *(LdsU32*)(rlb + (nslot << 7));
-        if (I8) {  // as tile_gemv_i8
+        if (I8 && MT > 1) {
+          if (SYMB == 4) {
+            wv[p] = __builtin_amdgcn_perm(e2, e1, 0x07060302u);
+          } else {
+            const uint32_t w2 = __builtin_amdgcn_perm(e2, e1, 0x0C0C0602u);
+            if (p & 1) wv[p / 2] = wprev | (w2 << 16);
+            else wprev = w2;
+          }
+        } else if (I8) {  // as tile_gemv_i8
           if (SYMB == 4) {
             iacc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2, e1, 0x07060302u), (int)xq4[8 * g + p], iacc, false);
           } else {
@@ -1323,8 +1389,25 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
           acc = dot2(w, xcol[8 * g + p], acc);
         }
       }
+      if (I8 && MT > 1) {
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          if (j < mt) {
+            KU32* xj = xq4 + (size_t)j * (uint32_t)(__builtin_amdgcn_readfirstlane(M.K) / 4) + NW * g;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) iaccm[j] = __builtin_amdgcn_sdot4((int)wv[q], (int)xj[q], iaccm[j], false);
+          }
+      }
       if (GPSUB == 1 || (gi & 1)) {
-        accrow[g / GPSUB] = I8 ? (float)iacc : acc;  // |iacc| < 2^24: exact
+        if (I8 && MT > 1) {
+#pragma unroll
+          for (int j = 0; j < MT; ++j) {
+            accrow[(g / GPSUB) * MT + j] = (float)iaccm[j];
+            iaccm[j] = 0;
+          }
+        } else {
+          accrow[g / GPSUB] = I8 ? (float)iacc : acc;  // |iacc| < 2^24: exact
+        }
         acc = 0.f;
         iacc = 0;
       }
@@ -1335,28 +1418,35 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
 
   // row partials, as tile_gemv forms them: per super-block the min / bias term first, then d x the scaled sum of
   // the sub-block dot products in order
-  const float* accrow = accb + lane * NSUBT;
+  const float* accrow = accb + lane * NSUBT * MT;
   float tot = 0.f;
-  if (I8) {  // tile_gemv_i8's order: per sub-block s d_x acc, then - o s_x
+  if (I8) {  // tile_gemv_i8's order: per sub-block s d_x acc, then - o s_x; token by token
     typedef __attribute__((address_space(4))) const float KF32;
-    KF32* dx = (KF32*)(E.DX + (size_t)tc * (TW / 32));
-    KF32* sx = (KF32*)(E.SX + (size_t)tc * (TW / 32));
+#pragma unroll 1
+    for (int j = 0; j < mt; ++j) {
+      KF32* dx = (KF32*)(E.DX + (size_t)j * (M.K / 32) + (size_t)tc * (TW / 32));
+      KF32* sx = (KF32*)(E.SX + (size_t)j * (M.K / 32) + (size_t)tc * (TW / 32));
+      tot = 0.f;
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) {
-      float dA, dB, mf[8];
-      uint64_t scq, scq2;
-      side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
-      if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
+      for (int sb = 0; sb < NSB; ++sb) {
+        float dA, dB, mf[8];
+        uint64_t scq, scq2;
+        side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
 #pragma unroll
-      for (int jj = 0; jj < NSUB; ++jj) {
-        if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
-        const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
-                                                             : (float)(uint32_t)(scq & 255u);
-        scq >>= 8;
-        const int xb = (sb * 256 + jj * GW) / 32;
-        tot = fmaf(dA * scv * dx[xb], accrow[sb * NSUB + jj], tot);
-        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+        for (int jj = 0; jj < NSUB; ++jj) {
+          if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                               : (float)(uint32_t)(scq & 255u);
+          scq >>= 8;
+          const int xb = (sb * 256 + jj * GW) / 32;
+          tot = fmaf(dA * scv * dx[xb], accrow[(sb * NSUB + jj) * MT + (MT > 1 ? j : 0)], tot);
+          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+        }
       }
+      if (j + 1 < mt)
+        __hip_atomic_store(E.P + ((size_t)tc * mt + j) * N + (size_t)tr * TN + (uint32_t)lane, tot, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 #pragma unroll
@@ -1388,24 +1478,33 @@ __global__ void __launch_bounds__(256) k_fused_split(FlatPlan plan, int stage_ro
     }
     tot = fmaf(dA * VSCALE, tsum, tot);
   }
-  float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
+  float* out = E.P + ((size_t)tc * mt + (mt - 1)) * N + (size_t)tr * TN + (uint32_t)lane;  // the last token's
   __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  row_reduce(E, tr, KT, N, lane);
+  row_reduce(E, tr, KT, N, lane, mt);
 }
 
-template <int KQ, bool I8>
+template <int KQ, bool I8, int MT = 1>
 static hipError_t split_launch_t(const FlatPlan& p, int stage_rows, hipStream_t s) {
   const size_t smem = (size_t)stage_rows * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_split<KQ, I8>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_split<KQ, I8, MT>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((k_fused_split<KQ, I8>), dim3(p.ntiles), dim3(256), smem, s, p, stage_rows);
+  hipLaunchKernelGGL((k_fused_split<KQ, I8, MT>), dim3(p.ntiles), dim3(256), smem, s, p, stage_rows);
   return hipGetLastError();
 }
 
 template <int KQ>
 static hipError_t split_launch(const FlatPlan& p, int stage_rows, hipStream_t s) {
+  if (p.mt > 1) return split_launch_t<KQ, true, 8>(p, stage_rows, s);
   return p.i8 ? split_launch_t<KQ, true>(p, stage_rows, s) : split_launch_t<KQ, false>(p, stage_rows, s);
+}
+
+// the tokens of a flat plan: 0 / 1, or 2..8 with int8 activations (then every entry's Y needs ldy >= N)
+static bool flat_tokens_ok(const FlatPlan& p) {
+  if (p.mt < 0 || p.mt > 8 || (p.mt > 1 && !p.i8)) return false;
+  for (int i = 0; p.mt > 1 && i < p.n; ++i)
+    if (p.e[i].Y && p.e[i].ldy < p.e[i].M.N) return false;
+  return true;
 }
 
 int split_stage_rows(const FlatPlan& p) {
@@ -1425,8 +1524,9 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
         (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
       return hipErrorInvalidValue;
   }
+  if (!flat_tokens_ok(p)) return hipErrorInvalidValue;
   const int rows = split_stage_rows(p);
-  if (rows > 256 || rows * 128 + 4 * LUTN + TN * 16 * 4 > 160 * 1024) return hipErrorInvalidValue;
+  if (rows > 256 || rows * 128 + 4 * LUTN + TN * 16 * 4 * (p.mt > 1 ? 8 : 1) > 160 * 1024) return hipErrorInvalidValue;
   switch (kqt) {
     case KQ_Q4_K: return split_launch<KQ_Q4_K>(p, rows, s);
     case KQ_Q5_K: return split_launch<KQ_Q5_K>(p, rows, s);
@@ -1791,7 +1891,8 @@ int tiles_buf_rows(const FlatPlan& p) {
 }
 
 hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || per < p.W || p.ntiles < 1) return hipErrorInvalidValue;
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || per < p.W || p.ntiles < 1 || p.mt > 1)
+    return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
@@ -1813,22 +1914,45 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
   }
 }
 
-template <int KQ, int RS, int NTAB, bool I8>
+template <int KQ, int RS, int NTAB, bool I8, int MT = 1>
 static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
   const size_t smem = (size_t)(p.W + p.nspare) * 2 * RS * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB, I8>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, NTAB, I8, MT>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + p.W - 1) / p.W;
-  hipLaunchKernelGGL((k_fused_flat<KQ, RS, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p);
+  hipLaunchKernelGGL((k_fused_flat<KQ, RS, NTAB, I8, MT>), dim3(blocks), dim3(p.W * 64), smem, s, p);
   return hipGetLastError();
 }
 
 // one-wave blocks never span two matrices: one table
 template <int KQ, int RS>
 static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
+  if (p.mt > 1) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true, 8>(p, s) : flat_launch_t<KQ, RS, 2, true, 8>(p, s);
   if (p.i8) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true>(p, s) : flat_launch_t<KQ, RS, 2, true>(p, s);
   return p.W == 1 ? flat_launch_t<KQ, RS, 1, false>(p, s) : flat_launch_t<KQ, RS, 2, false>(p, s);
+}
+
+// Waves of the flat kernel for (kqt, rs, i8 tokens mt) one CU holds at once by its register use (4 SIMDs x 512
+// VGPRs, allocated in 8s; at most 8 waves per SIMD), 0 for an unknown configuration.
+template <int KQ, int RS>
+static int flat_waves_t(int mt) {
+  hipFuncAttributes a{};
+  const void* f = mt > 1 ? reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true, 8>)
+                         : reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true>);
+  if (hipFuncGetAttributes(&a, f) != hipSuccess || a.numRegs < 1) return 0;
+  return 4 * std::min(8, 512 / ((a.numRegs + 7) / 8 * 8));
+}
+
+int flat_waves_per_cu(int kqt, int rs, int mt) {
+  if (rs != 16 && rs != 32) return 0;
+  switch (kqt) {
+    case KQ_Q4_K: return rs == 16 ? flat_waves_t<KQ_Q4_K, 16>(mt) : flat_waves_t<KQ_Q4_K, 32>(mt);
+    case KQ_Q5_K: return rs == 16 ? flat_waves_t<KQ_Q5_K, 16>(mt) : flat_waves_t<KQ_Q5_K, 32>(mt);
+    case KQ_Q6_K: return rs == 16 ? flat_waves_t<KQ_Q6_K, 16>(mt) : flat_waves_t<KQ_Q6_K, 32>(mt);
+    case KQ_IQ4_XS: return rs == 16 ? flat_waves_t<KQ_IQ4_XS, 16>(mt) : flat_waves_t<KQ_IQ4_XS, 32>(mt);
+    default: return 0;
+  }
 }
 
 hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
@@ -1844,6 +1968,7 @@ hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
       return hipErrorInvalidValue;
   }
   if (rs != 16 && rs != 32) return hipErrorInvalidValue;
+  if (!flat_tokens_ok(p)) return hipErrorInvalidValue;
   if (rs == 32 && p.W > 8) return hipErrorInvalidValue;  // LDS: 16 KB of tables + W x 8 KB of rings
   // spare rings: 16-row launches only, within the LDS of one CU (160 KB: 16 KB of tables + 32 x 4 KB of rings)
   if (p.nspare < 0 || (p.nspare && (rs != 16 || p.W + p.nspare > 32))) return hipErrorInvalidValue;
@@ -1906,7 +2031,7 @@ static hipError_t packed_flat_launch(const FlatPlan& p, int blocks, size_t smem,
 }
 
 hipError_t launch_fused_packed_flat(const FlatPlan& p, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || p.ntiles < 1) return hipErrorInvalidValue;
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || p.ntiles < 1 || p.mt > 1) return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];

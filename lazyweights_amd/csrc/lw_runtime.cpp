@@ -423,9 +423,10 @@ int g_kernel_mode = 0;
 
 // Cost model of a flat launch: every block is w waves of one tile each and stays resident until its slowest wave
 // ends. The blocks spread evenly over the CUs; a CU runs its share in rounds of as many blocks as fit at once (LDS:
-// `lds` bytes per block of 160 KB; waves: 32), and a round takes about max(its waves, 16) tile times (below 16
-// waves a CU is no longer issue-bound). Returns the busiest CU's sum over rounds, in tile times.
-long long flat_cost(int total, int w, int lds) {
+// `lds` bytes per block of 160 KB; waves: wcu, 32 unless registers allow fewer), and a round takes about
+// max(its waves, 16) tile times (below 16 waves a CU is no longer issue-bound). Returns the busiest CU's sum over
+// rounds, in tile times.
+long long flat_cost(int total, int w, int lds, int wcu = 32) {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
@@ -433,7 +434,7 @@ long long flat_cost(int total, int w, int lds) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
       cus = 256;
   }
-  const long long per_cu = std::max(1, std::min(160 * 1024 / lds, 32 / w));
+  const long long per_cu = std::max(1, std::min(160 * 1024 / lds, wcu / w));
   const long long blocks = (total + w - 1) / w, b = (blocks + cus - 1) / cus;
   const long long full = b / per_cu, rest = b % per_cu;
   return full * std::max<long long>(per_cu * w, 16) + (rest ? std::max<long long>(rest * w, 16) : 0);
@@ -446,12 +447,12 @@ int flat_lds(int w, int rs, int extra) { return (w > 1 ? 2 : 1) * 8192 + w * 2 *
 // W) within the kernel's limits: 16 waves per block and W <= the smallest matrix's tile count (a block holds at most
 // two tables). Config 2's 6656 tiles on 256 CUs give W = 13: 512 blocks, one round of 26 waves on every CU (W = 16
 // leaves 96 CUs with one block of 16 waves and 160 with two).
-int flat_width(int total, int rs, int mintiles, int spare_bytes) {
-  const int wmax = std::min(rs == 16 ? 16 : 8, mintiles);
+int flat_width(int total, int rs, int mintiles, int spare_bytes, int wcu = 32) {
+  const int wmax = std::min(std::min(rs == 16 ? 16 : 8, mintiles), std::max(1, wcu));
   int best = 1;
   long long best_cost = -1;
   for (int w = 1; w <= wmax; ++w) {
-    const long long cost = flat_cost(total, w, flat_lds(w, rs, spare_bytes));
+    const long long cost = flat_cost(total, w, flat_lds(w, rs, spare_bytes), wcu);
     if (best_cost < 0 || cost <= best_cost) {
       best_cost = cost;
       best = w;
@@ -463,7 +464,7 @@ int flat_width(int total, int rs, int mintiles, int spare_bytes) {
 // Both kernels in units of one dependent symbol-pair step (about 630 cycles at full load). The ring kernel's waves
 // run 128 pairs per tile; the low-latency kernel's blocks (4 waves, one tile, whole tile staged in LDS) run 32 pairs
 // after staging (counted as 8 more) and a combine step.
-long long ring_cost(int total, int w, int lds) { return flat_cost(total, w, lds) * 128; }
+long long ring_cost(int total, int w, int lds, int wcu = 32) { return flat_cost(total, w, lds, wcu) * 128; }
 long long split_cost(int total, int stage_rows, int kqt) {
   static int cus = 0;
   if (!cus) {
@@ -490,16 +491,16 @@ struct X8 {
   const float* s;
 };
 
-// Quantize the m = 1 activation vector of each of `count` matrices (fp16 or fp32; a vector shared by several
-// matrices once) into the model's x8 scratch; x8[i] = matrix i's quantized x.
+// Quantize the activations of each of `count` matrices (m tokens [m][K_i], fp16 or fp32; a vector shared by several
+// matrices once) into the model's x8 scratch; x8[i] = matrix i's quantized x ([m][K_i] int8, [m][K_i / 32] scales).
 int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, std::vector<X8>& x8,
-                 hipStream_t s) {
+                 hipStream_t s, int m = 1) {
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   std::vector<size_t> off(count);
   std::map<const void*, int> first;
   size_t total = 0;
   for (int i = 0; i < count; ++i) {
-    const size_t K = (size_t)ts[i]->K;
+    const size_t K = (size_t)ts[i]->K * m;
     auto it = first.find(X[i]);
     if (it != first.end() && ts[it->second]->K == ts[i]->K) {
       off[i] = off[it->second];
@@ -515,7 +516,7 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
   q.x_f16 = x_f16;
   int blocks = 0;
   for (int i = 0; i < count; ++i) {
-    const size_t K = (size_t)ts[i]->K;
+    const size_t K = (size_t)ts[i]->K * m;
     uint8_t* b = M.x8 + off[i];
     x8[i] = X8{reinterpret_cast<const int8_t*>(b), reinterpret_cast<const float*>(b + al(K)),
                reinterpret_cast<const float*>(b + al(K) + al(K / 32 * 4))};
@@ -566,8 +567,8 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
 // others into whole-tile launches. The ordered reduction over tile columns runs inside the flat (m = 1) launch for
 // every matrix that launch decodes completely, else in one reduction launch per MAX_GROUP matrices. Partials of
 // all matrices live side by side in the model's P scratch; calls that overlap on one model race (P and counters).
-// `launches` (optional) counts the kernel launches. x8 (m = 1, flat kernels only): int8 activations (quant_x8_dev)
-// instead of X16.
+// `launches` (optional) counts the kernel launches. x8 (flat kernels only; m = 1, or up to 8 tokens in one pass with
+// kernel modes 0, 3-5 and no packed matrix): int8 activations (quant_x8_dev) instead of X16.
 int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
                     const int* ldy, hipStream_t s, int* launches = nullptr, const X8* x8 = nullptr) {
   const int mt = m * per;
@@ -588,17 +589,29 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     return 0;
   };
   const bool ring_ok = g_kernel_mode != 1;
-  const bool flat = ring_ok && mt == 1 && g_kernel_mode != 2;
+  const bool flat = ring_ok && g_kernel_mode != 2 && (mt == 1 || (x8 && mt <= 8 && g_kernel_mode != 6));
   if (x8 && !flat) {
-    g_err = "int8 activations: m = 1 and a flat kernel mode (0, 3, 4 or 5) only";
+    g_err = "int8 activations: a flat kernel mode (0, 3, 4, 5, or 6 for m = 1) and at most 8 tokens only";
     return -1;
   }
+  for (int i = 0; x8 && mt > 1 && i < count; ++i)
+    if (ts[i]->dm.packed) {
+      g_err = "int8 activations: packed matrices take one token per pass";
+      return -1;
+    }
   auto set8 = [&](lw::FlatPlan& fp, lw::FlatEntry& e, int j) {
     if (!x8) return;
     fp.i8 = 1;
+    fp.mt = mt;
     e.XQ = x8[j].q;
     e.DX = x8[j].d;
     e.SX = x8[j].s;
+    e.ldy = ldy[j];
+  };
+  // waves per CU of the flat kernel: fewer than 32 when the several-token kernel's registers allow fewer
+  auto waves_cu = [&](const lw::DevMat& dm) {
+    const int w = x8 && mt > 1 ? lw::flat_waves_per_cu(dm.kqt, dm.ring_rows, mt) : 32;
+    return w > 0 ? w : 32;
   };
   // m = 1 (fp16 x): one flat launch (balanced blocks) per (K-quant type, ring size) and batch of MAX_GROUP
   // matrices, whatever their order: the ring kernel, or the low-latency kernel when the cost model favours it (few
@@ -690,9 +703,11 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       }
     }
     bool split = !di.ring_rows || g_kernel_mode == 4;
+    const int wcu = di.ring_rows ? waves_cu(di) : 32;
     if (!split && g_kernel_mode != 5) {
-      const int w = flat_width(total, di.ring_rows, mintiles, 0);
-      split = split_cost(total, lw::split_stage_rows(fp), di.kqt) < ring_cost(total, w, flat_lds(w, di.ring_rows, 0));
+      const int w = flat_width(total, di.ring_rows, mintiles, 0, wcu);
+      split = split_cost(total, lw::split_stage_rows(fp), di.kqt) <
+              ring_cost(total, w, flat_lds(w, di.ring_rows, 0), wcu);
     }
     if (split) {  // every tile of these matrices, exceptions included; the reduction in the launch
       for (int k = 0; k < fp.n; ++k) {
@@ -704,7 +719,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       continue;
     }
     const int spare_ring = 2 * 16 * 128;
-    fp.W = flat_width(total, di.ring_rows, mintiles, nx && di.ring_rows == 16 ? spare_ring : 0);
+    fp.W = flat_width(total, di.ring_rows, mintiles, nx && di.ring_rows == 16 ? spare_ring : 0, wcu);
     if (nx && di.ring_rows == 16 && g_kernel_mode != 3) {
       // spare rings per block = the most 32-row exception tiles in one block (tile list position / W)
       std::map<int, int> per_block;
@@ -717,8 +732,8 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         }
       }
       // in place when the spare rings cost no more than the one spare ring the width was chosen with
-      if (fp.W + most <= 32 && flat_cost(total, fp.W, flat_lds(fp.W, 16, most * spare_ring)) <=
-                                   flat_cost(total, fp.W, flat_lds(fp.W, 16, spare_ring))) {
+      if (fp.W + most <= 32 && flat_cost(total, fp.W, flat_lds(fp.W, 16, most * spare_ring), wcu) <=
+                                   flat_cost(total, fp.W, flat_lds(fp.W, 16, spare_ring), wcu)) {
         fp.nspare = most;
         for (int j : sel) exc_in[j] = 1;
       }
@@ -853,14 +868,22 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
 
 // lw_group_matmul_dev's work (fp16 x [m][K_i] per matrix): the fused path, after the quantization launch when int8
 // activations are on (m = 1)
-// Int8-activation matmuls of `count` matrices for m tokens (x [m][K_i], fp16 or fp32, rows K_i apart; y rows ldy
-// apart): one quantization launch and one m = 1 fused pass per token, so every token gets the bits of an m = 1 call
-// (the reference's int8 kernel covers m <= 8 in one pass over the weights; here the weights are read once per token).
+// Int8-activation matmuls of `count` matrices for m <= 8 tokens (x [m][K_i], fp16 or fp32, rows K_i apart; y rows
+// ldy apart): one quantization launch, then one fused pass over the weights for all tokens (the reference's MT-token
+// int8 kernel, kernels/llmrt.cu:1057-1169), which gives every token the bits of an m = 1 call. Packed matrices and
+// kernel mode 6 take one m = 1 pass per token.
 int act8_tokens(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, int m, float* const* Y,
                 const int* ldy, hipStream_t s, int* launches) {
+  std::vector<X8> x8;
+  bool one = m > 1 && g_kernel_mode != 6;
+  for (int i = 0; i < count; ++i) one = one && !ts[i]->dm.packed;
+  if (one || m == 1) {
+    if (quant_x8_dev(M, ts, X, x_f16, count, x8, s, m)) return -1;
+    if (launches) ++*launches;
+    return fused_group_dev(M, ts, X, count, m, 1, Y, ldy, s, launches, x8.data());
+  }
   std::vector<const void*> xj(count);
   std::vector<float*> yj(count);
-  std::vector<X8> x8;
   for (int j = 0; j < m; ++j) {
     for (int i = 0; i < count; ++i) {
       xj[i] = static_cast<const char*>(X[i]) + (size_t)j * ts[i]->K * (x_f16 ? 2 : 4);

@@ -1,10 +1,11 @@
 """GPU parity of the int8-activation path (lw_set_act8) through the C-ABI, against the oracle.
 
 The reference's act8 kernels (kernels/llmrt.cu:1035-1169) quantize x per block of 32 and take integer dot products
-per sub-block. Bars: the quantization (q, d, d sum q) bit-exact against oracle.quant_x8, for fp32 and fp16 x; the
-GEMV within 2e-5 of max |y| of oracle.gemv_act8_f64 (the fp64 value of the same integer sums and scales: only the
-fp32 scale products and the accumulation over sub-blocks round); coded, packed, ring and low-latency kernels the
-same bits. Against the fp64 product with the unquantized x the int8 result carries the quantization error (about
+per sub-block, for up to 8 tokens in one pass over the weights. Bars: the quantization (q, d, d sum q) bit-exact
+against oracle.quant_x8, for fp32 and fp16 x; the GEMV within 2e-5 of max |y| of oracle.gemv_act8_f64 (the fp64 value
+of the same integer sums and scales: only the fp32 scale products and the accumulation over sub-blocks round); coded,
+packed, ring and low-latency kernels the same bits; a several-token pass the same bits, token by token, as m = 1
+calls. Against the fp64 product with the unquantized x the int8 result carries the quantization error (about
 0.5 % of max |y| for Gaussian x), asserted below 2e-2 as a sanity bound.
 """
 import ctypes
@@ -94,8 +95,8 @@ def check(y, ref, tol, what):
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_act8_gemv(a8_rt, orc, lib, act8, kqt, fmt, H):
     """rt_test_matmul (fp32 host x) and lw_matmul_dev (fp16 and fp32 device x) at m = 1 against the oracle's int8
-    GEMV; m = 3 (one pass per token): every token against the oracle and equal to its own m = 1 call; m = 12 (beyond
-    the int8 range) keeps fp32 activations on the prefill path (within 2e-5 of fp64)."""
+    GEMV; m = 3 and m = 8 (one pass over the weights): every token against the oracle and equal to its own m = 1
+    call; m = 12 (beyond the int8 range) keeps fp32 activations on the prefill path (within 2e-5 of fp64)."""
     import torch
     rc, rp, mats = a8_rt
     rng = np.random.default_rng(kqt)
@@ -120,23 +121,25 @@ def test_gpu_act8_gemv(a8_rt, orc, lib, act8, kqt, fmt, H):
         check(rp.test_matmul(nm, x), y8, TOL_ACT8, nm + " act8 packed twin")
         y8h, _ = y_act8(orc, mat, x16.float().numpy())
         check(Yh.cpu().numpy(), y8h, TOL_ACT8, nm + " act8 fp16 device")
-        X3 = rng.standard_normal((3, K)).astype(np.float32)
-        y8_3, _ = y_act8(orc, mat, X3)
-        Y3 = rc.test_matmul(nm, X3)
-        check(Y3, y8_3, TOL_ACT8, nm + " act8 m=3")
-        for j in range(3):
-            assert np.array_equal(Y3[j], rc.test_matmul(nm, X3[j:j + 1])[0]), (nm, j)
+        for m in (3, 8):
+            Xm = rng.standard_normal((m, K)).astype(np.float32)
+            y8_m, _ = y_act8(orc, mat, Xm)
+            Ym = rc.test_matmul(nm, Xm)
+            check(Ym, y8_m, TOL_ACT8, nm + " act8 m=%d" % m)
+            for j in range(m):
+                assert np.array_equal(Ym[j], rc.test_matmul(nm, Xm[j:j + 1])[0]), (nm, m, j)
         X12 = rng.standard_normal((12, K)).astype(np.float32)
         _, y64_12 = y_act8(orc, mat, X12)
         check(rc.test_matmul(nm, X12), y64_12, 2e-5, nm + " m=12 stays fp32 (prefill path)")
 
 
-def group(rt, names, xs):
+def group(rt, names, xs, m=1):
+    """lw_group_matmul_dev over `names` with fp16 x [m][K] per matrix; y [m][N] per matrix, as numpy."""
     import torch
-    ys = [torch.zeros(1, rt.info(nm)["N"], device="cuda") for nm in names]
+    ys = [torch.zeros(m, rt.info(nm)["N"], device="cuda") for nm in names]
     n = len(names)
     rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
-                                    (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                    (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), m,
                                     (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
     assert rc == 0, rt.lib.lw_last_error()
     torch.cuda.synchronize()
@@ -168,6 +171,22 @@ def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
         for k in (4, 5, 6, "packed"):
             for a, b in zip(runs[0], runs[k]):
                 assert np.array_equal(a, b), (fmt, k)
+        # m = 5 in one pass (modes 0, 4, 5) or one pass per token (mode 6, packed): every token the bits of its own
+        # m = 1 call
+        x5 = [torch.randn(5, mats[nm][3]).half().cuda() for nm in names]
+        ones = [group(rc, names, [x[j:j + 1].contiguous() for x in x5]) for j in range(5)]
+        say("act8 m=5 grouped", fmt)
+        for mode in (0, 4, 5, 6):
+            assert lib.lw_set_kernel_mode(mode) == 0
+            y5 = group(rc, names, x5, 5)
+            for i in range(len(names)):
+                for j in range(5):
+                    assert np.array_equal(y5[i][j], ones[j][i][0]), (fmt, mode, i, j)
+        lib.lw_set_kernel_mode(0)
+        y5 = group(rp, names, x5, 5)
+        for i in range(len(names)):
+            for j in range(5):
+                assert np.array_equal(y5[i][j], ones[j][i][0]), (fmt, "packed", i, j)
 
 
 def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
@@ -195,6 +214,17 @@ def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
                 assert np.array_equal(runs[0], runs[mode]), (nm, mode)
             q, d, s = orc.quant_x8(x.float().cpu().numpy())
             check(runs[0], orc.gemv_act8_f64(2, codes, side, q, d, s), TOL_ACT8, nm + " act8")
+            # 4 tokens in one pass (modes 0, 3-5; mode 6 one pass per token): the bits of m = 1 calls
+            x4 = torch.randn(4, 8192).half().cuda()
+            ones = [group(rt, [nm], [x4[j:j + 1].contiguous()])[0][0] for j in range(4)]
+            for mode in (0, 3, 4, 5, 6):
+                assert lib.lw_set_kernel_mode(mode) == 0
+                y4 = group(rt, [nm], [x4], 4)[0]
+                for j in range(4):
+                    assert np.array_equal(y4[j], ones[j]), (nm, mode, j)
+            lib.lw_set_kernel_mode(0)
+            q, d, s = orc.quant_x8(x4.float().cpu().numpy())
+            check(y4, orc.gemv_act8_f64(2, codes, side, q, d, s), TOL_ACT8, nm + " act8 m=4")
 
 
 def test_gpu_act8_rejects_block_kernel_modes(a8_rt, lib, act8):
