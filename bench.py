@@ -243,30 +243,40 @@ def main():
             log("bench: int8 activations %.3f ms per step (%.1f GB/s coded; kernels %.3f ms per pass, %d launches)"
                 % (ams, act8["GBps_coded"], out8[1], int(out8[2])))
 
-        # prefill shapes (m = 128, fp32 x resident): the decode-to-scratch path with its GEMM on the matrix cores,
-        # over layer 0's seven matrices (a reported figure, not the metric)
+        # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
+        # matrices, with the default GEMM (rocBLAS over fp16 hi + lo weights) and with the hand-written matrix-core
+        # GEMM over the codes (a reported figure, not the metric)
         prefill = None
         if not a.no_prefill:
-            pm = 128
-            XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
-            YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
+            prefill = {"path": "decode to scratch + dequant to fp16 hi + lo weights + two rocBLAS fp16 GEMMs "
+                               "(fp32 accumulation)", "runs": []}
+            for pm in (128, 512):
+                XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
+                YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
 
-            def prefill_layer():
-                for i in range(7):
-                    if lib.lw_matmul_dev(rt.h, names[i], ctypes.c_void_p(XP[i].data_ptr()), 0, pm,
-                                         ctypes.c_void_p(YP[i].data_ptr()), infos[i]["N"], stream) != 0:
-                        raise RuntimeError(lib.lw_last_error().decode())
-            prefill_layer()
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(5):
-                prefill_layer()
-            torch.cuda.synchronize()
-            fms = (time.perf_counter() - t0) * 1e3 / 5
-            flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos[:7])
-            prefill = {"m": pm, "ms_per_layer": round(fms, 3), "TFLOPs": round(flops / (fms * 1e-3) / 1e12, 1),
-                       "path": "decode to scratch + v_mfma_f32_32x32x8f16 GEMM (fp16 hi + lo x)"}
-            log("bench: prefill m=%d: %.3f ms per layer, %.1f TFLOP/s" % (pm, fms, prefill["TFLOPs"]))
+                def prefill_layer():
+                    for i in range(7):
+                        if lib.lw_matmul_dev(rt.h, names[i], ctypes.c_void_p(XP[i].data_ptr()), 0, pm,
+                                             ctypes.c_void_p(YP[i].data_ptr()), infos[i]["N"], stream) != 0:
+                            raise RuntimeError(lib.lw_last_error().decode())
+                flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos[:7])
+                run = {"m": pm}
+                for which, key in ((0, "rocblas"), (1, "own_mfma")):
+                    if which == 1 and pm > 128:
+                        continue
+                    lib.lw_set_prefill_gemm(which)
+                    prefill_layer()
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    for _ in range(5):
+                        prefill_layer()
+                    torch.cuda.synchronize()
+                    fms = (time.perf_counter() - t0) * 1e3 / 5
+                    run[key] = {"ms_per_layer": round(fms, 3), "TFLOPs": round(flops / (fms * 1e-3) / 1e12, 1)}
+                    log("bench: prefill m=%d (%s): %.3f ms per layer, %.1f TFLOP/s" % (pm, key, fms, run[key]["TFLOPs"]))
+                lib.lw_set_prefill_gemm(0)
+                prefill["runs"].append(run)
+                del XP, YP
 
         # packed-twin control: the same codes stored fixed-rate (pk4 / pk8), no decode chain; the achievable rate of
         # this access pattern and arithmetic without entropy decoding (the reference's pk4 baseline)

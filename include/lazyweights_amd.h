@@ -96,13 +96,20 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * exception tiles) for every m = 1 launch. Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
+/* The GEMM of the decode-to-scratch path (path 2: m > 8, or rt_test_matmul path 2), for all handles. The
+ * reference dequantizes to fp32 and runs its own fp32 GEMM (kernels/llmrt.cu:201-343, 1826-1841). 0 (default) =
+ * the decoded weights w = s f(q) - o split into fp16 hi + lo, x likewise, two rocBLAS fp16 GEMMs with fp32
+ * accumulation (x_hi w_hi + x_hi w_lo, then + x_lo w_hi); 1 = the hand-written matrix-core GEMM over the codes and
+ * side bytes (fp16 hi + lo x). Kernel mode 1 overrides both with the SIMT GEMM. Returns 0 or -1. */
+int lw_set_prefill_gemm(int which);
+
 /* Int8 activations for 1 <= m <= 8 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev
  * and lw_group_matmul_dev quantize x per block of 32 (d = max|x| / 127, q = x / d rounded to nearest even, plus
  * d sum q) and the fused kernels take integer dot products per sub-block, y += s d acc - o d sum q. Replaces the
  * reference's act8 switch (kernels/llmrt.cu:2221, LLMRT_FP_ACT; kernels k_quant_x8 / k_gemvm_kq8 at
- * kernels/llmrt.cu:1035-1169), which is on by default there. Here m > 1 runs one m = 1 pass per token (the same bits
- * per token as an m = 1 call; the weights are read once per token). Needs kernel mode 0, 3, 4, 5 or 6 (the flat
- * kernels). Returns 0 or -1. */
+ * kernels/llmrt.cu:1035-1169), which is on by default there. m > 1 runs one pass over the weights for all tokens
+ * (the same bits per token as an m = 1 call); with kernel mode 6 or a packed matrix, one m = 1 pass per token. Needs
+ * kernel mode 0, 3, 4, 5 or 6 (the flat kernels). Returns 0 or -1. */
 int lw_set_act8(int on);
 
 /* The int8 quantization of lw_set_act8 on host buffers (test entry, runs the device kernel): X [m, K] fp32 or fp16

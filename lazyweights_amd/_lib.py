@@ -42,6 +42,7 @@ SIGNATURES = {
     "lw_huffman_lengths": (_i, [_vp, _i, _i, _vp]),
     "lw_build_layout": (_ll, [_vp, _ll, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll]),
     "lw_set_kernel_mode": (_i, [_i]),
+    "lw_set_prefill_gemm": (_i, [_i]),
     "lw_set_act8": (_i, [_i]),
     "lw_test_quant_x8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
 }

@@ -4,7 +4,7 @@
 
 Device code: hipcc --offload-arch=gfx950, with packed-fp32 instruction selection disabled. Pure host C++ (codec,
 layout, bundle writer) is compiled with g++; everything is linked into one shared library exposing the C-ABI of
-include/lazyweights_amd.h.
+include/lazyweights_amd.h (with rocBLAS for the prefill GEMMs).
 """
 import os
 import shutil
@@ -20,6 +20,7 @@ LIB = os.path.join(PKG, "liblazyweights_amd.so")
 ARCH = os.environ.get("LW_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+ROCM_LIB = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
 CXX = shutil.which("g++") or "g++"
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", CSRC, "-I", os.path.join(ROOT, "include")]
 HIP_DEVICE = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -60,7 +61,8 @@ def build(verbose=False):
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(lambda s: _compile(*s), SOURCES))
     tmp = LIB + ".tmp"
-    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs + ["-pthread", "-lm"])
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs +
+         ["-L" + ROCM_LIB, "-lrocblas", "-pthread", "-lm"])
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)

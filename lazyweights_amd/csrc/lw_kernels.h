@@ -153,6 +153,15 @@ hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStr
 hipError_t launch_gemm_codes(const DevMat& M, const uint8_t* codes, int row0, int nrows, const float* X, int m,
                              float* Y, int ldy, hipStream_t s);
 // the same on the matrix cores, with X16 = fp16 hi / lo rows [2m][K] (launch_split_x), rows [row0, row0 + nrows)
+// Prefill through a library GEMM: codes rows [row0, row0 + nrows) (from launch_decode, [nrows][K]) -> WW, the
+// column-major [nrows x 2K] fp16 matrix of w = s f(q) - o (fp32, as the reference's kq_w4): hi of weight k of row r
+// at WW[k nrows + r], lo at WW[(K + k) nrows + r]
+hipError_t launch_dequant_hilo(const DevMat& M, const uint8_t* codes, int row0, int nrows, void* WW, hipStream_t s);
+// The same from the coded matrix directly (decode + dequant in one kernel; coded K-quant matrices with split
+// offsets): tile rows [tr0, tr1) -> WW rows relative to tr0 * 64
+hipError_t launch_decode_hilo(const DevMat& M, int tr0, int tr1, void* WW, hipStream_t s);
+// x [m][K] fp32 -> XX [m][2K] fp16 = [hi | hi], XL [m][K] fp16 = lo
+hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K, hipStream_t s);
 hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row0, int nrows, const void* X16, int m,
                                   float* Y, int ldy, hipStream_t s);
 // streaming read of n16 16-byte words (achievable HBM bandwidth control); out gets one value per block

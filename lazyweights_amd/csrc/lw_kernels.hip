@@ -2388,6 +2388,198 @@ hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row
   return hipGetLastError();
 }
 
+// ── prefill through a library GEMM: decoded codes -> fp16 hi + lo weights (path 2, the default for m > 8) ────
+// The reference's prefill dequantizes every weight to fp32, w = s f(q) - o (kernels/llmrt.cu:201-343, kq_w4), and runs
+// a fp32 GEMM. Here w (the same fp32 value: product, then difference, no contraction) is split into fp16 hi = fp16(w)
+// and lo = fp16(w - hi), stored per row as [hi x K | lo x K], and x likewise ([x hi | x hi] and [x lo]), so two fp16
+// GEMMs with fp32 accumulation give x_hi w_hi + x_hi w_lo + x_lo w_hi: w and x to about 22 bits.
+// WW is column-major for the GEMM (row n of the chunk, weight k): hi at WW[k nrows + n], lo at WW[(K + k) nrows + n],
+// so the 64 rows of a tile store one weight as one 128-byte line.
+// One thread = one sub-block of GW weights of one row; consecutive threads take consecutive rows.
+template <int KQ>
+__global__ void __launch_bounds__(256) k_dequant_hilo(DevMat M, const uint8_t* __restrict__ codes, int row0,
+                                                      int nrows, uint16_t* __restrict__ WW) {
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ), NSUB = 256 / GW;
+  const int K = M.K, per_row = K / GW;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)nrows * per_row) return;
+  const int g = (int)(i / nrows), r = (int)(i - (size_t)g * nrows), b = g / NSUB, jj = g - b * NSUB;
+  uint32_t sw[5];
+  side_load<KQ>(M.side + side_record(row0 + r, b, M.KT, M.symbits == 4 ? 2 : 1) * SB, sw);
+  float sc, o;
+  side_scale<KQ>(sw, jj, sc, o);
+  const uint8_t* cr = codes + (size_t)r * K + (size_t)g * GW;
+  uint16_t* hc = WW + (size_t)g * GW * nrows + r;
+  const size_t lo_off = (size_t)K * nrows;
+#pragma unroll
+  for (int c = 0; c < GW; c += 4) {
+    const uint32_t q4 = *reinterpret_cast<const uint32_t*>(cr + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t q = (q4 >> (8 * e)) & 255u;
+      const float f = KQ == KQ_Q6_K ? (float)q - 32.f : (KQ == KQ_IQ4_XS ? (float)IQ4_GRID[q & 15u] : (float)q);
+      const float w = __fsub_rn(__fmul_rn(sc, f), o);
+      const _Float16 hi = (_Float16)w;
+      const _Float16 lo = (_Float16)(w - (float)hi);
+      hc[(size_t)(c + e) * nrows] = __builtin_bit_cast(uint16_t, hi);
+      hc[lo_off + (size_t)(c + e) * nrows] = __builtin_bit_cast(uint16_t, lo);
+    }
+  }
+}
+
+hipError_t launch_dequant_hilo(const DevMat& M, const uint8_t* codes, int row0, int nrows, void* WW, hipStream_t s) {
+  if (nrows < 1 || M.K % 256) return hipErrorInvalidValue;
+  const size_t n = (size_t)nrows * (M.K / kq_gw(M.kqt));
+  const dim3 grid((unsigned)((n + 255) / 256));
+  uint16_t* w = static_cast<uint16_t*>(WW);
+  switch (M.kqt) {
+    case KQ_Q4_K: hipLaunchKernelGGL(k_dequant_hilo<KQ_Q4_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, w); break;
+    case KQ_Q5_K: hipLaunchKernelGGL(k_dequant_hilo<KQ_Q5_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, w); break;
+    case KQ_Q6_K: hipLaunchKernelGGL(k_dequant_hilo<KQ_Q6_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, w); break;
+    case KQ_IQ4_XS: hipLaunchKernelGGL(k_dequant_hilo<KQ_IQ4_XS>, grid, dim3(256), 0, s, M, codes, row0, nrows, w); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Decode + dequant in one kernel for the prefill GEMM: tile rows [tr0, tr1) of a coded K-quant matrix straight to
+// WW (column-major hi then lo, as k_dequant_hilo). One block of 4 waves per tile, the tile and its decode table
+// staged in LDS, 8 chains per lane over the load-time split offsets (as k_fused_split): wave w decodes symbols
+// [64 w, 64 w + 64) of row l (lanes 0-31) and row l + 32 (lanes 32-63) and stores each weight as it comes, one
+// 128-byte line per wave and weight (the tile's 64 rows).
+template <int KQ>
+__global__ void __launch_bounds__(256) k_decode_hilo(DevMat M, int tr0, int tr1, uint16_t* __restrict__ WW,
+                                                     int stage_rows) {
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ), NSB = TW / 256;
+  constexpr int WPP = SYMB == 4 ? 4 : 2;  // weights per symbol pair
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  __shared__ uint32_t lut4[LUTN];
+  extern __shared__ __align__(16) uint32_t tw[];
+  const int KT = M.KT, K = M.K;
+  const int t = tr0 * KT + (int)blockIdx.x;
+  if (t >= tr1 * KT) return;
+  const int tc = t % KT, tr = t / KT;
+  const int R = min((int)M.rows[t] + 2, stage_rows);
+  for (int i = threadIdx.x; i < LUTN / 4; i += 256)
+    reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
+  const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
+  for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  const int k = 4 * f + wave;
+  uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k * (SPLITS / 8)) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+  const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
+  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
+  uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
+  uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
+  uint32_t C = *(LdsU32*)(rlb + (slot << 7));
+  const int n = tr * TN + f * 32 + l;          // matrix row
+  const int col0 = tc * TW + wave * (TW / 4);  // the chain's first weight: 64 symbols = a quarter of the tile row
+  const int b = col0 / 256;                    // the chain's super-block (a quarter never spans two)
+  uint32_t sw[5];
+  side_load<KQ>(M.side + side_record(n, b, KT, NSB) * SB, sw);
+  const int nrows = (tr1 - tr0) * TN;
+  uint16_t* hc = WW + (size_t)col0 * nrows + (n - tr0 * TN);
+  const size_t lo_off = (size_t)K * nrows;
+#pragma unroll 1
+  for (int gi = 0; gi < 4; ++gi) {
+    // the group's 16 symbols = 32 (4-bit) or 16 weights: one sub-block scale (Q5_K: half a sub-block)
+    const int jj = ((col0 - 256 * b) + gi * 8 * WPP) / GW;
+    float sc, o;
+    side_scale<KQ>(sw, jj, sc, o);
+#pragma unroll
+    for (int p2 = 0; p2 < 8; p2 += 2) {
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
+        const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
+        const uint32_t w2 = w1 >> (e1 & 31u);
+        const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
+        P = P + e1 + e2;
+        const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, 8);
+        const bool slide = nslot != slot;
+        A = slide ? B : A;
+        B = slide ? C : B;
+        slot = nslot;
+        C = *(LdsU32*)(rlb + (nslot << 7));
+        float fv[WPP];
+        if (SYMB == 4) {  // entry bytes 2, 3: the symbol's two grid bytes (IQ4_XS: kv[q] + 128)
+          const float bias = KQ == KQ_IQ4_XS ? 128.f : 0.f;
+          fv[0] = (float)((e1 >> 16) & 255u) - bias;
+          fv[1] = (float)(e1 >> 24) - bias;
+          fv[2] = (float)((e2 >> 16) & 255u) - bias;
+          fv[3] = (float)(e2 >> 24) - bias;
+        } else {  // bits 16-31: fp16 f(q)
+          fv[0] = h2f(e1 >> 16);
+          fv[1] = h2f(e2 >> 16);
+        }
+        const int c = (gi * 8 + p2 + pp) * WPP;  // the pair's first weight within the chain
+#pragma unroll
+        for (int e = 0; e < WPP; ++e) {
+          const float w = __fsub_rn(__fmul_rn(sc, fv[e]), o);
+          const _Float16 hi = (_Float16)w;
+          const _Float16 lo = (_Float16)(w - (float)hi);
+          hc[(size_t)(c + e) * nrows] = __builtin_bit_cast(uint16_t, hi);
+          hc[lo_off + (size_t)(c + e) * nrows] = __builtin_bit_cast(uint16_t, lo);
+        }
+      }
+    }
+  }
+}
+
+hipError_t launch_decode_hilo(const DevMat& M, int tr0, int tr1, void* WW, hipStream_t s) {
+  if (M.packed || !M.split || !M.lut4 || !M.rows || tr0 < 0 || tr1 > M.NT || tr0 >= tr1 || M.K % 256)
+    return hipErrorInvalidValue;
+  const int rows = M.max_rows + 2;
+  const size_t smem = (size_t)rows * 128;
+  if (rows > 256 || smem + 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
+  uint16_t* w = static_cast<uint16_t*>(WW);
+  const void* f = nullptr;
+  switch (M.kqt) {
+    case KQ_Q4_K: f = reinterpret_cast<const void*>(&k_decode_hilo<KQ_Q4_K>); break;
+    case KQ_Q5_K: f = reinterpret_cast<const void*>(&k_decode_hilo<KQ_Q5_K>); break;
+    case KQ_Q6_K: f = reinterpret_cast<const void*>(&k_decode_hilo<KQ_Q6_K>); break;
+    case KQ_IQ4_XS: f = reinterpret_cast<const void*>(&k_decode_hilo<KQ_IQ4_XS>); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  switch (M.kqt) {
+    case KQ_Q4_K: hipLaunchKernelGGL(k_decode_hilo<KQ_Q4_K>, grid, dim3(256), smem, s, M, tr0, tr1, w, rows); break;
+    case KQ_Q5_K: hipLaunchKernelGGL(k_decode_hilo<KQ_Q5_K>, grid, dim3(256), smem, s, M, tr0, tr1, w, rows); break;
+    case KQ_Q6_K: hipLaunchKernelGGL(k_decode_hilo<KQ_Q6_K>, grid, dim3(256), smem, s, M, tr0, tr1, w, rows); break;
+    default: hipLaunchKernelGGL(k_decode_hilo<KQ_IQ4_XS>, grid, dim3(256), smem, s, M, tr0, tr1, w, rows); break;
+  }
+  return hipGetLastError();
+}
+
+// x [m][K] fp32 -> XX [m][2K] = [hi | hi] and XL [m][K] = lo (fp16)
+__global__ void k_split_x_gemm(const float* __restrict__ X, uint16_t* __restrict__ XX, uint16_t* __restrict__ XL,
+                               int m, int K) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)m * K) return;
+  const size_t j = i / K, k = i - j * K;
+  const float x = X[i];
+  const _Float16 hi = (_Float16)x;
+  const _Float16 lo = (_Float16)(x - (float)hi);
+  XX[j * 2 * K + k] = XX[j * 2 * K + K + k] = __builtin_bit_cast(uint16_t, hi);
+  XL[i] = __builtin_bit_cast(uint16_t, lo);
+}
+
+hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K, hipStream_t s) {
+  const size_t n = (size_t)m * K;
+  hipLaunchKernelGGL(k_split_x_gemm, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, X,
+                     static_cast<uint16_t*>(XX), static_cast<uint16_t*>(XL), m, K);
+  return hipGetLastError();
+}
+
 // ── HBM streaming-read control ──────────────────────────────────────────────────────────────────────────
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256) k_stream_read(const u32x4* __restrict__ src, size_t n16, float* __restrict__ out) {

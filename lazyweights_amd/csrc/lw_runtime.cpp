@@ -7,6 +7,7 @@
 // (lw_kernels.h), and there is no model runtime or weight streaming.
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -121,6 +122,9 @@ struct Model {
   size_t x8_cap = 0;
   uint8_t* codes = nullptr;
   size_t codes_cap = 0;
+  uint16_t* W16 = nullptr;  // prefill: fp16 [hi | lo] weights of a chunk of rows
+  size_t W16_cap = 0;
+  rocblas_handle blas = nullptr;  // prefill GEMMs, created on first use
   int verbose = 0;
   Tensor* find(const char* name) {
     if (!name) return nullptr;
@@ -393,6 +397,8 @@ void release(Model* M) {
   if (M->X16) (void)hipFree(M->X16);
   if (M->x8) (void)hipFree(M->x8);
   if (M->codes) (void)hipFree(M->codes);
+  if (M->W16) (void)hipFree(M->W16);
+  if (M->blas) (void)rocblas_destroy_handle(M->blas);
   if (M->stream) (void)hipStreamDestroy(M->stream);
   if (M->fd >= 0) close(M->fd);
   delete M;
@@ -907,13 +913,70 @@ int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, in
   return fused_group_dev(M, &tp, &X16, 1, m, per, &Y, &ldy, s);
 }
 
+// Prefill GEMM of path 2: 0 (default) = decoded codes dequantized to fp16 hi + lo weights and two rocBLAS GEMMs;
+// 1 = the hand-written MFMA GEMM over the codes (k_gemm_codes_mfma). Kernel mode 1 keeps the SIMT GEMM.
+int g_prefill = 0;
+
+// Y[:, r0 : r0 + nr] = x . w^T for a chunk of rows through rocBLAS. WW is the column-major nr x 2K matrix [w hi |
+// w lo] (ld nr), XX [m][2K] = [x hi | x hi] and XL [m][K] = x lo are the column-major 2K x m and K x m matrices of
+// their transposes. Column-major view: Y^T (nr x m, ld ldy) = WW . XX over K' = 2K (x_hi w_hi + x_hi w_lo), then
+// += WW[:, :K] . XL (x_lo w_hi).
+int blas_chunk(Model& M, const uint16_t* WW, const uint16_t* XX, const uint16_t* XL, int nr, int m, int K, float* Y,
+               int ldy) {
+  const float one = 1.f, zero = 0.f;
+  rocblas_status st = rocblas_gemm_ex(M.blas, rocblas_operation_none, rocblas_operation_none, nr, m, 2 * K, &one,
+                                      WW, rocblas_datatype_f16_r, nr, XX, rocblas_datatype_f16_r, 2 * K, &zero, Y,
+                                      rocblas_datatype_f32_r, ldy, Y, rocblas_datatype_f32_r, ldy,
+                                      rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st == rocblas_status_success)
+    st = rocblas_gemm_ex(M.blas, rocblas_operation_none, rocblas_operation_none, nr, m, K, &one, WW,
+                         rocblas_datatype_f16_r, nr, XL, rocblas_datatype_f16_r, K, &one, Y, rocblas_datatype_f32_r,
+                         ldy, Y, rocblas_datatype_f32_r, ldy, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success) {
+    g_err = std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st);
+    return -1;
+  }
+  return 0;
+}
+
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
-// (the GEMM on the matrix cores over fp16 hi + lo activations; kernel mode 1 keeps the SIMT GEMM)
 int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
+  const bool blas = g_kernel_mode != 1 && g_prefill == 0;
+  const bool mfma = g_kernel_mode != 1 && !blas;
+  if (blas) {
+    if (!M.blas && rocblas_create_handle(&M.blas) != rocblas_status_success) {
+      M.blas = nullptr;
+      g_err = "rocblas_create_handle failed";
+      return -1;
+    }
+    if (rocblas_set_stream(M.blas, s) != rocblas_status_success) {
+      g_err = "rocblas_set_stream failed";
+      return -1;
+    }
+    // fp16 x: [m][2K] hi | hi, then [m][K] lo; weights [rows][2K] fp16 per chunk of tile rows (at most 256 MB)
+    const size_t ww_row = (size_t)lw::TN * t.K * 4;
+    const size_t cap = std::max(ww_row, std::min<size_t>((size_t)t.N * t.K * 4, (size_t)256 << 20));
+    if (grow(M.X16, M.X16_cap, (size_t)3 * m * t.K * 2) || grow(M.W16, M.W16_cap, cap)) return -1;
+    HIPCHECK(lw::launch_split_x_gemm(X, M.X16, M.X16 + (size_t)2 * m * t.K, m, (int)t.K, s));
+    const int rows_fit = (int)std::max<size_t>(1, M.W16_cap / ww_row);
+    const bool fused = !t.dm.packed && t.dm.split;  // decode + dequant in one kernel
+    if (!fused && grow(M.codes, M.codes_cap, (size_t)rows_fit * lw::TN * t.K)) return -1;
+    for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit) {
+      const int tr1 = std::min(t.dm.NT, tr0 + rows_fit), nr = (tr1 - tr0) * lw::TN;
+      if (fused) {
+        HIPCHECK(lw::launch_decode_hilo(t.dm, tr0, tr1, M.W16, s));
+      } else {
+        HIPCHECK(lw::launch_decode(t.dm, M.codes, tr0, tr1, s));
+        HIPCHECK(lw::launch_dequant_hilo(t.dm, M.codes, tr0 * lw::TN, nr, M.W16, s));
+      }
+      if (blas_chunk(M, M.W16, M.X16, M.X16 + (size_t)2 * m * t.K, nr, m, (int)t.K, Y + (size_t)tr0 * lw::TN, ldy))
+        return -1;
+    }
+    return 0;
+  }
   const size_t row_bytes = (size_t)lw::TN * t.K;
   const size_t cap = std::max(row_bytes, std::min<size_t>((size_t)t.N * t.K, (size_t)64 << 20));
   if (grow(M.codes, M.codes_cap, cap)) return -1;
-  const bool mfma = g_kernel_mode != 1;
   if (mfma) {
     if (grow(M.X16, M.X16_cap, (size_t)2 * m * t.K * 2)) return -1;
     HIPCHECK(lw::launch_split_x(X, M.X16, m, (int)t.K, s));
@@ -1314,6 +1377,12 @@ int lw_set_act8(int on) {
 int lw_set_kernel_mode(int mode) {
   if (mode < 0 || mode > 6) return -1;
   g_kernel_mode = mode;
+  return 0;
+}
+
+int lw_set_prefill_gemm(int which) {
+  if (which != 0 && which != 1) return -1;
+  g_prefill = which;
   return 0;
 }
 

@@ -122,22 +122,42 @@ def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
-    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) on the matrix cores against fp64, and
-    against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
+    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) through both prefill GEMMs (rocBLAS over
+    fp16 hi + lo weights, the default; the hand-written matrix-core GEMM over the codes) against fp64, and against
+    the SIMT GEMM (kernel mode 1) to fp32 rounding."""
     rt, mats = fmt_rt
     mat = mats[fmt]
     rng = np.random.default_rng(30 + kqt)
     X = rng.uniform(-1, 1, (80, mat[3])).astype(np.float32)
     _, y64 = reference_y(orc, mat, X.astype(np.float64))
-    say("prefill m=80", fmt)
-    Y = rt.test_matmul(fmt, X, path=2)
-    check_err(Y, y64, fmt + " prefill m=80")
     assert rt.lib.lw_set_kernel_mode(1) == 0
     try:
         Ys = rt.test_matmul(fmt, X, path=2)
     finally:
         rt.lib.lw_set_kernel_mode(0)
-    assert np.abs(Y - Ys).max() <= 1e-5 * np.abs(Ys).max()
+    for which, what in ((0, "rocBLAS hi + lo"), (1, "matrix-core codes GEMM")):
+        say("prefill m=80", fmt, what)
+        assert rt.lib.lw_set_prefill_gemm(which) == 0
+        try:
+            Y = rt.test_matmul(fmt, X, path=2)
+        finally:
+            rt.lib.lw_set_prefill_gemm(0)
+        check_err(Y, y64, "%s prefill m=80 (%s)" % (fmt, what))
+        assert np.abs(Y - Ys).max() <= 1e-5 * np.abs(Ys).max()
+
+
+def test_gpu_prefill_gemm_row_chunks(gpu, tmp_path, orc, lib):
+    """A matrix whose codes exceed the 64 MB decode scratch (17408 x 4096 Q4_K: two row chunks), m = 9 (auto path
+    2), through the rocBLAS prefill GEMM: every chunk lands in its own rows of y."""
+    from lazyweights_amd import Runtime, bundle
+    mat = ("big", 1, 17408, 4096, 2.3, 91)
+    bundle.write_synthetic_bundle(str(tmp_path), [mat], threads=8)
+    rng = np.random.default_rng(91)
+    X = rng.uniform(-1, 1, (9, 4096)).astype(np.float32)
+    _, y64 = reference_y(orc, mat, X.astype(np.float64))
+    with Runtime(tmp_path) as rt:
+        say("prefill row chunks m=9")
+        check_err(rt.test_matmul("big", X), y64, "big m=9 (two row chunks)")
 
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
@@ -459,8 +479,8 @@ def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
 
 def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
     """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices,
-    with a one-tile IQ4_XS matrix so the flat launch runs one-wave blocks that use all 256 table entries), m = 5 and
-    the fp32-x path; its GPU decode returns the codes."""
+    with a one-tile IQ4_XS matrix so the flat launch runs one-wave blocks that use all 256 table entries), m = 5, the
+    fp32-x path and the prefill path; its GPU decode returns the codes."""
     import ctypes
 
     import torch
@@ -498,6 +518,12 @@ def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
             assert np.array_equal(yc, yp), name
             y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X3.astype(np.float64))
             check_err(yp, y64, name + " packed fp32 m=3")
+            # prefill path: the coded matrix's fused decode + dequant and the packed one's unpack + dequant give the
+            # same fp16 hi + lo weights, so the same GEMM bits
+            X12 = np.random.default_rng(kqt + 7).standard_normal((12, K)).astype(np.float32)
+            yc, yp = rc.test_matmul(name, X12, path=2), rp.test_matmul(name, X12, path=2)
+            assert np.array_equal(yc, yp), name
+            check_err(yp, orc.gemv_f64(orc.dequant(kqt, codes, side), X12.astype(np.float64)), name + " prefill m=12")
 
 
 def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
