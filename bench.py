@@ -243,6 +243,42 @@ def main():
             log("bench: int8 activations %.3f ms per step (%.1f GB/s coded; kernels %.3f ms per pass, %d launches)"
                 % (ams, act8["GBps_coded"], out8[1], int(out8[2])))
 
+        # speculative verify (config 4: m = 5 tokens on the same layers, one grouped call per layer): fp16 x and
+        # int8 x (one pass over the weights for all tokens); bytes as m = 1 plus 5x the x and y traffic
+        verify = None
+        if m == 1:
+            vm = 5
+            XV = [torch.randn(vm, inf["K"], generator=g).half().cuda() for inf in infos]
+            YV = [torch.zeros(vm, inf["N"], device="cuda") for inf in infos]
+            vcalls = []
+            for l in range(a.layers):
+                sl = slice(7 * l, 7 * l + 7)
+                vcalls.append(((ctypes.c_char_p * 7)(*names[sl]),
+                               (ctypes.c_void_p * 7)(*[x.data_ptr() for x in XV[sl]]),
+                               (ctypes.c_void_p * 7)(*[y.data_ptr() for y in YV[sl]])))
+            vbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * vm + 4 * vm * inf["N"]
+                               for inf in infos))
+            verify = {"m": vm}
+            for a8, key in ((0, "fp16_x"), (1, "int8_x")):
+                lib.lw_set_act8(a8)
+                try:
+                    def vstep():
+                        for nm, xx, yy in vcalls:
+                            if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, vm, yy, stream) != 0:
+                                raise RuntimeError(lib.lw_last_error().decode())
+                    vstep()
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    for _ in range(a.steps):
+                        vstep()
+                    torch.cuda.synchronize()
+                    vms = (time.perf_counter() - t0) * 1e3 / a.steps
+                finally:
+                    lib.lw_set_act8(0)
+                verify[key] = {"ms_per_step": round(vms, 4), "GBps_coded": round(vbytes / (vms * 1e-3) / 1e9, 1)}
+                log("bench: verify m=%d (%s): %.3f ms per step, %.1f GB/s coded" % (vm, key, vms, verify[key]["GBps_coded"]))
+            del XV, YV
+
         # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
         # matrices, with the default GEMM (rocBLAS over fp16 hi + lo weights) and with the hand-written matrix-core
         # GEMM over the codes (a reported figure, not the metric)
@@ -367,6 +403,7 @@ def main():
             "control_stream_read_GBps": round(ctrl, 1),
             "control_packed_twin": packed,
             "act8": act8,
+            "verify_m5": verify,
             "prefill_path2": prefill,
         }
         print(json.dumps(res), flush=True)
