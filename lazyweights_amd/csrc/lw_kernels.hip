@@ -1189,9 +1189,10 @@ __device__ __forceinline__ void flat_tile(const KEntryRef& E, int t, const uint4
 // Exception tiles (no 16-row schedule) are skipped, except with plan.nspare > 0 in a 16-row launch: then a tile
 // with a 32-row schedule is decoded in place, front 0 in the wave's own two rings (4 KB) and front 1 in spare ring
 // k of the block, k = the number of such tiles before it in the block (the host sizes nspare to the block maximum).
-// MT > 1 (int8 activations only): tokens j < plan.mt in one pass, partials [KT][mt][N].
+// MT > 1 (int8 activations only; 4 for up to 4 tokens, 8 for up to 8): tokens j < plan.mt in one pass, partials
+// [KT][mt][N].
 template <int KQ, int RS, int NTAB, bool I8, int MT = 1>
-__global__ void __launch_bounds__(1024, MT == 1 ? 2 : 1) k_fused_flat(FlatPlan plan) {
+__global__ void __launch_bounds__(1024, MT == 4 ? 7 : (MT == 8 ? 1 : 2)) k_fused_flat(FlatPlan plan) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
   constexpr int GW = kq_gw(KQ);
@@ -1495,7 +1496,8 @@ static hipError_t split_launch_t(const FlatPlan& p, int stage_rows, hipStream_t 
 
 template <int KQ>
 static hipError_t split_launch(const FlatPlan& p, int stage_rows, hipStream_t s) {
-  if (p.mt > 1) return split_launch_t<KQ, true, 8>(p, stage_rows, s);
+  if (p.mt > 4) return split_launch_t<KQ, true, 8>(p, stage_rows, s);
+  if (p.mt > 1) return split_launch_t<KQ, true, 4>(p, stage_rows, s);
   return p.i8 ? split_launch_t<KQ, true>(p, stage_rows, s) : split_launch_t<KQ, false>(p, stage_rows, s);
 }
 
@@ -1928,7 +1930,8 @@ static hipError_t flat_launch_t(const FlatPlan& p, hipStream_t s) {
 // one-wave blocks never span two matrices: one table
 template <int KQ, int RS>
 static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
-  if (p.mt > 1) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true, 8>(p, s) : flat_launch_t<KQ, RS, 2, true, 8>(p, s);
+  if (p.mt > 4) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true, 8>(p, s) : flat_launch_t<KQ, RS, 2, true, 8>(p, s);
+  if (p.mt > 1) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true, 4>(p, s) : flat_launch_t<KQ, RS, 2, true, 4>(p, s);
   if (p.i8) return p.W == 1 ? flat_launch_t<KQ, RS, 1, true>(p, s) : flat_launch_t<KQ, RS, 2, true>(p, s);
   return p.W == 1 ? flat_launch_t<KQ, RS, 1, false>(p, s) : flat_launch_t<KQ, RS, 2, false>(p, s);
 }
@@ -1938,8 +1941,9 @@ static hipError_t flat_launch(const FlatPlan& p, hipStream_t s) {
 template <int KQ, int RS>
 static int flat_waves_t(int mt) {
   hipFuncAttributes a{};
-  const void* f = mt > 1 ? reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true, 8>)
-                         : reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true>);
+  const void* f = mt > 4   ? reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true, 8>)
+                  : mt > 1 ? reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true, 4>)
+                           : reinterpret_cast<const void*>(&k_fused_flat<KQ, RS, 2, true>);
   if (hipFuncGetAttributes(&a, f) != hipSuccess || a.numRegs < 1) return 0;
   return 4 * std::min(8, 512 / ((a.numRegs + 7) / 8 * 8));
 }
