@@ -560,3 +560,43 @@ def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
             assert torch.equal(a, c) and torch.equal(a, b), nm
             _, y64 = reference_y(orc, mats[nm], x.double().numpy())
             check_err(a.cpu().numpy(), y64, "%s flat" % nm)
+
+
+def test_gpu_model_shaped_bundle(gpu, tmp_path, orc):
+    """A bundle laid out as the reference's model exporter writes one (cfg lines, raw8 / f32 tensors, mixed-format
+    K-quant matrices with their side tensors): every matrix resident, its GPU decode equal to the codes, m = 1 and
+    m = 3 products within the contract, one grouped call over a layer's four formats equal to per-matrix calls; the
+    raw8 tensor reads back as stored and the f32 tensors are refused by the matrix entry points."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from test_runtime_cpu import write_model_bundle
+    mats, embed = write_model_bundle(tmp_path)
+    rng = np.random.default_rng(4)
+    with Runtime(tmp_path) as rt:
+        assert rt.stat("resident_bytes") > 0
+        for name, kqt, N, K, H, seed in mats:
+            say("model bundle", name)
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
+            assert np.array_equal(rt.test_decode(name), codes), name
+            X = rng.standard_normal((3, K)).astype(np.float32)
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X.astype(np.float64))
+            check_err(rt.test_matmul(name, X[:1]), y64[:1], name + " m=1")
+            check_err(rt.test_matmul(name, X), y64, name + " m=3")
+        assert np.array_equal(rt.test_decode("embed"), embed)
+        with pytest.raises(RuntimeError):
+            rt.test_matmul("lnf", np.zeros((1, 512), np.float32))
+        layer = [m for m in mats if m[0].startswith("l1.")]
+        names = [m[0] for m in layer]
+        xs = [torch.randn(1, m[3]).half().cuda() for m in layer]
+        ys = [torch.zeros(1, m[2], device="cuda") for m in layer]
+        n = len(names)
+        assert rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[s.encode() for s in names]),
+                                          (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                          (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None) == 0
+        for nm, x, y in zip(names, xs, ys):
+            y1 = torch.zeros_like(y)
+            rt.matmul_dev(nm, x, y1)
+            torch.cuda.synchronize()
+            assert torch.equal(y, y1), nm

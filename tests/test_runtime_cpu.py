@@ -157,3 +157,58 @@ def test_packed_twin_bundle(lib, tmp_path):
     w.close()
     with pytest.raises(RuntimeError, match="packed blob shorter"):
         Runtime(tmp_path / "bad", budget_mb=0)
+
+
+def write_model_bundle(path, layers=2, hidden=512, inter=1024, vocab=96, seed=3):
+    """A bundle laid out as the reference's model exporter writes one (scripts/a2_kq_bundle.py:189-218): cfg lines,
+    a raw8 embedding with f32 row scales, f32 rope tables and norms, then per layer K-quant matrices of mixed formats
+    (Q4_K / IQ4_XS as huf4p, Q6_K / Q5_K as huf8) each followed by its .kqs side tensor. Returns the matrices."""
+    from lazyweights_amd import bundle
+    rng = np.random.default_rng(seed)
+    w = bundle.Writer(str(path))
+    for k, v in dict(n_layers=layers, hidden=hidden, n_heads=8, n_kv_heads=2, head_dim=hidden // 8, inter=inter,
+                     vocab=vocab, eps=1e-5, rope_rows=64, rope_half=hidden // 16, attn_scale=0.125, enc="kq_huf",
+                     tied=0, eos=2).items():
+        w.cfg(k, v)
+
+    def f32(name, v):
+        v = np.asarray(v, np.float32).reshape(1, -1) if np.ndim(v) == 1 else np.asarray(v, np.float32)
+        w.add(name, "f32", v.shape[0], v.shape[1], 1.0, 0, v.tobytes())
+    embed = rng.integers(0, 256, (vocab, hidden), dtype=np.uint8)
+    w.add("embed", "raw8", vocab, hidden, 1.0, 0, embed.tobytes())
+    f32("embed.rs", rng.uniform(0.01, 0.02, vocab))
+    f32("embed.rsub", rng.uniform(-1, 1, vocab))
+    f32("cos", rng.uniform(-1, 1, (64, hidden // 16)))
+    f32("sin", rng.uniform(-1, 1, (64, hidden // 16)))
+    mats = []
+    for i in range(layers):
+        f32("l%d.ln1" % i, rng.uniform(0.5, 1.5, hidden))
+        f32("l%d.ln2" % i, rng.uniform(0.5, 1.5, hidden))
+        for nm, kqt, N, K, H in (("q", 1, hidden, hidden, 2.3), ("gate", 4, inter, hidden, 2.6),
+                                 ("up", 2, inter, hidden, 3.4), ("down", 3, hidden, inter, 4.3)):
+            name = "l%d.%s" % (i, nm)
+            codes, side = bundle.synth_matrix(kqt, N, K, H, 100 * i + kqt)
+            w.add_kquant(name, kqt, codes, side)
+            mats.append((name, kqt, N, K, H, 100 * i + kqt))
+    f32("lnf", rng.uniform(0.5, 1.5, hidden))
+    w.close()
+    return mats, embed
+
+
+def test_open_model_shaped_bundle(lib, tmp_path):
+    """A model-shaped bundle (non-matrix f32 / raw8 tensors and cfg lines beside mixed-format K-quant matrices) opens;
+    every matrix decodes on the CPU to its symbols, the raw8 tensor reads back as stored, and the matrix-only entry
+    points refuse the non-matrix tensors with an error instead of exiting."""
+    from lazyweights_amd import Runtime, bundle
+    mats, embed = write_model_bundle(tmp_path)
+    cfg, ts = bundle.read_manifest(str(tmp_path))
+    assert cfg["n_layers"] == "2" and cfg["enc"] == "kq_huf"
+    with Runtime(tmp_path, budget_mb=0) as rt:
+        for name, kqt, N, K, H, seed in mats:
+            codes, _ = bundle.synth_matrix(kqt, N, K, H, seed)
+            assert np.array_equal(rt.test_cpu_decode(name, 2), bundle.form_symbols(kqt, codes)), name
+        s, n = rt.cpu_decode_all(2)
+        assert n == sum(N * (K // 2 if kqt in (1, 4) else K) for _, kqt, N, K, _, _ in mats)
+        for name in ("embed", "lnf", "l1.ln2"):
+            with pytest.raises(RuntimeError):
+                rt.test_cpu_decode(name, 1)
