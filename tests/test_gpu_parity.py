@@ -566,7 +566,8 @@ def test_gpu_model_shaped_bundle(gpu, tmp_path, orc):
     """A bundle laid out as the reference's model exporter writes one (cfg lines, raw8 / f32 tensors, mixed-format
     K-quant matrices with their side tensors): every matrix resident, its GPU decode equal to the codes, m = 1 and
     m = 3 products within the contract, one grouped call over a layer's four formats equal to per-matrix calls; the
-    raw8 tensor reads back as stored and the f32 tensors are refused by the matrix entry points."""
+    raw8 tensor reads back as stored and the f32 tensors are refused by the matrix entry points; with a 1 MB
+    residency budget the first matrices are resident and the last is refused."""
     import ctypes
 
     import torch
@@ -600,3 +601,15 @@ def test_gpu_model_shaped_bundle(gpu, tmp_path, orc):
             rt.matmul_dev(nm, x, y1)
             torch.cuda.synchronize()
             assert torch.equal(y, y1), nm
+    # residency budget (the reference's budget_mb, kernels/llmrt.cu:2037-2061): matrices in manifest order until the
+    # next one would pass the budget; the rest stay host-only and the GPU entry points refuse them
+    with Runtime(tmp_path, budget_mb=1) as rt:
+        say("model bundle, budget 1 MB: resident %.0f bytes" % rt.stat("resident_bytes"))
+        assert 0 < rt.stat("resident_bytes") < 2 << 20  # the budget counts coded bytes; sides come on top
+        first, last = mats[0], mats[-1]
+        codes, side = bundle.synth_matrix(*first[1:])
+        X = rng.standard_normal((1, first[3])).astype(np.float32)
+        check_err(rt.test_matmul(first[0], X), orc.gemv_f64(orc.dequant(first[1], codes, side), X.astype(np.float64)),
+                  first[0] + " within budget")
+        with pytest.raises(RuntimeError, match="not resident"):
+            rt.test_matmul(last[0], np.zeros((1, last[3]), np.float32))
