@@ -79,7 +79,8 @@ int lw_tensor_info(void* h, const char* name, int64_t* out);
 /* Device-pointer GEMV / skinny GEMM on `stream` (a hipStream_t; NULL = the null stream), no host copies, no
  * synchronisation: Y[m, N] (row stride ldy) = X[m, K] @ dequant(W)^T. X is fp16 (x_f16 = 1, the headline path,
  * m <= 16) or fp32 (x_f16 = 0: split into fp16 hi + lo; m <= 8 fused, any larger m the prefill path: decode into a
- * device scratch and a GEMM on the matrix cores, as rt_test_matmul's path 2). Returns 0 or -1. */
+ * device scratch and GEMMs on the matrix cores, as rt_test_matmul's path 2, see lw_set_prefill_gemm). Returns 0 or
+ * -1. */
 int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy, void* stream);
 
 /* Several independent matmuls (e.g. the matrices of one decoder layer), each with its own fp16 activations X[i]
