@@ -1539,10 +1539,11 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
 }
 
 // acc += dot2(x, w) with x = lane k of the lane's 16-lane row of xrow (DPP row_newbcast: x held the same in every
-// row, so the broadcast costs no v_readlane); xrow is only ever written by loads, so no VALU-to-DPP hazard arises
+// row, so the broadcast costs no v_readlane). The s_nop gives the DPP source the wait states it needs after a VALU
+// write, whatever the compiler placed before the statement (xrow itself comes from loads).
 template <int K>
 __device__ __forceinline__ void dot2_bcast(float& acc, uint32_t xrow, uint32_t w) {
-  asm("v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+  asm("s_nop 1\n\tv_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
       : "+v"(acc)
       : "v"(xrow), "v"(w), "n"(K));
 }
@@ -1949,14 +1950,18 @@ static int flat_waves_t(int mt) {
 }
 
 int flat_waves_per_cu(int kqt, int rs, int mt) {
-  if (rs != 16 && rs != 32) return 0;
+  if ((rs != 16 && rs != 32) || kqt < KQ_Q4_K || kqt > KQ_IQ4_XS) return 0;
+  // per (format, ring, 1 / 4 / 8 tokens): the attribute query once, its answer kept (one device per process)
+  static int cache[5][2][3] = {};
+  int& c = cache[kqt][rs == 32][mt > 4 ? 2 : (mt > 1 ? 1 : 0)];
+  if (c) return c;
   switch (kqt) {
-    case KQ_Q4_K: return rs == 16 ? flat_waves_t<KQ_Q4_K, 16>(mt) : flat_waves_t<KQ_Q4_K, 32>(mt);
-    case KQ_Q5_K: return rs == 16 ? flat_waves_t<KQ_Q5_K, 16>(mt) : flat_waves_t<KQ_Q5_K, 32>(mt);
-    case KQ_Q6_K: return rs == 16 ? flat_waves_t<KQ_Q6_K, 16>(mt) : flat_waves_t<KQ_Q6_K, 32>(mt);
-    case KQ_IQ4_XS: return rs == 16 ? flat_waves_t<KQ_IQ4_XS, 16>(mt) : flat_waves_t<KQ_IQ4_XS, 32>(mt);
-    default: return 0;
+    case KQ_Q4_K: c = rs == 16 ? flat_waves_t<KQ_Q4_K, 16>(mt) : flat_waves_t<KQ_Q4_K, 32>(mt); break;
+    case KQ_Q5_K: c = rs == 16 ? flat_waves_t<KQ_Q5_K, 16>(mt) : flat_waves_t<KQ_Q5_K, 32>(mt); break;
+    case KQ_Q6_K: c = rs == 16 ? flat_waves_t<KQ_Q6_K, 16>(mt) : flat_waves_t<KQ_Q6_K, 32>(mt); break;
+    default: c = rs == 16 ? flat_waves_t<KQ_IQ4_XS, 16>(mt) : flat_waves_t<KQ_IQ4_XS, 32>(mt); break;
   }
+  return c;
 }
 
 hipError_t launch_fused_flat(const FlatPlan& p, hipStream_t s) {
