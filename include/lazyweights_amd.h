@@ -100,8 +100,10 @@ int lw_set_kernel_mode(int mode);
 /* The GEMM of the decode-to-scratch path (path 2: m > 8, or rt_test_matmul path 2), for all handles. The
  * reference dequantizes to fp32 and runs its own fp32 GEMM (kernels/llmrt.cu:201-343, 1826-1841). 0 (default) =
  * the decoded weights w = s f(q) - o split into fp16 hi + lo, x likewise, two rocBLAS fp16 GEMMs with fp32
- * accumulation (x_hi w_hi + x_hi w_lo, then + x_lo w_hi); 1 = the hand-written matrix-core GEMM over the codes and
- * side bytes (fp16 hi + lo x). Kernel mode 1 overrides both with the SIMT GEMM. Returns 0 or -1. */
+ * accumulation (x_hi w_hi + x_hi w_lo, then + x_lo w_hi; up to 512 tokens as one GEMM over 2m columns, [x_hi | x_hi]
+ * and [x_lo | 0], whose halves are summed); 1 = the hand-written matrix-core GEMM over the codes and side bytes
+ * (fp16 hi + lo x); 2 / 3 = as 0 but always the two-GEMM / the one-GEMM form. Kernel mode 1 overrides all with the
+ * SIMT GEMM. Returns 0 or -1. */
 int lw_set_prefill_gemm(int which);
 
 /* Int8 activations for 1 <= m <= 8 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev

@@ -160,6 +160,10 @@ hipError_t launch_dequant_hilo(const DevMat& M, const uint8_t* codes, int row0, 
 // The same from the coded matrix directly (decode + dequant in one kernel; coded K-quant matrices with split
 // offsets): tile rows [tr0, tr1) -> WW rows relative to tr0 * 64
 hipError_t launch_decode_hilo(const DevMat& M, int tr0, int tr1, void* WW, hipStream_t s);
+// x [m][K] fp32 -> XB [2m][2K] fp16: rows t < m [hi | hi], rows m + t [lo | 0]
+hipError_t launch_split_x_gemm2(const float* X, void* XB, int m, int K, hipStream_t s);
+// Y[t][n] (rows ldy apart) = T[t][n] + T[m + t][n], T [2m][nr] fp32
+hipError_t launch_add_halves(const float* T, float* Y, int m, int nr, int ldy, hipStream_t s);
 // x [m][K] fp32 -> XX [m][2K] fp16 = [hi | hi], XL [m][K] fp16 = lo
 hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K, hipStream_t s);
 hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row0, int nrows, const void* X16, int m,

@@ -2582,6 +2582,43 @@ __global__ void k_split_x_gemm(const float* __restrict__ X, uint16_t* __restrict
   XL[i] = __builtin_bit_cast(uint16_t, lo);
 }
 
+// x [m][K] fp32 -> XB [2m][2K] fp16: rows t < m = [hi | hi], rows m + t = [lo | 0] (the B operand of the one-GEMM
+// prefill form, whose 2m columns give x_hi w_hi + x_hi w_lo and x_lo w_hi side by side)
+__global__ void k_split_x_gemm2(const float* __restrict__ X, uint16_t* __restrict__ XB, int m, int K) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)m * K) return;
+  const size_t j = i / K, k = i - j * K;
+  const float x = X[i];
+  const _Float16 hi = (_Float16)x;
+  const _Float16 lo = (_Float16)(x - (float)hi);
+  uint16_t* r = XB + j * 2 * K;
+  r[k] = r[K + k] = __builtin_bit_cast(uint16_t, hi);
+  uint16_t* q = XB + ((size_t)m + j) * 2 * K;
+  q[k] = __builtin_bit_cast(uint16_t, lo);
+  q[K + k] = 0;
+}
+
+hipError_t launch_split_x_gemm2(const float* X, void* XB, int m, int K, hipStream_t s) {
+  const size_t n = (size_t)m * K;
+  hipLaunchKernelGGL(k_split_x_gemm2, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, X, static_cast<uint16_t*>(XB),
+                     m, K);
+  return hipGetLastError();
+}
+
+// Y[t][n] = T[t][n] + T[m + t][n] for the one-GEMM prefill form (T [2m][nr] fp32, Y rows ldy apart)
+__global__ void k_add_halves(const float* __restrict__ T, float* __restrict__ Y, int m, int nr, int ldy) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)m * nr) return;
+  const size_t t = i / nr, n = i - t * nr;
+  Y[t * ldy + n] = T[i] + T[(size_t)m * nr + i];
+}
+
+hipError_t launch_add_halves(const float* T, float* Y, int m, int nr, int ldy, hipStream_t s) {
+  const size_t n = (size_t)m * nr;
+  hipLaunchKernelGGL(k_add_halves, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, T, Y, m, nr, ldy);
+  return hipGetLastError();
+}
+
 hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K, hipStream_t s) {
   const size_t n = (size_t)m * K;
   hipLaunchKernelGGL(k_split_x_gemm, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, X,

@@ -124,6 +124,8 @@ struct Model {
   size_t codes_cap = 0;
   uint16_t* W16 = nullptr;  // prefill: fp16 [hi | lo] weights of a chunk of rows
   size_t W16_cap = 0;
+  float* T32 = nullptr;  // prefill, one-GEMM form: the GEMM's [2m][rows] output
+  size_t T32_cap = 0;
   rocblas_handle blas = nullptr;  // prefill GEMMs, created on first use
   int verbose = 0;
   Tensor* find(const char* name) {
@@ -398,6 +400,7 @@ void release(Model* M) {
   if (M->x8) (void)hipFree(M->x8);
   if (M->codes) (void)hipFree(M->codes);
   if (M->W16) (void)hipFree(M->W16);
+  if (M->T32) (void)hipFree(M->T32);
   if (M->blas) (void)rocblas_destroy_handle(M->blas);
   if (M->stream) (void)hipStreamDestroy(M->stream);
   if (M->fd >= 0) close(M->fd);
@@ -913,8 +916,9 @@ int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, in
   return fused_group_dev(M, &tp, &X16, 1, m, per, &Y, &ldy, s);
 }
 
-// Prefill GEMM of path 2: 0 (default) = decoded codes dequantized to fp16 hi + lo weights and two rocBLAS GEMMs;
-// 1 = the hand-written MFMA GEMM over the codes (k_gemm_codes_mfma). Kernel mode 1 keeps the SIMT GEMM.
+// Prefill GEMM of path 2: 0 (default) = decoded codes dequantized to fp16 hi + lo weights and rocBLAS (the one-GEMM
+// form up to g_prefill_one_max tokens, else two GEMMs); 1 = the hand-written MFMA GEMM over the codes
+// (k_gemm_codes_mfma); 2 / 3 = rocBLAS, always the two-GEMM / the one-GEMM form. Kernel mode 1 keeps the SIMT GEMM.
 int g_prefill = 0;
 
 // Y[:, r0 : r0 + nr] = x . w^T for a chunk of rows through rocBLAS. WW is the column-major nr x 2K matrix [w hi |
@@ -939,9 +943,33 @@ int blas_chunk(Model& M, const uint16_t* WW, const uint16_t* XX, const uint16_t*
   return 0;
 }
 
+// The one-GEMM form for small m (memory-bound on the weights): T (column-major nr x 2m, ld nr) = WW . XB with XB the
+// column-major 2K x 2m matrix of [x hi | x hi] (columns t < m) and [x lo | 0] (columns m + t): the weights are read
+// once (4 B per weight instead of 6) and the launch has twice the output columns; a third of its products are with
+// the zero half. Y[:, r0 : r0 + nr] = T[:m] + T[m:].
+int blas_chunk_one(Model& M, const uint16_t* WW, const uint16_t* XB, int nr, int m, int K, float* Y, int ldy,
+                   hipStream_t s) {
+  const float one = 1.f, zero = 0.f;
+  rocblas_status st = rocblas_gemm_ex(M.blas, rocblas_operation_none, rocblas_operation_none, nr, 2 * m, 2 * K, &one,
+                                      WW, rocblas_datatype_f16_r, nr, XB, rocblas_datatype_f16_r, 2 * K, &zero, M.T32,
+                                      rocblas_datatype_f32_r, nr, M.T32, rocblas_datatype_f32_r, nr,
+                                      rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success) {
+    g_err = std::string("rocblas_gemm_ex: ") + rocblas_status_to_string(st);
+    return -1;
+  }
+  HIPCHECK(lw::launch_add_halves(M.T32, Y, m, nr, ldy, s));
+  return 0;
+}
+
+// m up to this takes the one-GEMM form: measured faster at every m from 32 to 512 on a config-2 layer (0.76 vs
+// 0.92 ms at m = 128, 1.38 vs 1.45 ms at m = 512); beyond, the third of its products that meet the zero half grows
+// with m while the weight reads it saves do not
+int g_prefill_one_max = 512;
+
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
 int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
-  const bool blas = g_kernel_mode != 1 && g_prefill == 0;
+  const bool blas = g_kernel_mode != 1 && g_prefill != 1;
   const bool mfma = g_kernel_mode != 1 && !blas;
   if (blas) {
     if (!M.blas && rocblas_create_handle(&M.blas) != rocblas_status_success) {
@@ -956,9 +984,12 @@ int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ld
     // fp16 x: [m][2K] hi | hi, then [m][K] lo; weights [rows][2K] fp16 per chunk of tile rows (at most 256 MB)
     const size_t ww_row = (size_t)lw::TN * t.K * 4;
     const size_t cap = std::max(ww_row, std::min<size_t>((size_t)t.N * t.K * 4, (size_t)256 << 20));
-    if (grow(M.X16, M.X16_cap, (size_t)3 * m * t.K * 2) || grow(M.W16, M.W16_cap, cap)) return -1;
-    HIPCHECK(lw::launch_split_x_gemm(X, M.X16, M.X16 + (size_t)2 * m * t.K, m, (int)t.K, s));
+    const bool one = g_prefill == 3 || (g_prefill == 0 && m <= g_prefill_one_max);
+    if (grow(M.X16, M.X16_cap, (size_t)(one ? 4 : 3) * m * t.K * 2) || grow(M.W16, M.W16_cap, cap)) return -1;
+    if (one) HIPCHECK(lw::launch_split_x_gemm2(X, M.X16, m, (int)t.K, s));
+    else HIPCHECK(lw::launch_split_x_gemm(X, M.X16, M.X16 + (size_t)2 * m * t.K, m, (int)t.K, s));
     const int rows_fit = (int)std::max<size_t>(1, M.W16_cap / ww_row);
+    if (one && grow(M.T32, M.T32_cap, (size_t)2 * m * std::min<size_t>((size_t)rows_fit * lw::TN, t.N) * 4)) return -1;
     const bool fused = !t.dm.packed && t.dm.split;  // decode + dequant in one kernel
     if (!fused && grow(M.codes, M.codes_cap, (size_t)rows_fit * lw::TN * t.K)) return -1;
     for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit) {
@@ -969,7 +1000,8 @@ int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ld
         HIPCHECK(lw::launch_decode(t.dm, M.codes, tr0, tr1, s));
         HIPCHECK(lw::launch_dequant_hilo(t.dm, M.codes, tr0 * lw::TN, nr, M.W16, s));
       }
-      if (blas_chunk(M, M.W16, M.X16, M.X16 + (size_t)2 * m * t.K, nr, m, (int)t.K, Y + (size_t)tr0 * lw::TN, ldy))
+      if (one ? blas_chunk_one(M, M.W16, M.X16, nr, m, (int)t.K, Y + (size_t)tr0 * lw::TN, ldy, s)
+              : blas_chunk(M, M.W16, M.X16, M.X16 + (size_t)2 * m * t.K, nr, m, (int)t.K, Y + (size_t)tr0 * lw::TN, ldy))
         return -1;
     }
     return 0;
@@ -1381,7 +1413,7 @@ int lw_set_kernel_mode(int mode) {
 }
 
 int lw_set_prefill_gemm(int which) {
-  if (which != 0 && which != 1) return -1;
+  if (which < 0 || which > 3) return -1;
   g_prefill = which;
   return 0;
 }

@@ -135,7 +135,8 @@ def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
         Ys = rt.test_matmul(fmt, X, path=2)
     finally:
         rt.lib.lw_set_kernel_mode(0)
-    for which, what in ((0, "rocBLAS hi + lo"), (1, "matrix-core codes GEMM")):
+    for which, what in ((0, "rocBLAS hi + lo"), (2, "rocBLAS two GEMMs"), (3, "rocBLAS one GEMM"),
+                        (1, "matrix-core codes GEMM")):
         say("prefill m=80", fmt, what)
         assert rt.lib.lw_set_prefill_gemm(which) == 0
         try:
