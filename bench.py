@@ -284,8 +284,8 @@ def main():
         # GEMM over the codes (a reported figure, not the metric)
         prefill = None
         if not a.no_prefill:
-            prefill = {"path": "decode to scratch + dequant to fp16 hi + lo weights + two rocBLAS fp16 GEMMs "
-                               "(fp32 accumulation)", "runs": []}
+            prefill = {"path": "decode + dequant to fp16 hi + lo weights, rocBLAS fp16 GEMM with fp32 accumulation "
+                               "(one GEMM over 2m columns up to m = 512)", "runs": []}
             for pm in (128, 512):
                 XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
                 YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
