@@ -2243,12 +2243,101 @@ __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ 
   }
 }
 
+// Codes of a coded matrix with split offsets (the decode bench, rt_test_decode, path 2's codes): one block of 4 waves
+// per tile, the tile staged in LDS, 8 chains per lane (wave w: symbols [64 w, 64 w + 64) of row l and row l + 32,
+// as k_fused_split). The table entries are rebuilt per block as len | sym << 16 from the reference layout's u16
+// LUT. Each wave collects its 64 rows x CW code bytes in LDS (rows 136 B apart: 8-byte aligned, 2-way bank
+// conflicts at most) and then stores them row by row, whole 64- or 128-byte segments, so the rows' lines are written
+// at once instead of 4 bytes per row and store.
+template <int SYMB>
+__global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1,
+                                                      int stage_rows) {
+  constexpr int CW = SYMB == 4 ? 128 : 64;  // code bytes per row and wave
+  constexpr int RSTR = 136;                 // LDS row stride of the code rows
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  // one static LDS object, the table first, so that the table sits at LDS address 0 (table_addr ORs its base into
+  // the index bits), then the 4 waves' code rows
+  __shared__ __align__(16) uint32_t lds_static[LUTN + 4 * 64 * RSTR / 4];
+  uint32_t* lut4 = lds_static;
+  uint8_t* rowbuf = reinterpret_cast<uint8_t*>(lds_static + LUTN);
+  extern __shared__ __align__(16) uint32_t tw[];
+  const int KT = M.KT, K = M.K;
+  const int t = tr0 * KT + (int)blockIdx.x;
+  if (t >= tr1 * KT) return;
+  const int tc = t % KT, tr = t / KT;
+  const int R = min((int)M.rows[t] + 2, stage_rows);
+  for (int i = threadIdx.x; i < LUTN; i += 256) {
+    const uint32_t e = M.lut[i];
+    lut4[i] = (e >> 8) | (e & 255u) << 16;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
+  for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  const int k = 4 * f + wave;
+  uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k * (SPLITS / 8)) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+  const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
+  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
+  uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
+  uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
+  uint32_t C = *(LdsU32*)(rlb + (slot << 7));
+  uint8_t* const wbuf = rowbuf + wave * 64 * RSTR;     // the wave's 64 code rows
+  uint8_t* rb = wbuf + (f * 32 + l) * RSTR;              // the lane's row
+#pragma unroll 4
+  for (int p = 0; p < 32; ++p) {
+    const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
+    const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
+    const uint32_t w2 = w1 >> (e1 & 31u);
+    const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
+    P = P + e1 + e2;
+    const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, 8);
+    const bool slide = nslot != slot;
+    A = slide ? B : A;
+    B = slide ? C : B;
+    slot = nslot;
+    C = *(LdsU32*)(rlb + (nslot << 7));
+    const uint32_t s1 = e1 >> 16, s2 = e2 >> 16;
+    if (SYMB == 4)  // codes low nibble first: 4 bytes per pair
+      *reinterpret_cast<uint32_t*>(rb + 4 * p) = (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
+    else
+      *reinterpret_cast<uint16_t*>(rb + 2 * p) = (uint16_t)(s1 | s2 << 8);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // the wave's 64 rows: 8-byte pieces, CW / 8 lanes per row
+  constexpr int LPR = CW / 8, RPI = 64 / LPR;  // lanes per row, rows per store instruction
+  const int pr = lane / LPR, pc = lane % LPR;
+  uint8_t* orow = out + (size_t)((tr - tr0) * TN) * K + (size_t)tc * (SYMB == 4 ? 2 * TK : TK) + wave * CW + pc * 8;
+#pragma unroll
+  for (int r0 = 0; r0 < 64; r0 += RPI) {
+    const int r = r0 + pr;
+    *reinterpret_cast<uint2*>(orow + (size_t)r * K) = *reinterpret_cast<const uint2*>(wbuf + r * RSTR + pc * 8);
+  }
+}
+
 hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
   if (M.packed) {
     const size_t n = (size_t)(tr1 - tr0) * M.KT * 16 * 64;
     if (!n) return hipSuccess;
     if (M.symbits == 4) hipLaunchKernelGGL(k_unpack<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
     else hipLaunchKernelGGL(k_unpack<8>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
+    return hipGetLastError();
+  }
+  if (M.split && M.rows && M.lut && tr0 < tr1 && M.max_rows + 2 <= 256) {  // the 8-chain kernel
+    const int rows = M.max_rows + 2;
+    const size_t sm = (size_t)rows * 128;
+    const void* f = M.symbits == 4 ? reinterpret_cast<const void*>(&k_decode_split<4>)
+                                   : reinterpret_cast<const void*>(&k_decode_split<8>);
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+    if (e != hipSuccess) return e;
+    const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
+    if (M.symbits == 4) hipLaunchKernelGGL(k_decode_split<4>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+    else hipLaunchKernelGGL(k_decode_split<8>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
     return hipGetLastError();
   }
   const size_t smem = (size_t)LUTN * 8 + (size_t)4 * 32 * (M.max_rows + 1) * 4;
