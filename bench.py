@@ -218,6 +218,15 @@ def main():
             % (kernel_ms_per_pass, launches, a.layers, layer_us, achieved))
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
+        # decode only (the reference's decode bench, rt_gpu_decode_all): every matrix of the workload to code bytes,
+        # median of 5 passes
+        dsec = lib.rt_gpu_decode_all(rt.h, 5)
+        ncodes = float(sum(inf["N"] * inf["K"] for inf in infos))
+        decode_only = {"ms_per_pass": round(dsec * 1e3, 4), "Gcodes_per_s": round(ncodes / dsec / 1e9, 1),
+                       "kernel": "k_decode_split"} if dsec > 0 else None
+        if decode_only:
+            log("bench: decode only %.3f ms per pass over %d layers, %.1f G codes/s"
+                % (dsec * 1e3, a.layers, decode_only["Gcodes_per_s"]))
 
         # int8 activations (the reference's default act8 mode; m = 1 only): the same step with x quantized per block
         # of 32 on the device (one quantization launch per distinct x) and integer sub-block dot products
@@ -403,6 +412,7 @@ def main():
             "control_stream_read_GBps": round(ctrl, 1),
             "control_packed_twin": packed,
             "act8": act8,
+            "decode_only": decode_only,
             "verify_m5": verify,
             "prefill_path2": prefill,
         }
