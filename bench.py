@@ -21,6 +21,7 @@ One JSON line on stdout.
 """
 import argparse
 import json
+import math
 import os
 import shutil
 import sys
@@ -94,6 +95,29 @@ def measure_traffic(layers):
         return (f[0] * f[1] + w[0] * w[1]) * 1024.0, f[1], w[1]
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
+
+
+def cpu_share():
+    """Threads for the CPU baseline: every core this process may run on (its affinity mask), capped by the cgroup's
+    CPU quota when one is set (a share of a larger host); plus what the host reports, for the record."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    n = aff if quota is None else max(1, min(aff, int(math.ceil(quota))))
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return n, {"nproc": os.cpu_count(), "affinity_cores": aff, "cgroup_cpu_quota": quota, "cpu_model": model}
 
 
 def main():
@@ -362,7 +386,8 @@ def main():
         cpu = None
         if not a.no_cpu:
             from oracle import oracle as orc
-            threads = min(16, len(os.sched_getaffinity(0)))
+            threads, host = cpu_share()
+            coded_total = float(sum(inf["blob_bytes"] for inf in infos))
             cfg, ts = bundle.read_manifest(work)
             by = {t["name"]: t for t in ts}
             layer0 = config2_layer(0)
@@ -386,12 +411,24 @@ def main():
                     orc.decode_gemv(1, b, s, N, K, x, min(6, threads))
                 t6 += time.perf_counter() - t0
                 reps6 += 1
+            # decode only, the reference's CPU decode bench (rt_cpu_decode_all: every coded matrix of the workload,
+            # blobs read before the clock starts, kernels/llmrt.cu:2558-2573), on all cores and on 6
+            dec = {}
+            for nth in sorted({threads, min(6, threads)}, reverse=True):
+                s_dec, nsym = rt.cpu_decode_all(nth)
+                dec[nth] = {"threads": nth, "seconds": round(s_dec, 3), "symbols": int(nsym),
+                            "Gsym_per_s": round(nsym / s_dec / 1e9, 3),
+                            "GBps_coded": round(coded_total / s_dec / 1e9, 3)}
             cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
                    "sample": "layer 0 of the workload (7 matrices, %.1f MB coded), %d passes, %.1f s; "
                              "oracle cpu_decode + dequant + fp32 GEMV" % (sample_bytes / 1e6, reps, t_cpu),
-                   "value_6_threads": round(sample_bytes * reps6 / t6 / 1e9, 3)}
-            log("bench: cpu baseline %.2f GB/s on %d threads, %.2f GB/s on %d"
-                % (cpu_gbs, threads, cpu["value_6_threads"], min(6, threads)))
+                   "value_6_threads": round(sample_bytes * reps6 / t6 / 1e9, 3),
+                   "host": host,
+                   "decode_only": {"what": "rt_cpu_decode_all over the %d layers (%.1f MB coded), symbols to memory"
+                                           % (a.layers, coded_total / 1e6),
+                                   "all_cores": dec[threads], "six_threads": dec[min(6, threads)]}}
+            log("bench: cpu baseline %.2f GB/s on %d threads, %.2f GB/s on %d; decode only %.2f G symbols/s on %d"
+                % (cpu_gbs, threads, cpu["value_6_threads"], min(6, threads), dec[threads]["Gsym_per_s"], threads))
 
         res = {
             "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": a.steps,

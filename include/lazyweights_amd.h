@@ -138,6 +138,17 @@ int lw_form_symbols(int kqt, const uint8_t* codes, int N, int K, uint8_t* sym);
 /* Encode symbols [N, KS] as a huf8/huf4p blob (lazyweights/bundle.py:57-85). Returns the blob size; writes it
  * to `blob` when cap is large enough; *bits = payload bits. -1 on bad shapes. */
 long long lw_encode(const uint8_t* sym, int N, int KS, uint8_t* blob, long long cap, uint64_t* bits);
+/* Incremental bundle-directory writer (the format of lazyweights/bundle.py:10-21, 114-136: weights.bin with every
+ * tensor at a 256-byte boundary, manifest.txt with `cfg <key> <value>` and
+ * `t <name> <enc> <N> <K> <scale> <zp> <offset> <nbytes>` lines). lw_bundle_create returns NULL if the directory
+ * cannot be written. Names, encodings, keys and values are single words (no white space): lw_bundle_cfg /
+ * lw_bundle_add return -1 and write nothing otherwise. lw_bundle_finish writes the manifest, frees the handle and
+ * returns 0, or -1 if any file write failed. */
+void* lw_bundle_create(const char* dir);
+int lw_bundle_cfg(void* w, const char* key, const char* value);
+int lw_bundle_add(void* w, const char* name, const char* enc, long long N, long long K, double scale, int zp,
+                  const void* data, long long nbytes);
+int lw_bundle_finish(void* w);
 /* Write a bundle directory of `count` synthetic K-quant matrices (each with its .kqs side tensor). */
 int lw_write_bundle(const char* dir, int count, const char* const* names, const int* kqts, const int* Ns,
                     const int* Ks, const double* entropies, const uint64_t* seeds, int threads);

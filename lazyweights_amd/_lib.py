@@ -39,6 +39,10 @@ SIGNATURES = {
     "lw_form_symbols": (_i, [_i, _vp, _i, _i, _vp]),
     "lw_encode": (_ll, [_vp, _i, _i, _vp, _ll, _c.POINTER(_u64)]),
     "lw_write_bundle": (_i, [_cp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i]),
+    "lw_bundle_create": (_vp, [_cp]),
+    "lw_bundle_cfg": (_i, [_vp, _cp, _cp]),
+    "lw_bundle_add": (_i, [_vp, _cp, _cp, _ll, _ll, _d, _i, _vp, _ll]),
+    "lw_bundle_finish": (_i, [_vp]),
     "lw_huffman_lengths": (_i, [_vp, _i, _i, _vp]),
     "lw_build_layout": (_ll, [_vp, _ll, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll]),
     "lw_set_kernel_mode": (_i, [_i]),

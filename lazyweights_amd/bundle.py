@@ -1,8 +1,10 @@
 """Bundle directories and coded blobs, with the reference's Python names (lazyweights/bundle.py).
 
-Writer / read_manifest follow lazyweights/bundle.py:114-148 (manifest.txt + weights.bin, every blob 256-byte
-aligned). encode_huf8 produces the same blob bytes as lazyweights/bundle.py:57-85 (checked byte for byte against
-fixtures written by the reference encoder), computed by the C++ codec of this library.
+A bundle directory (lazyweights/bundle.py:10-21, 114-150) is `weights.bin`, every tensor starting at a 256-byte
+boundary, plus `manifest.txt`: `cfg <key> <value>` lines and one `t <name> <enc> <N> <K> <scale> <zp> <offset>
+<nbytes>` line per tensor. Writer drives the library's C++ bundle writer (lw_bundle_*); read_manifest parses the
+manifest by the field table below. encode_huf8 produces the same blob bytes as lazyweights/bundle.py:57-85 (checked
+byte for byte against fixtures written by the reference encoder), computed by the C++ codec of this library.
 """
 import ctypes
 import os
@@ -52,23 +54,27 @@ def form_symbols(kqt, codes):
 
 
 class Writer:
+    """Writer(path).cfg(key, value) / .add(name, enc, N, K, scale, zp, blob) / .add_kquant(...) / .close()."""
+
     def __init__(self, path):
-        os.makedirs(path, exist_ok=True)
-        self.path = path
-        self.f = open(os.path.join(path, "weights.bin"), "wb")
-        self.lines = []
-        self.off = 0
+        self.lib = load_library()
+        self.path = str(path)
+        self.h = self.lib.lw_bundle_create(self.path.encode())
+        if not self.h:
+            raise OSError("cannot write a bundle at %s" % self.path)
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise ValueError("bundle %s: %s refused (a name, key or value with white space, or a write error)"
+                             % (self.path, what))
 
     def cfg(self, k, v):
-        self.lines.append("cfg %s %s" % (k, v))
+        self._check(self.lib.lw_bundle_cfg(self.h, str(k).encode(), str(v).encode()), "cfg " + str(k))
 
     def add(self, name, enc, N, K, scale, zp, blob):
-        pad = (-self.off) % ALIGN
-        self.f.write(b"\0" * pad)
-        self.off += pad
-        self.f.write(blob)
-        self.lines.append("t %s %s %d %d %.9g %d %d %d" % (name, enc, N, K, scale, zp, self.off, len(blob)))
-        self.off += len(blob)
+        data = np.frombuffer(bytes(blob), np.uint8)
+        self._check(self.lib.lw_bundle_add(self.h, name.encode(), enc.encode(), int(N), int(K), float(scale), int(zp),
+                                           data.ctypes.data if data.size else None, data.size), "tensor " + name)
 
     def add_kquant(self, name, kqt, codes, side, packed=False):
         """A K-quant matrix as the reference bundler writes it (scripts/a2_kq_bundle.py:216-218): Huffman-coded
@@ -83,21 +89,28 @@ class Writer:
         self.add(name + ".kqs", "kq_" + KQ_NAME[kqt], N, side.shape[1], 1.0, 0, np.ascontiguousarray(side).tobytes())
 
     def close(self):
-        self.f.close()
-        with open(os.path.join(self.path, "manifest.txt"), "w") as f:
-            f.write("\n".join(self.lines) + "\n")
+        if self.h:
+            h, self.h = self.h, None
+            self._check(self.lib.lw_bundle_finish(h), "finish")
+
+
+# fields of a manifest `t` line after the tag, in order, with their types
+T_FIELDS = (("name", str), ("enc", str), ("N", int), ("K", int), ("scale", float), ("zp", int), ("offset", int),
+            ("nbytes", int))
 
 
 def read_manifest(path):
-    cfg, ts = {}, []
-    for line in open(os.path.join(path, "manifest.txt")):
-        p = line.split()
-        if p and p[0] == "cfg":
-            cfg[p[1]] = p[2]
-        elif p and p[0] == "t":
-            ts.append(dict(name=p[1], enc=p[2], N=int(p[3]), K=int(p[4]), scale=float(p[5]), zp=int(p[6]),
-                           offset=int(p[7]), nbytes=int(p[8])))
-    return cfg, ts
+    """(cfg dict of strings, list of tensor dicts with the T_FIELDS keys, in manifest order)."""
+    cfg, tensors = {}, []
+    with open(os.path.join(path, "manifest.txt")) as f:
+        text = f.read()
+    for fields in (ln.split() for ln in text.splitlines()):
+        tag, rest = (fields[0], fields[1:]) if fields else ("", [])
+        if tag == "t" and len(rest) == len(T_FIELDS):
+            tensors.append({key: conv(v) for (key, conv), v in zip(T_FIELDS, rest)})
+        elif tag == "cfg" and len(rest) >= 2:
+            cfg[rest[0]] = rest[1]
+    return cfg, tensors
 
 
 def read_tensor(path, t):

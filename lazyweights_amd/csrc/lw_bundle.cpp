@@ -50,31 +50,105 @@ long long lw_encode(const uint8_t* sym, int N, int KS, uint8_t* blob, long long 
   return (long long)e.blob.size();
 }
 
+}  // extern "C"
+
+namespace {
+// An open bundle directory: weights.bin is written as tensors arrive, each blob at the next 256-byte boundary; the
+// manifest text (cfg lines first, then one t line per tensor in write order) is kept in memory and written by
+// finish(). A refused name or key writes nothing and is reported by the call; an I/O error sticks, and finish() then
+// reports failure.
+class BundleWriter {
+ public:
+  explicit BundleWriter(const std::string& dir) : dir_(dir) {
+    mkdir(dir.c_str(), 0755);
+    bin_ = fopen((dir + "/weights.bin").c_str(), "wb");
+    ok_ = bin_ != nullptr;
+  }
+  ~BundleWriter() {
+    if (bin_) fclose(bin_);
+  }
+  bool ok() const { return ok_; }
+  static bool word(const char* w) { return w && *w && !strpbrk(w, " \t\n\r"); }
+  bool cfg(const char* key, const char* value) {
+    if (!word(key) || !word(value)) return false;
+    cfg_ += std::string("cfg ") + key + " " + value + "\n";
+    return true;
+  }
+  bool tensor(const char* name, const char* enc, long long N, long long K, double scale, int zp, const void* data,
+              size_t n) {
+    if (!ok_ || !word(name) || !word(enc) || (!data && n)) return false;
+    static const uint8_t zeros[kAlign] = {0};
+    const size_t gap = (size_t)((kAlign - at_ % kAlign) % kAlign);
+    if (gap && fwrite(zeros, 1, gap, bin_) != gap) ok_ = false;
+    at_ += gap;
+    if (n && fwrite(data, 1, n, bin_) != n) ok_ = false;
+    char line[640];
+    snprintf(line, sizeof line, "t %s %s %lld %lld %.9g %d %llu %zu\n", name, enc, N, K, scale, zp,
+             (unsigned long long)at_, n);
+    t_ += line;
+    at_ += n;
+    return ok_;
+  }
+  bool finish() {
+    if (bin_ && fclose(bin_) != 0) ok_ = false;
+    bin_ = nullptr;
+    if (!ok_) return false;
+    FILE* m = fopen((dir_ + "/manifest.txt").c_str(), "w");
+    if (!m) return false;
+    const std::string text = cfg_ + t_;
+    const bool wrote = fwrite(text.data(), 1, text.size(), m) == text.size();
+    return (fclose(m) == 0) && wrote;
+  }
+
+ private:
+  static constexpr size_t kAlign = 256;
+  std::string dir_, cfg_, t_;
+  FILE* bin_ = nullptr;
+  uint64_t at_ = 0;
+  bool ok_ = false;
+};
+}  // namespace
+
+extern "C" {
+
+void* lw_bundle_create(const char* dir) {
+  if (!dir) return nullptr;
+  auto* w = new BundleWriter(dir);
+  if (!w->ok()) {
+    delete w;
+    return nullptr;
+  }
+  return w;
+}
+
+int lw_bundle_cfg(void* w, const char* key, const char* value) {
+  if (!w) return -1;
+  return static_cast<BundleWriter*>(w)->cfg(key, value) ? 0 : -1;
+}
+
+int lw_bundle_add(void* w, const char* name, const char* enc, long long N, long long K, double scale, int zp,
+                  const void* data, long long nbytes) {
+  if (!w || nbytes < 0) return -1;
+  return static_cast<BundleWriter*>(w)->tensor(name, enc, N, K, scale, zp, data, (size_t)nbytes) ? 0 : -1;
+}
+
+int lw_bundle_finish(void* w) {
+  if (!w) return -1;
+  auto* b = static_cast<BundleWriter*>(w);
+  const bool ok = b->finish();
+  delete b;
+  return ok ? 0 : -1;
+}
+
 int lw_write_bundle(const char* dir, int count, const char* const* names, const int* kqts, const int* Ns,
                     const int* Ks, const double* entropies, const uint64_t* seeds, int threads) {
   if (!dir || count < 1 || !names || !kqts || !Ns || !Ks || !entropies || !seeds) return -1;
   for (int i = 0; i < count; ++i)
     if (!names[i] || !shape_ok(kqts[i], Ns[i], Ks[i])) return -1;
-  mkdir(dir, 0755);
-  const std::string d(dir);
-  FILE* w = fopen((d + "/weights.bin").c_str(), "wb");
-  if (!w) return -1;
-  std::string manifest;
-  uint64_t off = 0;
-  auto add = [&](const std::string& name, const char* enc, long long N, long long K, const uint8_t* p, size_t n) {
-    static const uint8_t zeros[256] = {0};
-    const size_t pad = (size_t)((256 - off % 256) % 256);
-    if (pad) fwrite(zeros, 1, pad, w);
-    off += pad;
-    fwrite(p, 1, n, w);
-    char line[512];
-    snprintf(line, sizeof line, "t %s %s %lld %lld %.9g %d %llu %zu\n", name.c_str(), enc, N, K, 1.0, 0,
-             (unsigned long long)off, n);
-    manifest += line;
-    off += n;
-  };
+  BundleWriter w(dir);
+  if (!w.ok()) return -1;
   std::vector<uint8_t> codes, side, sym;
-  for (int i = 0; i < count; ++i) {
+  for (int i = 0; i < count && w.ok(); ++i) {
     const int kqt = kqts[i], N = Ns[i], K = Ks[i], SB = lw::kq_sbytes(kqt);
     codes.resize((size_t)N * K);
     side.resize((size_t)N * (K / 256) * SB);
@@ -84,18 +158,13 @@ int lw_write_bundle(const char* dir, int count, const char* const* names, const 
     lw::form_symbols(kqt, codes.data(), N, K, sym.data());
     lw::Encoded e;
     std::string err;
-    if (!lw::encode_huf8(sym.data(), N, KS, threads, e, err)) {
-      fclose(w);
+    if (!lw::encode_huf8(sym.data(), N, KS, threads, e, err)) return -1;
+    if (!w.tensor(names[i], lw::kq_symbits(kqt) == 4 ? "huf4p" : "huf8", N, K, 1.0, 0, e.blob.data(), e.blob.size()) ||
+        !w.tensor((std::string(names[i]) + ".kqs").c_str(), kq_name(kqt), N, (long long)(K / 256) * SB, 1.0, 0,
+                  side.data(), side.size()))
       return -1;
-    }
-    add(names[i], lw::kq_symbits(kqt) == 4 ? "huf4p" : "huf8", N, K, e.blob.data(), e.blob.size());
-    add(std::string(names[i]) + ".kqs", kq_name(kqt), N, (long long)(K / 256) * SB, side.data(), side.size());
   }
-  const bool ok = fclose(w) == 0;
-  FILE* m = fopen((d + "/manifest.txt").c_str(), "w");
-  if (!m) return -1;
-  fwrite(manifest.data(), 1, manifest.size(), m);
-  return (fclose(m) == 0 && ok) ? 0 : -1;
+  return w.finish() ? 0 : -1;
 }
 
 int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L) {

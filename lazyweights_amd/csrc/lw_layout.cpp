@@ -371,36 +371,97 @@ bool build_layout_il(const uint8_t* data, size_t len, int N, int KS, bool compac
   return true;
 }
 
-double cpu_decode(const uint8_t* blob, int N, int KS, int threads, uint8_t* out) {
+// One lane stream of a raw blob as a bit source: a 64-bit buffer topped up a word at a time from the payload, so
+// each symbol costs one table lookup and one shift; words past the payload's end read as zero.
+struct LaneBits {
+  const uint32_t* pay;
+  uint64_t nwords, next;  // payload words, next word to load
+  uint64_t buf = 0;       // unread bits, LSB first
+  int have = 0;           // valid bits in buf
+  LaneBits(const uint32_t* p, uint64_t n, uint64_t bit) : pay(p), nwords(n), next(bit >> 5) {
+    fill();
+    const int skip = (int)(bit & 31);
+    buf >>= skip;
+    have -= skip;
+  }
+  void fill() {
+    while (have <= 32) {
+      const uint64_t w = next < nwords ? pay[next] : 0u;
+      ++next;
+      buf |= w << have;
+      have += 32;
+    }
+  }
+  uint32_t peek() const { return (uint32_t)buf; }
+  void drop(int n) {
+    buf >>= n;
+    have -= n;
+    if (have <= 32) fill();
+  }
+};
+
+bool cpu_decode(const uint8_t* blob, size_t nbytes, int N, int KS, int threads, uint8_t* out, double* seconds,
+                std::string& err) {
+  if (N <= 0 || KS <= 0 || N % TN || KS % TK) {
+    err = "cpu decode: shape is not a whole number of 64 x 256 tiles";
+    return false;
+  }
   const int KT = KS / TK, T = (N / TN) * KT;
-  const uint16_t* lut = reinterpret_cast<const uint16_t*>(blob);
-  const uint32_t* starts = reinterpret_cast<const uint32_t*>(blob + 2 * LUTN);
-  const uint8_t* payload = reinterpret_cast<const uint8_t*>(starts + (size_t)T * LANES);
-  threads = std::max(1, threads);
-  auto work = [&](int tid) {
-    for (int tt = tid; tt < T; tt += threads) {
-      const int tr = tt / KT, tc = tt - tr * KT;
-      for (int lane = 0; lane < LANES; ++lane) {
-        uint64_t bp = starts[(size_t)tt * LANES + lane];
-        for (int half = 0; half < 2; ++half) {
-          uint8_t* row = out + (size_t)(tr * TN + half * 32 + lane) * KS + (size_t)tc * TK;
+  const size_t head = sizeof(uint16_t) * LUTN + sizeof(uint32_t) * (size_t)T * LANES;
+  if (!blob || nbytes < head + 8) {
+    err = "cpu decode: blob shorter than its header";
+    return false;
+  }
+  uint16_t lut[LUTN];
+  memcpy(lut, blob, sizeof lut);
+  std::vector<uint32_t> start((size_t)T * LANES);
+  memcpy(start.data(), blob + sizeof(uint16_t) * LUTN, 4 * start.size());
+  const uint64_t nwords = (nbytes - head) / 4, nbits = 32 * nwords;
+  std::vector<uint32_t> pay(nwords);
+  memcpy(pay.data(), blob + head, 4 * nwords);
+  for (uint32_t s : start)
+    if (s >= nbits) {
+      err = "cpu decode: a lane starts beyond the payload (truncated or corrupt blob)";
+      return false;
+    }
+  std::atomic<int> bad{0};
+  // tiles are split into contiguous ranges, one per thread; a lane writes row 64 tr + l, then row 64 tr + 32 + l
+  auto work = [&](int t0, int t1) {
+    for (int t = t0; t < t1 && !bad.load(std::memory_order_relaxed); ++t) {
+      const int tr = t / KT, tc = t % KT;
+      for (int l = 0; l < LANES; ++l) {
+        LaneBits lb(pay.data(), nwords, start[(size_t)t * LANES + l]);
+        uint64_t used = start[(size_t)t * LANES + l];
+        for (int r = 0; r < 2; ++r) {
+          uint8_t* dst = out + ((size_t)tr * TN + 32 * r + l) * KS + (size_t)tc * TK;
           for (int c = 0; c < TK; ++c) {
-            uint64_t w;
-            memcpy(&w, payload + ((bp >> 5) << 2), 8);
-            const uint16_t e = lut[(w >> (bp & 31)) & (LUTN - 1)];
-            row[c] = (uint8_t)e;
-            bp += e >> 8;
+            const uint16_t e = lut[lb.peek() & (LUTN - 1)];
+            const int len = e >> 8;
+            if (len == 0) {  // only a degenerate table has empty entries; a stream that reaches one is corrupt
+              bad = 1;
+              return;
+            }
+            dst[c] = (uint8_t)e;
+            lb.drop(len);
+            used += len;
           }
+        }
+        if (used > nbits) {
+          bad = 1;
+          return;
         }
       }
     }
   };
   const auto t0 = std::chrono::steady_clock::now();
-  std::vector<std::thread> th;
-  for (int i = 1; i < threads; ++i) th.emplace_back(work, i);
-  work(0);
-  for (auto& x : th) x.join();
-  return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  parallel_for(T, std::max(1, threads), work);
+  const double dt = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  if (bad) {
+    err = "cpu decode: a lane runs past the end of the payload (truncated or corrupt blob)";
+    return false;
+  }
+  if (seconds) *seconds = dt;
+  return true;
 }
 
 }  // namespace lw

@@ -53,9 +53,13 @@ bool build_layout_raw(const uint8_t* blob, size_t len, int N, int KS, int thread
 bool build_layout_il(const uint8_t* data, size_t len, int N, int KS, bool compact, int threads, Layout& L,
                      std::string& err);
 
-// CPU decode of a raw blob to symbols [N, KS] (kernels/llmrt.cu:2513-2541: per-lane scalar LUT decode with a 64-bit
-// window from the lane's absolute start, tiles strided across `threads`). Returns seconds.
-double cpu_decode(const uint8_t* blob, int N, int KS, int threads, uint8_t* out);
+// CPU decode of a raw blob (nbytes long) to symbols [N, KS]: the semantics of the reference's cpu_decode
+// (kernels/llmrt.cu:2513-2541: one table lookup per symbol from each lane's absolute start, lane l of tile t writing
+// row 64 tr + l then row 64 tr + 32 + l). Each lane reads through its own 64-bit bit buffer; tiles are split into
+// contiguous ranges over `threads` threads. The header, every lane start and every lane's end are checked against
+// the blob's size: false (with err) on a truncated or corrupt blob. *seconds = decode time (blob already in memory).
+bool cpu_decode(const uint8_t* blob, size_t nbytes, int N, int KS, int threads, uint8_t* out, double* seconds,
+                std::string& err);
 
 int default_threads();
 

@@ -506,16 +506,20 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
                  hipStream_t s, int m = 1) {
   auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
   std::vector<size_t> off(count);
-  std::map<const void*, int> first;
+  // one quantized copy per distinct (vector, K): owner[i] = true for the matrix whose slot quantizes it
+  std::map<std::pair<const void*, long long>, int> first;
+  std::vector<char> owner(count, 0);
   size_t total = 0;
   for (int i = 0; i < count; ++i) {
     const size_t K = (size_t)ts[i]->K * m;
-    auto it = first.find(X[i]);
-    if (it != first.end() && ts[it->second]->K == ts[i]->K) {
+    const auto key = std::make_pair(X[i], (long long)ts[i]->K);
+    auto it = first.find(key);
+    if (it != first.end()) {
       off[i] = off[it->second];
       continue;
     }
-    first[X[i]] = i;
+    first[key] = i;
+    owner[i] = 1;
     off[i] = total;
     total += al(K) + 2 * al(K / 32 * 4);
   }
@@ -529,7 +533,7 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
     uint8_t* b = M.x8 + off[i];
     x8[i] = X8{reinterpret_cast<const int8_t*>(b), reinterpret_cast<const float*>(b + al(K)),
                reinterpret_cast<const float*>(b + al(K) + al(K / 32 * 4))};
-    if (first[X[i]] != i) continue;
+    if (!owner[i]) continue;
     if (q.n == lw::MAX_GROUP) {
       HIPCHECK(lw::launch_quant_x8_group(q, s));
       q.n = 0;
@@ -1269,9 +1273,13 @@ int rt_test_cpu_decode(void* h, const char* name, int threads, uint8_t* out) {
     g_err = std::string(name ? name : "(null)") + ": not a raw coded tensor";
     return -1;
   }
-  std::vector<uint8_t> blob(t->nbytes + 16, 0);
+  std::vector<uint8_t> blob(t->nbytes, 0);
   if (!pread_all(M->fd, blob.data(), t->nbytes, t->off)) return -1;
-  lw::cpu_decode(blob.data(), (int)t->N, t->KS(), std::max(1, threads), out);
+  std::string err;
+  if (!lw::cpu_decode(blob.data(), blob.size(), (int)t->N, t->KS(), std::max(1, threads), out, nullptr, err)) {
+    g_err = std::string(name) + ": " + err;
+    return -1;
+  }
   return 0;
 }
 
@@ -1283,10 +1291,16 @@ double rt_cpu_decode_all(void* h, int threads, long long* symbols) {
   std::vector<uint8_t> blob, out;
   for (auto& t : M->ts) {
     if (!t.coded() || t.pre_il) continue;
-    blob.assign(t.nbytes + 16, 0);
+    blob.assign(t.nbytes, 0);
     if (!pread_all(M->fd, blob.data(), t.nbytes, t.off)) return -1;
     out.resize((size_t)t.N * t.KS());
-    total += lw::cpu_decode(blob.data(), (int)t.N, t.KS(), std::max(1, threads), out.data());
+    double s = 0;
+    std::string err;
+    if (!lw::cpu_decode(blob.data(), blob.size(), (int)t.N, t.KS(), std::max(1, threads), out.data(), &s, err)) {
+      g_err = t.name + ": " + err;
+      return -1;
+    }
+    total += s;
     nsym += (long long)t.N * t.KS();
   }
   if (symbols) *symbols = nsym;

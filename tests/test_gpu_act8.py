@@ -237,3 +237,29 @@ def test_gpu_act8_rejects_block_kernel_modes(a8_rt, lib, act8):
         with pytest.raises(RuntimeError, match="int8 activations"):
             rc.matmul_dev("Q4_K_small", x, y)
     lib.lw_set_kernel_mode(0)
+
+
+def test_gpu_act8_full_config2_layer(gpu, tmp_path, orc, lib, act8):
+    """Int8 activations on one full config-2 layer (Mistral-shaped Q4_K, H = 2.3) as one grouped m = 1 call, the
+    bench's launch shape: every matrix within 2e-5 of the oracle's int8 GEMV, and q / k / v sharing one x (quantized
+    once) equal to the same matrices called with copies of it."""
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from lazyweights_amd.configs import config2_layer
+    mats = config2_layer(0)
+    bundle.write_synthetic_bundle(str(tmp_path), mats, threads=16)
+    with Runtime(tmp_path) as rt:
+        names = [m[0] for m in mats]
+        shared = torch.randn(1, 4096).half().cuda()
+        xs = [shared if m[0].endswith((".q", ".k", ".v")) else torch.randn(1, m[3]).half().cuda() for m in mats]
+        say("act8 config 2 layer grouped")
+        ys = group(rt, names, xs)
+        copies = group(rt, names[:3], [shared.clone() for _ in range(3)])
+        for a, b in zip(ys[:3], copies):
+            assert np.array_equal(a, b)
+        for mat, x, y in zip(mats, xs, ys):
+            name, kqt, N, K, H, seed = mat
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            q, d, s = orc.quant_x8(x.float().cpu().numpy())
+            check(y, orc.gemv_act8_f64(kqt, codes, side, q, d, s), TOL_ACT8, name + " act8 full layer")
+            del codes, side

@@ -259,6 +259,81 @@ def test_full_config4_q5k_verify(gpu, tmp_path):
     full_size_check(tmp_path, [m for m in CONFIG4 if m[0] in ("q5.gate", "q5.down")], (5,))
 
 
+def grouped_matmul(rt, names, xs, m, ys):
+    """One lw_group_matmul_dev call over `names` (device x / y torch tensors)."""
+    import ctypes
+    n = len(names)
+    rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                    (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), m,
+                                    (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+    assert rc == 0, rt.lib.lw_last_error()
+
+
+def test_full_config1_layer(gpu, tmp_path):
+    """Config 1, the Phi-3-mini-shaped layer (qkv 9216 x 3072, o 3072 x 3072, gate_up 16384 x 3072, down 3072 x 8192,
+    one Huffman table per matrix): decode bit-exact and m = 1 GEMV against fp64 per matrix, then the whole layer as
+    one grouped call (the bench's launch shape) with the same bits as the per-matrix calls."""
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from lazyweights_amd.configs import CONFIG1
+    from oracle import oracle as orc
+    bundle.write_synthetic_bundle(str(tmp_path), CONFIG1, threads=16)
+    with Runtime(tmp_path) as rt:
+        xs, ys, names = [], [], []
+        for mat in CONFIG1:
+            name, kqt, N, K, H, seed = mat
+            say("config 1", name, N, K)
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            assert np.array_equal(rt.test_decode(name), codes)
+            X = torch.randn(1, K, generator=torch.Generator().manual_seed(seed)).half()
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X.double().numpy())
+            Y = torch.zeros(1, N, device="cuda")
+            rt.matmul_dev(name, X.cuda(), Y)
+            torch.cuda.synchronize()
+            check_err(Y.cpu().numpy(), y64, "config 1 %s m=1" % name)
+            names.append(name)
+            xs.append(X.cuda())
+            ys.append(Y)
+            del codes, side
+        yg = [torch.full_like(y, float("nan")) for y in ys]
+        say("config 1 grouped layer")
+        grouped_matmul(rt, names, xs, 1, yg)
+        torch.cuda.synchronize()
+        for nm, a, b in zip(names, yg, ys):
+            assert torch.equal(a, b), nm
+
+
+def test_full_config4_q4k_verify(gpu, tmp_path):
+    """Config 4's Q4_K half: the Mistral-shaped layer (H = 2.3) verified with m = 5 tokens as one grouped call, each
+    matrix against fp64 (the contract) and against five m = 1 calls token by token (fp32 rounding: the m = 5 kernel
+    forms its products on the matrix cores in another order)."""
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from lazyweights_amd.configs import CONFIG4
+    from oracle import oracle as orc
+    mats = [m for m in CONFIG4 if m[0].startswith("q4.")]
+    bundle.write_synthetic_bundle(str(tmp_path), mats, threads=16)
+    with Runtime(tmp_path) as rt:
+        names = [m[0] for m in mats]
+        X = {m[0]: torch.randn(5, m[3], generator=torch.Generator().manual_seed(m[5])).half() for m in mats}
+        y5 = {m[0]: torch.zeros(5, m[2], device="cuda") for m in mats}
+        say("config 4 Q4_K m=5 grouped")
+        grouped_matmul(rt, names, [X[n].cuda() for n in names], 5, [y5[n] for n in names])
+        y1 = {m[0]: torch.zeros(5, m[2], device="cuda") for m in mats}
+        for j in range(5):
+            grouped_matmul(rt, names, [X[n][j:j + 1].cuda() for n in names], 1, [y1[n][j:j + 1] for n in names])
+        torch.cuda.synchronize()
+        for mat in mats:
+            name, kqt, N, K, H, seed = mat
+            a, b = y5[name].cpu().numpy(), y1[name].cpu().numpy()
+            say("config 4", name, "m=5 vs 5 x m=1: %.3g" % (np.abs(a - b).max() / np.abs(b).max()))
+            assert np.abs(a - b).max() <= 2e-6 * np.abs(b).max(), name
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X[name].double().numpy())
+            check_err(a, y64, "config 4 %s m=5" % name)
+            del codes, side
+
+
 def test_gpu_whole_tile_kernel_mode(fmt_rt, orc):
     """The whole-tile kernel (the fallback for matrices without a ring schedule) stays exact too."""
     import torch

@@ -121,6 +121,36 @@ def test_dequant_known_grid(orc):
     assert np.array_equal(w6[0], 0.5 * (codes6[0].astype(np.float32) - 32))
 
 
+def test_dequant_known_answers_q4k_q5k(orc):
+    """Q4_K / Q5_K dequant of one super-block with eight distinct sub-block scales and mins, the 12 scale bytes
+    written out by hand (not by a packer) from get_scale_min_k4's field layout:
+    sc = [1, 2, 3, 4, 17, 34, 51, 63], m = [5, 6, 7, 8, 20, 40, 60, 9], d = 0.5, dmin = 0.25, so w = 0.5 sc_j q - 0.25 m_j
+    on sub-block j (weights 32 j .. 32 j + 31)."""
+    q = [0x41, 0x82, 0xC3, 0xC4,   # sc0..3 in bits 0-5; bits 6-7: high bits of sc4..7 (1, 2, 3, 3)
+         0x45, 0x86, 0xC7, 0x08,   # m0..3 in bits 0-5; bits 6-7: high bits of m4..7 (1, 2, 3, 0)
+         0x41, 0x82, 0xC3, 0x9F]   # low nibble: sc4..7 low 4 bits (1, 2, 3, 15); high nibble: m4..7 low (4, 8, 12, 9)
+    rec = np.concatenate([np.array([0.5, 0.25], np.float16).view(np.uint8), np.array(q, np.uint8)])[None]
+    s, o = orc.sub_scales(1, rec)
+    assert list(s[0]) == [0.5, 1.0, 1.5, 2.0, 8.5, 17.0, 25.5, 31.5]
+    assert list(o[0]) == [1.25, 1.5, 1.75, 2.0, 5.0, 10.0, 15.0, 2.25]
+    k = np.arange(256)
+    for kqt, codes in ((1, (k + k // 32) % 16), (2, (k + 3 * (k // 32)) % 32)):
+        w = orc.dequant(kqt, codes.astype(np.uint8)[None], rec)[0]
+        # a few entries by hand
+        if kqt == 1:
+            assert w[0] == -1.25                    # sub-block 0, q 0: 0 - 0.25 * 5
+            assert w[37] == 1.0 * 6 - 1.5           # sub-block 1, q (37 + 1) % 16 = 6
+            assert w[165] == 17.0 * 10 - 10.0       # sub-block 5, q (165 + 5) % 16 = 10: 160
+            assert w[255] == 31.5 * 6 - 2.25        # sub-block 7, q (255 + 7) % 16 = 6
+        else:
+            assert w[31] == 0.5 * 31 - 1.25         # q 31 at the end of sub-block 0
+            assert w[200] == 25.5 * 26 - 15.0       # sub-block 6, q (200 + 18) % 32 = 26
+            assert w[250] == 31.5 * 15 - 2.25       # sub-block 7, q (250 + 21) % 32 = 15
+        sc = np.array([1, 2, 3, 4, 17, 34, 51, 63], np.float64).repeat(32)
+        m = np.array([5, 6, 7, 8, 20, 40, 60, 9], np.float64).repeat(32)
+        assert np.array_equal(w.astype(np.float64), 0.5 * sc * codes - 0.25 * m)
+
+
 def test_gemv_f64_matches_numpy(orc):
     rng = np.random.default_rng(0)
     w = rng.standard_normal((64, 512)).astype(np.float32)

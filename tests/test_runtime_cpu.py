@@ -212,3 +212,61 @@ def test_open_model_shaped_bundle(lib, tmp_path):
         for name in ("embed", "lnf", "l1.ln2"):
             with pytest.raises(RuntimeError):
                 rt.test_cpu_decode(name, 1)
+
+
+def test_cpu_decode_rejects_truncated_and_corrupt_blobs(lib, tmp_path):
+    """rt_test_cpu_decode / rt_cpu_decode_all read raw blobs that rt_open did not validate (budget_mb = 0: nothing
+    resident). A blob cut inside its lane-start table, one cut inside its payload, and one whose lane starts point
+    past the payload are refused with -1 and an error text, never read past the buffer."""
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer, encode_huf8
+    g = load_golden("huf4p_q4k_128x1024")
+    N, KS = g["sym"].shape
+    blob, _ = encode_huf8(g["sym"])
+    T = (N // 64) * (KS // 256)
+    head = 4096 + 128 * T
+    bad_start = bytearray(blob)
+    bad_start[4096:4100] = np.array([1 << 30], np.uint32).tobytes()   # tile 0, lane 0 starts far past the end
+    cases = {"cut_header": blob[:head - 64], "cut_payload": blob[:head + (len(blob) - head) // 2],
+             "bad_start": bytes(bad_start)}
+    w = Writer(str(tmp_path))
+    for name, b in cases.items():
+        w.add(name, "huf4p", N, 2 * KS, 1.0, 0, b)
+    w.close()
+    with Runtime(tmp_path, budget_mb=0) as rt:
+        out = np.zeros((N, KS), np.uint8)
+        for name in cases:
+            assert rt.lib.rt_test_cpu_decode(rt.h, name.encode(), 2, out.ctypes.data) == -1, name
+            assert "cpu decode" in rt.lib.lw_last_error().decode(), name
+        s, _ = rt.cpu_decode_all(2)
+        assert s == -1
+
+
+def test_writer_and_manifest_round_trip(lib, tmp_path):
+    """Writer (the C++ bundle writer through ctypes) and read_manifest: cfg lines, tensors at 256-byte boundaries in
+    write order, bytes read back as written, and names with white space refused."""
+    from lazyweights_amd import bundle
+    rng = np.random.default_rng(5)
+    blobs = {"a": rng.integers(0, 256, 300, dtype=np.uint8).tobytes(), "b.kqs": b"", "c": b"\x01" * 257}
+    w = bundle.Writer(str(tmp_path))
+    w.cfg("hidden", 512)
+    w.cfg("eps", "1e-05")
+    for i, (name, b) in enumerate(blobs.items()):
+        w.add(name, "raw8", 1 + i, max(1, len(b)), 0.5 * (i + 1), i, b)
+    with pytest.raises(ValueError):
+        w.add("bad name", "raw8", 1, 1, 1.0, 0, b"x")
+    w2 = bundle.Writer(str(tmp_path / "two"))
+    w2.add("x", "raw8", 1, 3, 1.0, 0, b"xyz")
+    w2.close()
+    cfg, ts = bundle.read_manifest(str(tmp_path / "two"))
+    assert cfg == {} and [t["name"] for t in ts] == ["x"] and ts[0]["offset"] == 0 and ts[0]["nbytes"] == 3
+    w.close()
+    cfg, ts = bundle.read_manifest(str(tmp_path))
+    assert cfg == {"hidden": "512", "eps": "1e-05"}
+    assert [t["name"] for t in ts] == list(blobs)
+    prev_end = 0
+    for i, t in enumerate(ts):
+        assert t["offset"] % 256 == 0 and t["offset"] >= prev_end
+        assert (t["N"], t["scale"], t["zp"], t["enc"]) == (1 + i, 0.5 * (i + 1), i, "raw8")
+        assert bundle.read_tensor(str(tmp_path), t).tobytes() == blobs[t["name"]]
+        prev_end = t["offset"] + t["nbytes"]
