@@ -766,13 +766,14 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 }
 
 // ── flat launches (m = 1): shared pieces ─────────────────────────────────────────────────────────────────
-// Reduction in the launch, after a wave stored its tile's 64 partials (agent-scope atomic stores). Ordering, in the
-// HIP memory model: a wave synchronization (__syncwarp: wavefront-scope release fence, wave barrier, acquire fence)
-// puts every lane's store before lane 0's counter increment, which is an agent-scope acquire-release
-// read-modify-write: it publishes the tile's partials, and the wave that counts the row's last tile acquires every
-// earlier tile's partials through the same counter; a second wave synchronization hands that acquire to all its
-// lanes before they load. That wave resets the counter and sums the row's partials in tile-column order (the order of
-// k_reduce_group, so the bits are the same). No-op when the entry has no Y (reduced by a separate launch).
+// Reduction in the launch, after a wave stored its tile's 64 partials (agent-scope atomic stores): it waits for
+// the stores to complete (vmcnt(0)) before lane 0 counts the tile in its tile row with a relaxed agent-scope atomic;
+// the wave that counts the row's last tile resets the counter and sums the row's partials in tile-column order (the
+// order of k_reduce_group, so the bits are the same) with agent-scope atomic loads. This relies on the hardware's
+// completion order (the store acknowledgements precede the increment), not on release / acquire semantics: on
+// gfx950 an agent-scope release is a buffer_wbl2 and an acquire a buffer_inv per wave, which measured 106-143 us per
+// config-2 layer against 45 us. Used only by kernels outside the m = 1 headline path (whose blocks reduce whole tile
+// rows in LDS behind a workgroup barrier). No-op when the entry has no Y (reduced by a separate launch).
 // The sum of tile row tr's partials by the wave that counted the row's last tile (resets the counter).
 template <class KEntryRef>
 __device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
@@ -799,12 +800,11 @@ __device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int 
 template <class KEntryRef>
 __device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
   if (!E.Y) return;
-  __syncwarp();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   uint32_t old = 0;
-  if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __builtin_amdgcn_readlane(old, 0);
   if (old != (uint32_t)(KT - 1)) return;
-  __syncwarp();
   row_sum(E, tr, KT, N, lane, mt);
 }
 
@@ -1663,10 +1663,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   auto finish_pending = [&]() {
     if (pend < 0) return;
     const uint32_t old = (uint32_t)__builtin_amdgcn_readlane((int)pold, 0);
-    if (old == (uint32_t)(pKT - 1)) {
-      __syncwarp();  // lane 0's acquiring increment, handed to every lane (as in row_reduce)
-      row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
-    }
+    if (old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
     pend = -1;
   };
   int n = wave;
@@ -1710,11 +1707,9 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       for (int m = 0; m < XR; ++m) xr[m] = xs[16 * m];
     }
     auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS
-    // the pending tile's partials, published as in row_reduce
-    __syncwarp();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
     if (pend >= 0 && lane == 0)
-      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // register windows: rows r, r + 1 (A, B) of each chain, row r + 2 (C) read after every pair (P = bit
     // position + 64: bits 5+ give the row C holds)
     uint32_t slot[NC], A[NC], B[NC], C[NC];
@@ -1871,9 +1866,9 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     }
   }
   if (pend >= 0) {  // the last tile's reduction
-    __syncwarp();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
-      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_pending();
   }
 }
