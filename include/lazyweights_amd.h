@@ -83,6 +83,16 @@ int lw_tensor_info(void* h, const char* name, int64_t* out);
  * -1. */
 int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy, void* stream);
 
+/* lw_matmul_dev without any device allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The launches' partials,
+ * tile-row counters and (fp32 x) split activations live in a static 16 MiB device array held by every GPU the library
+ * runs on until the process ends; the counters are cleared by a kernel on `stream` at each call. Fused path only:
+ * fp16 X with 1 <= m <= 16 or fp32 X with 1 <= m <= 8, int8 activations off; -1 with an error text when the call
+ * needs more than the 16 MiB (KT * m * N * 4 bytes of partials, 8 with fp32 X, + 4 * N / 64 of counters + 4 m K of
+ * split x). Calls that overlap on one GPU (several streams or threads) race on the array. */
+int lw_matmul_dev_noalloc(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy,
+                          void* stream);
+
 /* Several independent matmuls (e.g. the matrices of one decoder layer), each with its own fp16 activations X[i]
  * [m, K_i] and output Y[i] [m, N_i], launched back to back on `stream`. Returns 0 or -1. */
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,

@@ -32,6 +32,7 @@ SIGNATURES = {
     "lw_last_error": (_cp, []),
     "lw_tensor_info": (_i, [_vp, _cp, _vp]),
     "lw_matmul_dev": (_i, [_vp, _cp, _vp, _i, _i, _vp, _i, _vp]),
+    "lw_matmul_dev_noalloc": (_i, [_vp, _cp, _vp, _i, _i, _vp, _i, _vp]),
     "lw_group_matmul_dev": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp]),
     "lw_bench_groups": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _vp]),
     "lw_stream_read_gbps": (_d, [_ll, _i]),

@@ -168,6 +168,8 @@ hipError_t launch_add_halves(const float* T, float* Y, int m, int nr, int ldy, h
 hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K, hipStream_t s);
 hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row0, int nrows, const void* X16, int m,
                                   float* Y, int ldy, hipStream_t s);
+// p[i] = v for i < n, as a kernel on stream s
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s);
 // streaming read of n16 16-byte words (achievable HBM bandwidth control); out gets one value per block
 hipError_t launch_stream_read(const void* src, size_t n16, float* out, int blocks, hipStream_t s);
 

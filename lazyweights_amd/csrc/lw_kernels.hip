@@ -2721,6 +2721,18 @@ hipError_t launch_split_x_gemm(const float* X, void* XX, void* XL, int m, int K,
 
 // ── HBM streaming-read control ──────────────────────────────────────────────────────────────────────────
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// p[i] = v for i < n (clears counters in caller-owned scratch; a kernel, so that a graph capture records no memset)
+__global__ void __launch_bounds__(256) k_fill_u32(uint32_t* __restrict__ p, size_t n, uint32_t v) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, size_t n, uint32_t v, hipStream_t s) {
+  if (!n) return hipSuccess;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(k_fill_u32, dim3(blocks), dim3(256), 0, s, p, n, v);
+  return hipGetLastError();
+}
+
 __global__ void __launch_bounds__(256) k_stream_read(const u32x4* __restrict__ src, size_t n16, float* __restrict__ out) {
   uint32_t acc = 0;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) {

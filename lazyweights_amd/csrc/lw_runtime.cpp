@@ -20,6 +20,7 @@
 #include <fstream>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -500,6 +501,12 @@ struct X8 {
   const float* s;
 };
 
+// Device scratch owned by the caller of a fused launch (lw_matmul_dev_noalloc): `bytes` at `base`.
+struct FixedScratch {
+  uint8_t* base;
+  size_t bytes;
+};
+
 // Quantize the activations of each of `count` matrices (m tokens [m][K_i], fp16 or fp32; a vector shared by several
 // matrices once) into the model's x8 scratch; x8[i] = matrix i's quantized x ([m][K_i] int8, [m][K_i / 32] scales).
 int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, std::vector<X8>& x8,
@@ -583,14 +590,33 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
 // `launches` (optional) counts the kernel launches. x8 (flat kernels only; m = 1, or up to 8 tokens in one pass with
 // kernel modes 0, 3-5 and no packed matrix): int8 activations (quant_x8_dev) instead of X16.
 int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int count, int m, int per, float* const* Y,
-                    const int* ldy, hipStream_t s, int* launches = nullptr, const X8* x8 = nullptr) {
+                    const int* ldy, hipStream_t s, int* launches = nullptr, const X8* x8 = nullptr,
+                    const FixedScratch* fixed = nullptr) {
   const int mt = m * per;
   std::vector<size_t> off(count + 1, 0);
   for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
-  if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
   std::vector<size_t> coff(count + 1, 0);  // tile-row counters per entry (in-launch reduction)
   for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + (size_t)ts[i]->dm.NT;
-  if (grow_zeroed(M.cnt, M.cnt_cap, coff[count] * sizeof(uint32_t))) return -1;
+  // partials and counters: the model's (grown on demand) or a caller's fixed scratch (nothing allocated; its counters
+  // are cleared by a fill kernel on the stream, since the last call on that scratch may have left anything there)
+  float* Pb = nullptr;
+  uint32_t* Cb = nullptr;
+  if (fixed) {
+    const size_t cnt_bytes = (coff[count] * sizeof(uint32_t) + 255) & ~(size_t)255;
+    if (cnt_bytes + off[count] * sizeof(float) > fixed->bytes) {
+      g_err = "scratch of " + std::to_string(fixed->bytes) + " bytes is too small: this call needs " +
+              std::to_string(cnt_bytes + off[count] * sizeof(float));
+      return -1;
+    }
+    Cb = reinterpret_cast<uint32_t*>(fixed->base);
+    Pb = reinterpret_cast<float*>(fixed->base + cnt_bytes);
+    HIPCHECK(lw::launch_fill_u32(Cb, coff[count], 0u, s));
+  } else {
+    if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
+    if (grow_zeroed(M.cnt, M.cnt_cap, coff[count] * sizeof(uint32_t))) return -1;
+    Pb = M.P;
+    Cb = M.cnt;
+  }
   std::vector<char> reduced(count, 0);  // entries whose reduction runs inside their flat launch
   lw::GroupPlan plan{};
   plan.mt = mt;
@@ -646,11 +672,11 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
       set8(fp, e, j);
-      e.P = M.P + off[j];
+      e.P = Pb + off[j];
       e.tile0 = fp.ntiles;
       e.ntile = dm.NT * dm.KT;
       e.Y = Y[j];
-      e.cnt = M.cnt + coff[j];
+      e.cnt = Cb + coff[j];
       fp.ntiles += e.ntile;
       mintiles = std::min(mintiles, e.ntile);
       reduced[j] = 1;
@@ -670,7 +696,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       lw::GroupEntry& e = pp.e[pp.n++];
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
-      e.P = M.P + off[j];
+      e.P = Pb + off[j];
       e.block0 = pp.blocks;
       pp.blocks += dm.KT * ((dm.NT + 15) / 16);
       done[j] = 1;
@@ -692,7 +718,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
       set8(fp, e, j);
-      e.P = M.P + off[j];
+      e.P = Pb + off[j];
       e.list = nullptr;
       e.tile0 = total;
       e.ntile = dm.NT * dm.KT;
@@ -708,7 +734,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       if (fp.W > 0) {
         for (int k = 0; k < fp.n; ++k) {
           fp.e[k].Y = Y[sel[k]];
-          fp.e[k].cnt = M.cnt + coff[sel[k]];
+          fp.e[k].cnt = Cb + coff[sel[k]];
           reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
         }
         tile_plans.emplace_back(fp, rounds);
@@ -725,7 +751,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     if (split) {  // every tile of these matrices, exceptions included; the reduction in the launch
       for (int k = 0; k < fp.n; ++k) {
         fp.e[k].Y = Y[sel[k]];
-        fp.e[k].cnt = M.cnt + coff[sel[k]];
+        fp.e[k].cnt = Cb + coff[sel[k]];
         reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
       }
       split_plans.push_back(fp);
@@ -757,7 +783,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       const lw::DevMat& dm = ts[j]->dm;
       if (dm.nexc && !(exc_in[j] && dm.nexc == dm.nexc32)) continue;
       fp.e[k].Y = Y[j];
-      fp.e[k].cnt = M.cnt + coff[j];
+      fp.e[k].cnt = Cb + coff[j];
       reduced[j] = 1;
     }
     flat_plans.push_back(fp);
@@ -779,7 +805,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         e.M.ring_rows = 32;  // these tiles' schedules are for a 32-row ring
         e.X2 = static_cast<const uint32_t*>(X16[j]);
         set8(fp, e, j);
-        e.P = M.P + off[j];
+        e.P = Pb + off[j];
         e.list = dm.exc;
         e.tile0 = fp.ntiles;
         e.ntile = dm.nexc32;
@@ -805,12 +831,12 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         e.M = dm;
         e.X2 = static_cast<const uint32_t*>(X16[i]);
         set8(fp, e, i);
-        e.P = M.P + off[i];
+        e.P = Pb + off[i];
         e.list = rest.exc;
         e.ntile = fp.ntiles = rest.nexc;
         HIPCHECK(lw::launch_fused_split(fp, s));
       } else {
-        HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, M.P + off[i], s));
+        HIPCHECK(lw::launch_fused_exceptions(rest, X16[i], mt, Pb + off[i], s));
       }
       if (launches) ++*launches;
     }
@@ -831,7 +857,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
     if (!ring_ok || di.ring_rows == 0) {
-      HIPCHECK(lw::launch_fused(di, X16[i], mt, M.P + off[i], s));
+      HIPCHECK(lw::launch_fused(di, X16[i], mt, Pb + off[i], s));
       if (launches) ++*launches;
       done[i] = 1;
       continue;
@@ -843,7 +869,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       lw::GroupEntry& e = plan.e[plan.n++];
       e.M = dm;
       e.X2 = static_cast<const uint32_t*>(X16[j]);
-      e.P = M.P + off[j];
+      e.P = Pb + off[j];
       e.block0 = plan.blocks;
       const int wpb = lw::group_waves_per_block(dm.ring_rows);
       plan.blocks += dm.KT * ((dm.NT + wpb - 1) / wpb);
@@ -858,7 +884,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   for (int i = 0; i < count; ++i) {
     if (reduced[i]) continue;
     lw::ReduceEntry& e = rp.e[rp.n++];
-    e.P = M.P + off[i];
+    e.P = Pb + off[i];
     e.Y = Y[i];
     e.N = (int)ts[i]->N;
     e.KT = ts[i]->dm.KT;
@@ -1029,6 +1055,36 @@ int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ld
   return 0;
 }
 
+// ── caller-allocation-free matmul: one static scratch array per device ──────────────────────────────────────
+// lw_matmul_dev_noalloc keeps the partials, tile-row counters and split activations of its launches in `scratch`,
+// which every GPU the library runs on holds from module load until the process ends. Host code never passes the
+// array's name to a kernel (that is a host-side stand-in, not a device address): each device's copy is found once
+// with hipGetSymbolAddress, with that device current (scratch_on_device, first called from rt_open), and only that
+// address is used.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+std::map<int, uint8_t*> g_scratch_addr;  // device -> address of its copy of `scratch`
+
+uint8_t* scratch_on_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    g_err = "no current HIP device";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  const auto it = g_scratch_addr.find(dev);
+  if (it != g_scratch_addr.end()) return it->second;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    g_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+    return nullptr;
+  }
+  g_scratch_addr[dev] = static_cast<uint8_t*>(p);
+  return static_cast<uint8_t*>(p);
+}
+
 }  // namespace
 
 // ── C-ABI ────────────────────────────────────────────────────────────────────────────────────────────────
@@ -1080,6 +1136,12 @@ void* rt_open(const char* dir, int max_ctx, int max_batch, long long budget_mb, 
       return nullptr;
     }
     M->gpu = true;
+    // the no-allocation entry point's scratch on this device (its address, found once per device)
+    if (!scratch_on_device()) {
+      fail("rt_open: " + g_err);
+      release(M.release());
+      return nullptr;
+    }
     const int threads = lw::default_threads();
     const long long floor_kb = (long long)floor_mb * 1024;
     size_t used = 0;
@@ -1391,6 +1453,47 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
   if (grow(M->X16, M->X16_cap, (size_t)2 * m * t->K * 2)) return -1;
   HIPCHECK(lw::launch_split_x(static_cast<const float*>(X), M->X16, m, (int)t->K, s));
   return fused_dev(*M, *t, M->X16, m, 2, Y, ldy, s);
+}
+
+int lw_matmul_dev_noalloc(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy,
+                          void* stream) {
+  Model* M = static_cast<Model*>(h);
+  if (!M || !X || !Y) {
+    g_err = "lw_matmul_dev_noalloc: bad arguments";
+    return -1;
+  }
+  Tensor* t = M->find(name);
+  if (check_matmul(t, name)) return -1;
+  if (g_act8) {
+    g_err = "lw_matmul_dev_noalloc: int8 activations are not supported (lw_set_act8(0) first)";
+    return -1;
+  }
+  if (x_f16 ? (m < 1 || m > 16) : (m < 1 || m > 8)) {
+    g_err = "lw_matmul_dev_noalloc: needs 1 <= m <= 16 with fp16 activations, 1 <= m <= 8 with fp32";
+    return -1;
+  }
+  uint8_t* base = scratch_on_device();
+  if (!base) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  FixedScratch fx{base, kNoAllocScratchBytes};
+  const void* X16 = X;
+  int per = 1;
+  if (!x_f16) {  // fp32 x split into fp16 hi + lo rows, at the end of the scratch
+    const size_t xb = ((size_t)2 * m * t->K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    if (xb >= fx.bytes) {
+      g_err = "lw_matmul_dev_noalloc: activations exceed the " + std::to_string(kNoAllocScratchBytes) +
+              "-byte scratch";
+      return -1;
+    }
+    fx.bytes -= xb;
+    void* x16 = base + fx.bytes;
+    HIPCHECK(lw::launch_split_x(static_cast<const float*>(X), x16, m, (int)t->K, s));
+    X16 = x16;
+    per = 2;
+  }
+  const int rc = fused_group_dev(*M, &t, &X16, 1, m, per, &Y, &ldy, s, nullptr, nullptr, &fx);
+  if (rc) g_err = "lw_matmul_dev_noalloc: " + g_err;
+  return rc;
 }
 
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
