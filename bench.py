@@ -313,12 +313,14 @@ def main():
             del XV, YV
 
         # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
-        # matrices, with the default GEMM (rocBLAS over fp16 hi + lo weights) and with the hand-written matrix-core
-        # GEMM over the codes (a reported figure, not the metric)
+        # matrices, with the default GEMM (the hand-written matrix-core GEMM over the codes, k_gemm_prefill) and with
+        # rocBLAS over fp16 hi + lo weights (a reported figure, not the metric)
         prefill = None
         if not a.no_prefill:
-            prefill = {"path": "decode + dequant to fp16 hi + lo weights, rocBLAS fp16 GEMM with fp32 accumulation "
-                               "(one GEMM over 2m columns up to m = 512)", "runs": []}
+            prefill = {"path": "own_mfma (default): codes decoded to scratch, scaled to exact fp16 weights, "
+                               "v_mfma_f32_32x32x16_f16 with fp16 hi + lo x and fp32 accumulation; rocblas: codes "
+                               "dequantized to fp16 hi + lo weights, rocBLAS fp16 GEMM (one GEMM over 2m columns up "
+                               "to m = 512)", "runs": []}
             for pm in (128, 512):
                 XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
                 YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
@@ -330,9 +332,7 @@ def main():
                             raise RuntimeError(lib.lw_last_error().decode())
                 flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos[:7])
                 run = {"m": pm}
-                for which, key in ((0, "rocblas"), (1, "own_mfma")):
-                    if which == 1 and pm > 128:
-                        continue
+                for which, key in ((0, "own_mfma"), (4, "rocblas")):
                     lib.lw_set_prefill_gemm(which)
                     prefill_layer()
                     torch.cuda.synchronize()

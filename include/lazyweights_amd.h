@@ -107,13 +107,15 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * exception tiles) for every m = 1 launch. Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
-/* The GEMM of the decode-to-scratch path (path 2: m > 8, or rt_test_matmul path 2), for all handles. The
- * reference dequantizes to fp32 and runs its own fp32 GEMM (kernels/llmrt.cu:201-343, 1826-1841). 0 (default) =
- * the decoded weights w = s f(q) - o split into fp16 hi + lo, x likewise, two rocBLAS fp16 GEMMs with fp32
- * accumulation (x_hi w_hi + x_hi w_lo, then + x_lo w_hi; up to 512 tokens as one GEMM over 2m columns, [x_hi | x_hi]
- * and [x_lo | 0], whose halves are summed); 1 = the hand-written matrix-core GEMM over the codes and side bytes
- * (fp16 hi + lo x); 2 / 3 = as 0 but always the two-GEMM / the one-GEMM form. Kernel mode 1 overrides all with the
- * SIMT GEMM. Returns 0 or -1. */
+/* Prefill GEMM (path 2, and fp32 X with m > 8) for every handle. The reference dequantizes to fp32 and runs its own
+ * fp32 GEMM (kernels/llmrt.cu:201-343, 1826-1841). 0 (default) = the hand-written matrix-core GEMM for Q4_K / Q5_K
+ * (codes decoded to a device scratch, each scaled by its 6-bit sub-block scale into an exact fp16 weight, x split into
+ * fp16 hi + lo, v_mfma_f32_32x32x16_f16 with fp32 accumulation, super-block scales and mins applied in registers) and
+ * rocBLAS for Q6_K / IQ4_XS; 1 = hand-written for every format (Q6_K / IQ4_XS through a per-sub-block-scaled MFMA
+ * GEMM); 2 / 3 = rocBLAS always, over the decoded weights w = s f(q) - o split into fp16 hi + lo (two fp16 GEMMs with
+ * fp32 accumulation, x_hi w_hi + x_hi w_lo, then + x_lo w_hi / one GEMM over 2m columns [x_hi | x_hi] and [x_lo | 0]);
+ * 4 = rocBLAS with the one-GEMM form up to 512 tokens. Kernel mode 1 overrides all with the SIMT GEMM. Returns 0 or
+ * -1. */
 int lw_set_prefill_gemm(int which);
 
 /* Int8 activations for 1 <= m <= 8 (on = 1; default 0 = fp16 hi + lo activations): rt_test_matmul, lw_matmul_dev

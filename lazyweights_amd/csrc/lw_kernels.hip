@@ -2224,7 +2224,7 @@ __global__ void __launch_bounds__(256) k_decode(DevMat M, uint8_t* __restrict__ 
 
 // codes of a packed matrix for tile rows [tr0, tr1): one thread per 16-symbol chunk (pk4: two codes per symbol,
 // low nibble first; pk8: one), rows relative to tr0
-template <int SYMB>
+template <int SYMB, bool TILED>
 __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // chunk within the row range
   const size_t n = (size_t)(tr1 - tr0) * M.KT * 16 * 64;
@@ -2234,6 +2234,27 @@ __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ 
   const int tc = (int)(tt % M.KT), trr = (int)(tt / M.KT);
   const uint4 c = reinterpret_cast<const uint4*>(M.words)[((size_t)(tr0 + trr) * M.KT + tc) * 1024 + (size_t)(g * 64 + L)];
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  if (TILED) {  // the prefill GEMM's layout (launch_decode_tiled): 16 codes per 16-byte piece
+    const int row = trr * TN + L, KC = M.K / 32;
+    uint8_t* o = out + ((size_t)(row >> 5) * KC * 64 + (row & 31)) * 16;
+    if (SYMB == 4) {  // 32 codes = one chunk: symbols 0..7 -> piece h = 0, 8..15 -> h = 1
+      const size_t kc = (size_t)(tc * TK + 16 * g) / 16;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t sy = (w[2 * hh + (q >> 1)] >> (16 * (q & 1))) & 0xFFFFu;
+          v[q] = (sy & 15u) | ((sy >> 4) & 15u) << 8 | ((sy >> 8) & 15u) << 16 | (sy >> 12) << 24;
+        }
+        *reinterpret_cast<uint4*>(o + (kc * 64 + 32 * hh) * 16) = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+    } else {  // 16 codes = half a chunk
+      const int k = tc * TK + 16 * g;
+      *reinterpret_cast<uint4*>(o + ((size_t)(k >> 5) * 64 + 32 * ((k >> 4) & 1)) * 16) = c;
+    }
+    return;
+  }
   uint8_t* o = out + (size_t)(trr * TN + L) * M.K + (size_t)(tc * TK + 16 * g) * (SYMB == 4 ? 2 : 1);
 #pragma unroll
   for (int b = 0; b < 16; ++b) {
@@ -2253,7 +2274,7 @@ __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ 
 // LUT. Each wave collects its 64 rows x CW code bytes in LDS (rows 136 B apart: 8-byte aligned, 2-way bank
 // conflicts at most) and then stores them row by row, whole 64- or 128-byte segments, so the rows' lines are written
 // at once instead of 4 bytes per row and store.
-template <int SYMB>
+template <int SYMB, bool TILED>
 __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1,
                                                       int stage_rows) {
   constexpr int CW = SYMB == 4 ? 128 : 64;  // code bytes per row and wave
@@ -2313,6 +2334,20 @@ __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restr
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (TILED) {  // the prefill GEMM's layout: per 32-row tile and 32-code chunk one 1 KB piece, lane-linear
+    const int KC = K / 32, kc0 = (tc * (SYMB == 4 ? 2 * TK : TK) + wave * CW) / 32;
+#pragma unroll
+    for (int f2 = 0; f2 < 2; ++f2) {
+      const size_t rt = (size_t)(tr - tr0) * 2 + f2;
+#pragma unroll
+      for (int cc = 0; cc < CW / 32; ++cc) {
+        const uint8_t* src = wbuf + (f2 * 32 + l) * RSTR + cc * 32 + 16 * f;  // row c = l, half h = f
+        const uint2 a = *reinterpret_cast<const uint2*>(src), b = *reinterpret_cast<const uint2*>(src + 8);
+        *reinterpret_cast<uint4*>(out + ((rt * KC + kc0 + cc) * 64 + lane) * 16) = make_uint4(a.x, a.y, b.x, b.y);
+      }
+    }
+    return;
+  }
   // the wave's 64 rows: 8-byte pieces, CW / 8 lanes per row
   constexpr int LPR = CW / 8, RPI = 64 / LPR;  // lanes per row, rows per store instruction
   const int pr = lane / LPR, pc = lane % LPR;
@@ -2324,26 +2359,40 @@ __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restr
   }
 }
 
-hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
+template <bool TILED>
+static hipError_t decode_fast(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
   if (M.packed) {
     const size_t n = (size_t)(tr1 - tr0) * M.KT * 16 * 64;
     if (!n) return hipSuccess;
-    if (M.symbits == 4) hipLaunchKernelGGL(k_unpack<4>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
-    else hipLaunchKernelGGL(k_unpack<8>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
+    if (M.symbits == 4) hipLaunchKernelGGL((k_unpack<4, TILED>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
+    else hipLaunchKernelGGL((k_unpack<8, TILED>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, out, tr0, tr1);
     return hipGetLastError();
   }
-  if (M.split && M.rows && M.lut && tr0 < tr1 && M.max_rows + 2 <= 256) {  // the 8-chain kernel
-    const int rows = M.max_rows + 2;
-    const size_t sm = (size_t)rows * 128;
-    const void* f = M.symbits == 4 ? reinterpret_cast<const void*>(&k_decode_split<4>)
-                                   : reinterpret_cast<const void*>(&k_decode_split<8>);
-    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
-    if (e != hipSuccess) return e;
-    const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
-    if (M.symbits == 4) hipLaunchKernelGGL(k_decode_split<4>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
-    else hipLaunchKernelGGL(k_decode_split<8>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
-    return hipGetLastError();
-  }
+  if (tr0 >= tr1) return hipSuccess;
+  const int rows = M.max_rows + 2;
+  const size_t sm = (size_t)rows * 128;
+  const void* f = M.symbits == 4 ? reinterpret_cast<const void*>(&k_decode_split<4, TILED>)
+                                 : reinterpret_cast<const void*>(&k_decode_split<8, TILED>);
+  hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
+  if (M.symbits == 4) hipLaunchKernelGGL((k_decode_split<4, TILED>), grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  else hipLaunchKernelGGL((k_decode_split<8, TILED>), grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  return hipGetLastError();
+}
+
+bool decode_tiled_ok(const DevMat& M) {
+  return M.K % 32 == 0 && (M.packed || (M.split && M.rows && M.lut && M.max_rows + 2 <= 256));
+}
+
+hipError_t launch_decode_tiled(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
+  if (!decode_tiled_ok(M)) return hipErrorNotSupported;
+  return decode_fast<true>(M, out, tr0, tr1, s);
+}
+
+hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
+  if (M.packed || (M.split && M.rows && M.lut && M.max_rows + 2 <= 256))  // the unpack / 8-chain kernels
+    return decode_fast<false>(M, out, tr0, tr1, s);
   const size_t smem = (size_t)LUTN * 8 + (size_t)4 * 32 * (M.max_rows + 1) * 4;
   const int tiles = (tr1 - tr0) * M.KT, blocks = (tiles + 3) / 4;
   if (blocks <= 0) return hipSuccess;
@@ -2485,6 +2534,220 @@ hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row
     case KQ_Q5_K: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_Q5_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
     case KQ_Q6_K: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_Q6_K>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
     case KQ_IQ4_XS: hipLaunchKernelGGL(k_gemm_codes_mfma<KQ_IQ4_XS>, grid, dim3(256), 0, s, M, codes, row0, nrows, x, m, Y, ldy); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ── prefill GEMM on the matrix cores, Q4_K / Q5_K (path 2 and m > 8, the default for these formats) ─────────
+// Y[t][n] = sum over super-blocks of d_n (x_t . w'_n) - dmin_n (Sx_t . m_n), where w'_k = sc_j f(q_k) is the code
+// scaled by its sub-block's 6-bit scale (at most 63 x 31 = 1953: an exact fp16 integer), Sx_t,j the sum of x_t over
+// sub-block j and m_n,j the sub-block's 6-bit min. Both dot products run on v_mfma_f32_32x32x16_f16 with x split into
+// fp16 hi + lo (two products per weight, exact in fp32), the mins term as one K = 16 product per super-block (8
+// sub-blocks, zero-padded) with Sx split likewise; fp32 accumulation, d and dmin applied once per super-block.
+// Operand layout (32x32x16): lane l holds A[i = l % 32][k = 8 (l / 32) + 0..7] (token i) and B[k = 8 (l / 32) + 0..7]
+// [j = l % 32] (weight row j), and receives D[i = 8 (r / 4) + 4 (l / 32) + r % 4][j = l % 32] in register r: a lane owns
+// one weight row (one set of scales) and 16 tokens of each 32-token tile.
+// Block = GEMM_WAVES waves over one tile of 32 weight rows x 64 tokens (two token tiles); the waves split K by
+// super-block (wave w takes super-blocks w, w + GEMM_WAVES, ...) and their partial tiles are summed through LDS in
+// wave order, so the result does not depend on timing. A skinny prefill (m = 128, N = 4096) still gives 256 blocks.
+constexpr int GEMM_WAVES = 8;
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+// codes q0..q3 (bytes of qw) scaled by sc (fp16 pair of the sub-block scale) -> 4 fp16 weights in two words: each
+// pair of bytes becomes fp16(1024 + q) by a byte permute against 0x64 bytes, then (v - 1024) * sc, exact
+__device__ __forceinline__ uint2 scaled_codes(uint32_t qw, h2v sc) {
+  const h2v bias = {(_Float16)-1024.f, (_Float16)-1024.f};
+  const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04010400u));
+  const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04030402u));
+  return make_uint2(__builtin_bit_cast(uint32_t, (h2v)((a + bias) * sc)),
+                    __builtin_bit_cast(uint32_t, (h2v)((b + bias) * sc)));
+}
+
+// Layouts (all lane-linear: one wave's load of a piece is one contiguous 1 KB read):
+//   codes CT: per 32-row tile rt and 32-code chunk kc (the weights of one sub-block) a 1 KB piece at
+//     (rt KC + kc) 1024, lane (h, c) = 32 h + c holding row c's codes 16 h .. 16 h + 15 of the chunk;
+//   x XT: per 32-token tile tt, chunk kc, half (hi / lo) and step s a 1 KB piece at (((tt KC + kc) 2 + half) 2 + s)
+//     1024, lane (h, c) holding x[token c][32 kc + 16 h + 8 s + 0..7] as fp16;
+//   SXT: per token tile tt, super-block sb and half a 512-byte piece, lane c (< 32) holding Sx[token c][8 sb + 0..7].
+// Step s of chunk kc gives lane (h, c) the weights 32 kc + 16 h + 8 s + 0..7 in both operands: the products of the
+// 32 weights of the chunk are all taken once, in a different order than k, which a dot product does not see.
+template <int KQ>
+__global__ void __launch_bounds__(64 * GEMM_WAVES) k_gemm_prefill(DevMat M, const uint8_t* __restrict__ CT, int row0,
+                                                               const uint16_t* __restrict__ XT,
+                                                               const uint16_t* __restrict__ SXT, int m,
+                                                               float* __restrict__ Y, int ldy) {
+  static_assert(KQ == KQ_Q4_K || KQ == KQ_Q5_K, "scaled weights are exact in fp16 for Q4_K / Q5_K only");
+  constexpr int SB = kq_sbytes(KQ), NSB = kq_symbits(KQ) == 4 ? 2 : 1;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int rt = blockIdx.x, tp = blockIdx.y;            // 32-row tile of the chunk, pair of 32-token tiles
+  const int K = M.K, KC = K / 32, NB = K / 256;
+  const int n = rt * 32 + c;                             // the lane's weight row within the chunk
+  const uint8_t* cw = CT + (size_t)rt * KC * 1024 + lane * 16;
+  const uint16_t* xw0 = XT + (size_t)(2 * tp) * KC * 2048 + lane * 8;
+  const uint16_t* xw1 = xw0 + (size_t)KC * 2048;
+  const uint16_t* sw0 = SXT + (size_t)(2 * tp) * NB * 512 + c * 8;
+  const uint16_t* sw1 = sw0 + (size_t)NB * 512;
+  struct Ops {  // one chunk: the lane's 16 codes and its 4 x pieces (half, step) of each token tile
+    uint4 q, x0[4], x1[4];
+  };
+  auto load = [&](int kc) {
+    Ops o;
+    o.q = *reinterpret_cast<const uint4*>(cw + (size_t)kc * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o.x0[i] = *reinterpret_cast<const uint4*>(xw0 + (size_t)kc * 2048 + i * 512);
+      o.x1[i] = *reinterpret_cast<const uint4*>(xw1 + (size_t)kc * 2048 + i * 512);
+    }
+    return o;
+  };
+  f16x16 tot0 = {}, tot1 = {};
+  uint32_t swn[5] = {};
+  Ops cur = {};
+  if (wave < NB) {
+    side_load<KQ>(M.side + side_record(row0 + n, wave, M.KT, NSB) * SB, swn);
+    cur = load(wave * 8);
+  }
+  for (int sb = wave; sb < NB; sb += GEMM_WAVES) {
+    uint32_t sw[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) sw[i] = swn[i];
+    const int nsb = sb + GEMM_WAVES;
+    if (nsb < NB) side_load<KQ>(M.side + side_record(row0 + n, nsb, M.KT, NSB) * SB, swn);
+    // Sx of this super-block (lanes h = 0; k 8..15 of the mins product stay zero)
+    uint4 s0h = {}, s0l = {}, s1h = {}, s1l = {};
+    if (h == 0) {
+      s0h = *reinterpret_cast<const uint4*>(sw0 + (size_t)sb * 512);
+      s0l = *reinterpret_cast<const uint4*>(sw0 + (size_t)sb * 512 + 256);
+      s1h = *reinterpret_cast<const uint4*>(sw1 + (size_t)sb * 512);
+      s1l = *reinterpret_cast<const uint4*>(sw1 + (size_t)sb * 512 + 256);
+    }
+    uint64_t scq, scq2;
+    float dA, dB;
+    side_packed<KQ>(sw, scq, scq2, dA, dB);
+    f16x16 d10 = {}, d11 = {};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // the super-block's 8 chunks (sub-blocks), the next chunk's loads one ahead
+      Ops nxt = {};
+      if (j < 7) nxt = load(sb * 8 + j + 1);
+      else if (nsb < NB) nxt = load(nsb * 8);
+      const _Float16 scf = (_Float16)(float)(uint32_t)((scq >> (8 * j)) & 255u);
+      const h2v sc = {scf, scf};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const uint2 wa = scaled_codes(st ? cur.q.z : cur.q.x, sc), wb = scaled_codes(st ? cur.q.w : cur.q.y, sc);
+        const h8v b = __builtin_bit_cast(h8v, make_uint4(wa.x, wa.y, wb.x, wb.y));
+        d10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x0[st]), b, d10, 0, 0, 0);
+        d10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x0[2 + st]), b, d10, 0, 0, 0);
+        d11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x1[st]), b, d11, 0, 0, 0);
+        d11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x1[2 + st]), b, d11, 0, 0, 0);
+      }
+      cur = nxt;
+    }
+    // mins: A2 = the tokens' Sx over the super-block's 8 sub-blocks, B2 = the row's 8 mins
+    float mf[8];
+    side_mins(sw, mf);
+    h8v b2 = {};
+    if (h == 0)
+      b2 = h8v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3],
+               (_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
+    f16x16 d20 = {}, d21 = {};
+    d20 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s0h), b2, d20, 0, 0, 0);
+    d20 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s0l), b2, d20, 0, 0, 0);
+    d21 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s1h), b2, d21, 0, 0, 0);
+    d21 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s1l), b2, d21, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      tot0[r] = fmaf(dA, d10[r], fmaf(-dB, d20[r], tot0[r]));
+      tot1[r] = fmaf(dA, d11[r], fmaf(-dB, d21[r], tot1[r]));
+    }
+  }
+  // partial tiles -> LDS as part[wave][tile][r][lane] (lane-contiguous, no bank conflicts), then each thread sums
+  // its outputs over the waves in order; consecutive threads take consecutive lanes = consecutive weight rows
+  __shared__ float part[GEMM_WAVES][2][16][64];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    part[wave][0][r][lane] = tot0[r];
+    part[wave][1][r][lane] = tot1[r];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 2 * 16 * 64; e += 64 * GEMM_WAVES) {
+    const int tile = e >> 10, r = (e >> 6) & 15, l = e & 63;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < GEMM_WAVES; ++w) acc += part[w][tile][r][l];
+    const int t = tp * 64 + 32 * tile + 8 * (r / 4) + 4 * (l >> 5) + (r % 4);
+    if (t < m) Y[(size_t)t * ldy + row0 + rt * 32 + (l & 31)] = acc;
+  }
+}
+
+// x of the prefill GEMM: fp32 X [m][K] -> XT (fp16 hi = fp16(x), lo = fp16(x - hi)) and SXT (per sub-block of 32
+// weights s = ((a0 + a1) + (a2 + a3)), a_i the in-order fp32 sum of its i-th 8 values, as fp16 hi / lo), tokens
+// padded with zeros to a multiple of 64. One thread per token and 8 consecutive weights; the 4 threads of a chunk are
+// consecutive lanes.
+__global__ void __launch_bounds__(256) k_prefill_x(const float* __restrict__ X, uint16_t* __restrict__ XT,
+                                                   uint16_t* __restrict__ SXT, int m, int K) {
+  const int G = K / 8, KC = K / 32, NB = K / 256;
+  const int i = (int)blockIdx.x * 256 + threadIdx.x;
+  const int t = i / G, g = i - t * G;                    // the grid covers the padded tokens exactly
+  float v[8];
+  if (t < m) {
+    const float4 a = *reinterpret_cast<const float4*>(X + (size_t)t * K + 8 * g);
+    const float4 b = *reinterpret_cast<const float4*>(X + (size_t)t * K + 8 * g + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  }
+  uint32_t hw[4], lw[4];
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const _Float16 h0 = (_Float16)v[e], h1 = (_Float16)v[e + 1];
+    const _Float16 l0 = (_Float16)(v[e] - (float)h0), l1 = (_Float16)(v[e + 1] - (float)h1);
+    hw[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+    lw[e / 2] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+    sum += v[e];
+    sum += v[e + 1];
+  }
+  const int tt = t >> 5, c = t & 31, kc = g >> 2, hh = (g >> 1) & 1, st = g & 1;
+  const size_t piece = ((size_t)tt * KC + kc) * 2;
+  uint4* o = reinterpret_cast<uint4*>(XT) + (piece * 2 + st) * 64 + 32 * hh + c;
+  o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  o[2 * 64] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  const float s01 = sum + __shfl_xor(sum, 1);
+  const float s = s01 + __shfl_xor(s01, 2);
+  if ((g & 3) == 0) {
+    const _Float16 hi = (_Float16)s;
+    const int sb = kc >> 3, j = kc & 7;
+    uint16_t* q = SXT + (((size_t)tt * NB + sb) * 2 * 32 + c) * 8 + j;
+    q[0] = __builtin_bit_cast(uint16_t, hi);
+    q[32 * 8] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hi));
+  }
+}
+
+hipError_t launch_prefill_x(const float* X, void* XT, void* SXT, int m, int K, hipStream_t s) {
+  if (m < 1 || K % 256) return hipErrorInvalidValue;
+  const int mp = (m + 63) / 64 * 64;
+  const size_t n = (size_t)mp * (K / 8);                 // a multiple of 256 (mp and K / 8 multiples of 32)
+  hipLaunchKernelGGL(k_prefill_x, dim3((unsigned)(n / 256)), dim3(256), 0, s, X, static_cast<uint16_t*>(XT),
+                     static_cast<uint16_t*>(SXT), m, K);
+  return hipGetLastError();
+}
+
+size_t prefill_x_bytes(int m, int K) { return (size_t)((m + 63) / 64 * 64) * K * 4; }
+size_t prefill_sx_bytes(int m, int K) { return (size_t)((m + 63) / 64 * 64) * (K / 32) * 4; }
+
+hipError_t launch_gemm_prefill(const DevMat& M, const uint8_t* CT, int row0, int nrows, const void* XT,
+                               const void* SXT, int m, float* Y, int ldy, hipStream_t s) {
+  if (nrows < 1 || m < 1 || nrows % 32 || M.K % 256) return hipErrorInvalidValue;
+  const dim3 grid(nrows / 32, (m + 63) / 64), block(64 * GEMM_WAVES);
+  const uint16_t* x = static_cast<const uint16_t*>(XT);
+  const uint16_t* sx = static_cast<const uint16_t*>(SXT);
+  switch (M.kqt) {
+    case KQ_Q4_K: hipLaunchKernelGGL(k_gemm_prefill<KQ_Q4_K>, grid, block, 0, s, M, CT, row0, x, sx, m, Y, ldy); break;
+    case KQ_Q5_K: hipLaunchKernelGGL(k_gemm_prefill<KQ_Q5_K>, grid, block, 0, s, M, CT, row0, x, sx, m, Y, ldy); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

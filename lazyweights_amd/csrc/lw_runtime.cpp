@@ -119,6 +119,8 @@ struct Model {
   size_t cnt_cap = 0;
   uint16_t* X16 = nullptr;
   size_t X16_cap = 0;
+  uint16_t* SX = nullptr;  // per-sub-block activation sums (prefill GEMM)
+  size_t SX_cap = 0;
   uint8_t* x8 = nullptr;  // int8 activations: per vector [K int8][K / 32 d][K / 32 d sum q], 256-B aligned parts
   size_t x8_cap = 0;
   uint8_t* codes = nullptr;
@@ -398,6 +400,7 @@ void release(Model* M) {
   if (M->P) (void)hipFree(M->P);
   if (M->cnt) (void)hipFree(M->cnt);
   if (M->X16) (void)hipFree(M->X16);
+  if (M->SX) (void)hipFree(M->SX);
   if (M->x8) (void)hipFree(M->x8);
   if (M->codes) (void)hipFree(M->codes);
   if (M->W16) (void)hipFree(M->W16);
@@ -946,9 +949,10 @@ int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, in
   return fused_group_dev(M, &tp, &X16, 1, m, per, &Y, &ldy, s);
 }
 
-// Prefill GEMM of path 2: 0 (default) = decoded codes dequantized to fp16 hi + lo weights and rocBLAS (the one-GEMM
-// form up to g_prefill_one_max tokens, else two GEMMs); 1 = the hand-written MFMA GEMM over the codes
-// (k_gemm_codes_mfma); 2 / 3 = rocBLAS, always the two-GEMM / the one-GEMM form. Kernel mode 1 keeps the SIMT GEMM.
+// Prefill GEMM of path 2: 0 (default) = the hand-written MFMA GEMM with scaled fp16 weights for Q4_K / Q5_K
+// (k_gemm_prefill), rocBLAS for the other formats; 1 = hand-written for every format (Q6_K / IQ4_XS through
+// k_gemm_codes_mfma); 2 / 3 = rocBLAS, always the two-GEMM / the one-GEMM form over fp16 hi + lo weights; 4 = rocBLAS
+// with the one-GEMM form up to g_prefill_one_max tokens, else two GEMMs. Kernel mode 1 keeps the SIMT GEMM.
 int g_prefill = 0;
 
 // Y[:, r0 : r0 + nr] = x . w^T for a chunk of rows through rocBLAS. WW is the column-major nr x 2K matrix [w hi |
@@ -999,7 +1003,25 @@ int g_prefill_one_max = 512;
 
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
 int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
-  const bool blas = g_kernel_mode != 1 && g_prefill != 1;
+  const bool scaled_ok = t.kqt == lw::KQ_Q4_K || t.kqt == lw::KQ_Q5_K;
+  const bool own = g_kernel_mode != 1 && (g_prefill == 1 || (g_prefill == 0 && scaled_ok));
+  if (own && scaled_ok && t.K % 256 == 0 && lw::decode_tiled_ok(t.dm)) {
+    // the hand-written GEMM with scaled fp16 weights over tiled codes, x hi + lo and Sx hi + lo
+    const size_t row_bytes = (size_t)lw::TN * t.K;
+    const size_t cap = std::max(row_bytes, std::min<size_t>((size_t)t.N * t.K, (size_t)64 << 20));
+    if (grow(M.codes, M.codes_cap, cap) || grow(M.X16, M.X16_cap, lw::prefill_x_bytes(m, (int)t.K)) ||
+        grow(M.SX, M.SX_cap, lw::prefill_sx_bytes(m, (int)t.K)))
+      return -1;
+    HIPCHECK(lw::launch_prefill_x(X, M.X16, M.SX, m, (int)t.K, s));
+    const int rows_fit = (int)std::max<size_t>(1, M.codes_cap / row_bytes);
+    for (int tr0 = 0; tr0 < t.dm.NT; tr0 += rows_fit) {
+      const int tr1 = std::min(t.dm.NT, tr0 + rows_fit);
+      HIPCHECK(lw::launch_decode_tiled(t.dm, M.codes, tr0, tr1, s));
+      HIPCHECK(lw::launch_gemm_prefill(t.dm, M.codes, tr0 * lw::TN, (tr1 - tr0) * lw::TN, M.X16, M.SX, m, Y, ldy, s));
+    }
+    return 0;
+  }
+  const bool blas = g_kernel_mode != 1 && !own;
   const bool mfma = g_kernel_mode != 1 && !blas;
   if (blas) {
     if (!M.blas && rocblas_create_handle(&M.blas) != rocblas_status_success) {
@@ -1014,7 +1036,7 @@ int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ld
     // fp16 x: [m][2K] hi | hi, then [m][K] lo; weights [rows][2K] fp16 per chunk of tile rows (at most 256 MB)
     const size_t ww_row = (size_t)lw::TN * t.K * 4;
     const size_t cap = std::max(ww_row, std::min<size_t>((size_t)t.N * t.K * 4, (size_t)256 << 20));
-    const bool one = g_prefill == 3 || (g_prefill == 0 && m <= g_prefill_one_max);
+    const bool one = g_prefill == 3 || ((g_prefill == 0 || g_prefill == 4) && m <= g_prefill_one_max);
     if (grow(M.X16, M.X16_cap, (size_t)(one ? 4 : 3) * m * t.K * 2) || grow(M.W16, M.W16_cap, cap)) return -1;
     if (one) HIPCHECK(lw::launch_split_x_gemm2(X, M.X16, m, (int)t.K, s));
     else HIPCHECK(lw::launch_split_x_gemm(X, M.X16, M.X16 + (size_t)2 * m * t.K, m, (int)t.K, s));
@@ -1530,7 +1552,7 @@ int lw_set_kernel_mode(int mode) {
 }
 
 int lw_set_prefill_gemm(int which) {
-  if (which < 0 || which > 3) return -1;
+  if (which < 0 || which > 4) return -1;
   g_prefill = which;
   return 0;
 }

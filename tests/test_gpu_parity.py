@@ -122,9 +122,9 @@ def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
-    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) through both prefill GEMMs (rocBLAS over
-    fp16 hi + lo weights, the default; the hand-written matrix-core GEMM over the codes) against fp64, and against
-    the SIMT GEMM (kernel mode 1) to fp32 rounding."""
+    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) through every prefill GEMM (the hand-written
+    matrix-core GEMMs over the codes, the default for Q4_K / Q5_K; rocBLAS over fp16 hi + lo weights in its forms)
+    against fp64, and against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
     rt, mats = fmt_rt
     mat = mats[fmt]
     rng = np.random.default_rng(30 + kqt)
@@ -135,8 +135,8 @@ def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
         Ys = rt.test_matmul(fmt, X, path=2)
     finally:
         rt.lib.lw_set_kernel_mode(0)
-    for which, what in ((0, "rocBLAS hi + lo"), (2, "rocBLAS two GEMMs"), (3, "rocBLAS one GEMM"),
-                        (1, "matrix-core codes GEMM")):
+    for which, what in ((0, "default (hand-written for Q4_K / Q5_K)"), (2, "rocBLAS two GEMMs"),
+                        (3, "rocBLAS one GEMM"), (4, "rocBLAS auto"), (1, "hand-written matrix-core GEMM")):
         say("prefill m=80", fmt, what)
         assert rt.lib.lw_set_prefill_gemm(which) == 0
         try:
