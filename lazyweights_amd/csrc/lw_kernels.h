@@ -161,7 +161,7 @@ hipError_t launch_dequant_hilo(const DevMat& M, const uint8_t* codes, int row0, 
 // offsets): tile rows [tr0, tr1) -> WW rows relative to tr0 * 64
 hipError_t launch_decode_hilo(const DevMat& M, int tr0, int tr1, void* WW, hipStream_t s);
 // Prefill GEMM on the matrix cores for Q4_K / Q5_K (k_gemm_prefill): Y[t][row0 + r] for the chunk's rows r < nrows
-// (a multiple of 32) from its codes in the tiled layout (launch_decode_tiled) and x in the tiled layouts of
+// (a multiple of 64) from its codes in the tiled layout (launch_decode_tiled) and x in the tiled layouts of
 // launch_prefill_x; K a multiple of 256
 hipError_t launch_gemm_prefill(const DevMat& M, const uint8_t* CT, int row0, int nrows, const void* XT,
                                const void* SXT, int m, float* Y, int ldy, hipStream_t s);

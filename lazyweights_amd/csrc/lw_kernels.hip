@@ -2359,6 +2359,84 @@ __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restr
   }
 }
 
+// Codes in the prefill GEMM's tiled layout (launch_decode_tiled): one block of 4 waves per tile as k_decode_split,
+// but each lane runs the two 32-symbol chains of its 64-symbol segment (split starts 2k and 2k + 1) interleaved, and
+// stores its codes straight from registers: 16 codes make one lane's piece of the tiled layout, and the 32 lanes of a
+// row half write 32 consecutive pieces (512 B) per store. No code rows in LDS: the block holds the table and the tile.
+template <int SYMB>
+__global__ void __launch_bounds__(256) k_decode_tiled(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1,
+                                                      int stage_rows) {
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  __shared__ __align__(16) uint32_t lut4[LUTN];  // the only static LDS object: at LDS address 0 (table_addr ORs it in)
+  extern __shared__ __align__(16) uint32_t tw[];
+  const int KT = M.KT, KC = M.K / 32;
+  const int t = tr0 * KT + (int)blockIdx.x;
+  if (t >= tr1 * KT) return;
+  const int tc = t % KT, tr = t / KT;
+  const int R = min((int)M.rows[t] + 2, stage_rows);
+  for (int i = threadIdx.x; i < LUTN; i += 256) {
+    const uint32_t e = M.lut[i];
+    lut4[i] = (e >> 8) | (e & 255u) << 16;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
+  for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
+  __syncthreads();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  const int k = 4 * f + wave;  // segment of bit-lane l: row f * 32 + l, symbols 64 wave .. 64 wave + 63
+  const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
+  uint32_t P[2], slot[2], A[2], B[2], C[2];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    P[ch] = (uint32_t)M.split[((size_t)t * SPLITS + 2 * k + ch) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+    slot[ch] = __builtin_amdgcn_ubfe(P[ch], 5, 8);
+    A[ch] = *(LdsU32*)(rlb + ((slot[ch] - 2u) << 7));
+    B[ch] = *(LdsU32*)(rlb + ((slot[ch] - 1u) << 7));
+    C[ch] = *(LdsU32*)(rlb + (slot[ch] << 7));
+  }
+  // chain ch holds codes [2 (64 wave + 32 ch), + 64) (SYMB 4) or [64 wave + 32 ch, + 32) (SYMB 8) of the row
+  const size_t rt = (size_t)(tr - tr0) * 2 + f;
+  uint8_t* const obase = out + (rt * KC * 64 + l) * 16;
+  const int kc0 = SYMB == 4 ? tc * (2 * TK / 32) + 4 * wave : tc * (TK / 32) + 2 * wave;
+  uint32_t acc[2][4];
+#pragma unroll
+  for (int p = 0; p < 16; ++p) {
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const uint32_t w1 = __builtin_amdgcn_alignbit(B[ch], A[ch], P[ch]);
+      const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
+      const uint32_t w2 = w1 >> (e1 & 31u);
+      const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
+      P[ch] = P[ch] + e1 + e2;
+      const uint32_t nslot = __builtin_amdgcn_ubfe(P[ch], 5, 8);
+      const bool slide = nslot != slot[ch];
+      A[ch] = slide ? B[ch] : A[ch];
+      B[ch] = slide ? C[ch] : B[ch];
+      slot[ch] = nslot;
+      C[ch] = *(LdsU32*)(rlb + (nslot << 7));
+      const uint32_t s1 = e1 >> 16, s2 = e2 >> 16;
+      if (SYMB == 4) {  // 4 codes per pair, low nibble first; a piece every 4 pairs
+        acc[ch][p & 3] = (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
+        if ((p & 3) == 3) {
+          const int q = p >> 2;  // piece q of the chain's 64 codes: chunk kc0 + 2 ch + q / 2, half q % 2
+          *reinterpret_cast<uint4*>(obase + ((size_t)(kc0 + 2 * ch + (q >> 1)) * 64 + 32 * (q & 1)) * 16) =
+              make_uint4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
+        }
+      } else {  // 2 codes per pair; a piece every 8 pairs
+        const uint32_t v = s1 | s2 << 8;
+        if (p & 1) acc[ch][(p >> 1) & 3] |= v << 16;
+        else acc[ch][(p >> 1) & 3] = v;
+        if ((p & 7) == 7)
+          *reinterpret_cast<uint4*>(obase + ((size_t)(kc0 + ch) * 64 + 32 * (p >> 3)) * 16) =
+              make_uint4(acc[ch][0], acc[ch][1], acc[ch][2], acc[ch][3]);
+      }
+    }
+  }
+}
+
 template <bool TILED>
 static hipError_t decode_fast(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
   if (M.packed) {
@@ -2387,7 +2465,17 @@ bool decode_tiled_ok(const DevMat& M) {
 
 hipError_t launch_decode_tiled(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
   if (!decode_tiled_ok(M)) return hipErrorNotSupported;
-  return decode_fast<true>(M, out, tr0, tr1, s);
+  if (M.packed || tr0 >= tr1) return decode_fast<true>(M, out, tr0, tr1, s);
+  const int rows = M.max_rows + 2;
+  const size_t sm = (size_t)rows * 128;
+  const void* f = M.symbits == 4 ? reinterpret_cast<const void*>(&k_decode_tiled<4>)
+                                 : reinterpret_cast<const void*>(&k_decode_tiled<8>);
+  hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
+  if (e != hipSuccess) return e;
+  const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
+  if (M.symbits == 4) hipLaunchKernelGGL(k_decode_tiled<4>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  else hipLaunchKernelGGL(k_decode_tiled<8>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
@@ -2540,28 +2628,61 @@ hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row
 }
 
 // ── prefill GEMM on the matrix cores, Q4_K / Q5_K (path 2 and m > 8, the default for these formats) ─────────
-// Y[t][n] = sum over super-blocks of d_n (x_t . w'_n) - dmin_n (Sx_t . m_n), where w'_k = sc_j f(q_k) is the code
-// scaled by its sub-block's 6-bit scale (at most 63 x 31 = 1953: an exact fp16 integer), Sx_t,j the sum of x_t over
-// sub-block j and m_n,j the sub-block's 6-bit min. Both dot products run on v_mfma_f32_32x32x16_f16 with x split into
-// fp16 hi + lo (two products per weight, exact in fp32), the mins term as one K = 16 product per super-block (8
-// sub-blocks, zero-padded) with Sx split likewise; fp32 accumulation, d and dmin applied once per super-block.
+// Y[t][n] = sum over super-blocks of d_n (x_t . w'_n) - dmin_n (Sx_t . m_n), where w'_k = sc_j q_k is the code scaled
+// by its sub-block's 6-bit scale (at most 63 x 31 = 1953) and Sx_t,j the sum of x_t over sub-block j, m_n,j the
+// sub-block's 6-bit min. Both dot products run on v_mfma_f32_32x32x16_f16 with x split into fp16 hi + lo (two
+// products per weight, fp32 accumulation), the mins term as one K = 16 product per super-block (8 sub-blocks,
+// zero-padded) with Sx split likewise; d and dmin applied once per super-block.
+// Weights enter the products as w'/16, exact in fp16: a byte permute against 0x54 bytes makes fp16(64 + q/16) of each
+// code, and one fma with sc and -64 sc leaves sc q / 16 (every intermediate exact); the 16 goes into d.
 // Operand layout (32x32x16): lane l holds A[i = l % 32][k = 8 (l / 32) + 0..7] (token i) and B[k = 8 (l / 32) + 0..7]
 // [j = l % 32] (weight row j), and receives D[i = 8 (r / 4) + 4 (l / 32) + r % 4][j = l % 32] in register r: a lane owns
-// one weight row (one set of scales) and 16 tokens of each 32-token tile.
-// Block = GEMM_WAVES waves over one tile of 32 weight rows x 64 tokens (two token tiles); the waves split K by
-// super-block (wave w takes super-blocks w, w + GEMM_WAVES, ...) and their partial tiles are summed through LDS in
-// wave order, so the result does not depend on timing. A skinny prefill (m = 128, N = 4096) still gives 256 blocks.
+// one weight row (one set of scales) per row tile and 16 tokens of the token tile.
+// Block = GEMM_WAVES waves over 64 weight rows (two row tiles) x 32 tokens; the waves split K by super-block (wave w
+// takes super-blocks w, w + GEMM_WAVES, ...) and their partial tiles are summed through LDS in wave order, so the
+// result does not depend on timing. A skinny prefill (m = 128, N = 4096) gives 256 blocks.
 constexpr int GEMM_WAVES = 8;
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw dword loads on CDNA (32-bit data format)
 
-// codes q0..q3 (bytes of qw) scaled by sc (fp16 pair of the sub-block scale) -> 4 fp16 weights in two words: each
-// pair of bytes becomes fp16(1024 + q) by a byte permute against 0x64 bytes, then (v - 1024) * sc, exact
-__device__ __forceinline__ uint2 scaled_codes(uint32_t qw, h2v sc) {
-  const h2v bias = {(_Float16)-1024.f, (_Float16)-1024.f};
-  const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04010400u));
-  const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04030402u));
-  return make_uint2(__builtin_bit_cast(uint32_t, (h2v)((a + bias) * sc)),
-                    __builtin_bit_cast(uint32_t, (h2v)((b + bias) * sc)));
+// codes q0..q3 (bytes of qw) -> sc q / 16 as 4 fp16 in two words (nsc = -64 sc)
+__device__ __forceinline__ uint2 scaled_codes16(uint32_t qw, h2v sc, h2v nsc) {
+  const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, qw, 0x04010400u));
+  const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, qw, 0x04030402u));
+  return make_uint2(__builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc, nsc)),
+                    __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc, nsc)));
+}
+
+// a row's Q4_K / Q5_K super-block record, compacted: the 8 scales and the 8 mins as bytes, d x 16 and dmin
+struct KSide {
+  uint32_t sc_lo, sc_hi, m_lo, m_hi;
+  float d16, dmin;
+};
+__device__ __forceinline__ KSide kside(const uint32_t* w) {
+  KSide k;
+  k.sc_lo = w[1] & 0x3F3F3F3Fu;
+  k.sc_hi = (w[3] & 0x0F0F0F0Fu) | ((w[1] >> 2) & 0x30303030u);
+  k.m_lo = w[2] & 0x3F3F3F3Fu;
+  k.m_hi = ((w[3] >> 4) & 0x0F0F0F0Fu) | ((w[2] >> 2) & 0x30303030u);
+  k.d16 = 16.f * h2f(w[0]);
+  k.dmin = h2f(w[0] >> 16);
+  return k;
+}
+// sub-block j's scale as an fp16 pair
+__device__ __forceinline__ h2v kside_sc(const KSide& k, int j) {
+  const _Float16 v = (_Float16)(float)((((j < 4) ? k.sc_lo : k.sc_hi) >> (8 * (j & 3))) & 255u);
+  return h2v{v, v};
+}
+// the 8 mins as the B operand of the mins product (k 0..7; lanes h = 1 pass zeros)
+__device__ __forceinline__ h8v kside_mins(const KSide& k) {
+  h8v v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[i] = (_Float16)(float)((k.m_lo >> (8 * i)) & 255u);
+    v[4 + i] = (_Float16)(float)((k.m_hi >> (8 * i)) & 255u);
+  }
+  return v;
 }
 
 // Layouts (all lane-linear: one wave's load of a piece is one contiguous 1 KB read):
@@ -2581,120 +2702,128 @@ __global__ void __launch_bounds__(64 * GEMM_WAVES) k_gemm_prefill(DevMat M, cons
   constexpr int SB = kq_sbytes(KQ), NSB = kq_symbits(KQ) == 4 ? 2 : 1;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
-  const int rt = blockIdx.x, tp = blockIdx.y;            // 32-row tile of the chunk, pair of 32-token tiles
+  const int rp = blockIdx.x, tt = blockIdx.y;            // pair of 32-row tiles of the chunk, 32-token tile
   const int K = M.K, KC = K / 32, NB = K / 256;
-  const int n = rt * 32 + c;                             // the lane's weight row within the chunk
-  const uint8_t* cw = CT + (size_t)rt * KC * 1024 + lane * 16;
-  const uint16_t* xw0 = XT + (size_t)(2 * tp) * KC * 2048 + lane * 8;
-  const uint16_t* xw1 = xw0 + (size_t)KC * 2048;
-  const uint16_t* sw0 = SXT + (size_t)(2 * tp) * NB * 512 + c * 8;
-  const uint16_t* sw1 = sw0 + (size_t)NB * 512;
-  struct Ops {  // one chunk: the lane's 16 codes and its 4 x pieces (half, step) of each token tile
-    uint4 q, x0[4], x1[4];
+  const int nA = rp * 64 + c, nB = nA + 32;              // the lane's weight rows within the chunk
+  // buffer resources over the block's codes (its two row tiles) and x (its token tile): the lane's byte offset is
+  // the only per-lane address, the chunk offset a scalar
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(CT + (size_t)rp * 2 * KC * 1024), (short)0, 2 * KC * 1024, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(XT + (size_t)tt * KC * 2048), (short)0, KC * 4096, kBufferRsrcWord3);
+  const uint16_t* sxw = SXT + (size_t)tt * NB * 512 + c * 8;
+  const uint32_t vo = (uint32_t)lane * 16;
+  // operands in flight: codes and x three chunks ahead on 4-slot rings (one depth for both: the load counter
+  // completes in issue order); 8 chunks per super-block keep the rings aligned
+  auto load_q = [&](int kc, u32x4& qa, u32x4& qb) {
+    qa = __builtin_amdgcn_raw_buffer_load_b128(rc, vo, kc * 1024, 0);
+    qb = __builtin_amdgcn_raw_buffer_load_b128(rc, vo, (KC + kc) * 1024, 0);
   };
-  auto load = [&](int kc) {
-    Ops o;
-    o.q = *reinterpret_cast<const uint4*>(cw + (size_t)kc * 1024);
+  auto load_x = [&](int kc, u32x4* x) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o.x0[i] = *reinterpret_cast<const uint4*>(xw0 + (size_t)kc * 2048 + i * 512);
-      o.x1[i] = *reinterpret_cast<const uint4*>(xw1 + (size_t)kc * 2048 + i * 512);
-    }
-    return o;
+    for (int i = 0; i < 4; ++i) x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, vo + i * 1024, kc * 4096, 0);
   };
-  f16x16 tot0 = {}, tot1 = {};
-  uint32_t swn[5] = {};
-  Ops cur = {};
+  f16x16 totA = {}, totB = {};
+  uint32_t swa[5] = {}, swb[5] = {};
+  u32x4 qa[4] = {}, qb[4] = {}, xr[4][4] = {};
   if (wave < NB) {
-    side_load<KQ>(M.side + side_record(row0 + n, wave, M.KT, NSB) * SB, swn);
-    cur = load(wave * 8);
+    side_load<KQ>(M.side + side_record(row0 + nA, wave, M.KT, NSB) * SB, swa);
+    side_load<KQ>(M.side + side_record(row0 + nB, wave, M.KT, NSB) * SB, swb);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      load_q(wave * 8 + i, qa[i], qb[i]);
+      load_x(wave * 8 + i, xr[i]);
+    }
   }
   for (int sb = wave; sb < NB; sb += GEMM_WAVES) {
-    uint32_t sw[5];
-#pragma unroll
-    for (int i = 0; i < 5; ++i) sw[i] = swn[i];
+    const KSide ka = kside(swa), kb = kside(swb);
     const int nsb = sb + GEMM_WAVES;
-    if (nsb < NB) side_load<KQ>(M.side + side_record(row0 + n, nsb, M.KT, NSB) * SB, swn);
-    // Sx of this super-block (lanes h = 0; k 8..15 of the mins product stay zero)
-    uint4 s0h = {}, s0l = {}, s1h = {}, s1l = {};
-    if (h == 0) {
-      s0h = *reinterpret_cast<const uint4*>(sw0 + (size_t)sb * 512);
-      s0l = *reinterpret_cast<const uint4*>(sw0 + (size_t)sb * 512 + 256);
-      s1h = *reinterpret_cast<const uint4*>(sw1 + (size_t)sb * 512);
-      s1l = *reinterpret_cast<const uint4*>(sw1 + (size_t)sb * 512 + 256);
+    if (nsb < NB) {
+      side_load<KQ>(M.side + side_record(row0 + nA, nsb, M.KT, NSB) * SB, swa);
+      side_load<KQ>(M.side + side_record(row0 + nB, nsb, M.KT, NSB) * SB, swb);
     }
-    uint64_t scq, scq2;
-    float dA, dB;
-    side_packed<KQ>(sw, scq, scq2, dA, dB);
-    f16x16 d10 = {}, d11 = {};
+    uint4 sxh = {}, sxl = {};  // Sx of this super-block, loaded at chunk 5
+    f16x16 dA = {}, dB = {};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {  // the super-block's 8 chunks (sub-blocks), the next chunk's loads one ahead
-      Ops nxt = {};
-      if (j < 7) nxt = load(sb * 8 + j + 1);
-      else if (nsb < NB) nxt = load(nsb * 8);
-      const _Float16 scf = (_Float16)(float)(uint32_t)((scq >> (8 * j)) & 255u);
-      const h2v sc = {scf, scf};
+    for (int j = 0; j < 8; ++j) {  // the super-block's 8 chunks (sub-blocks)
+      if (j < 5 || nsb < NB) {
+        const int kn = j < 5 ? sb * 8 + j + 3 : nsb * 8 + j - 5;
+        load_q(kn, qa[(j + 3) & 3], qb[(j + 3) & 3]);
+        load_x(kn, xr[(j + 3) & 3]);
+      }
+      if (j == 5 && h == 0) {  // lanes h = 0 hold the mins product's k 0..7; k 8..15 stay zero
+        sxh = *reinterpret_cast<const uint4*>(sxw + (size_t)sb * 512);
+        sxl = *reinterpret_cast<const uint4*>(sxw + (size_t)sb * 512 + 256);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads issued here, ahead of this chunk's products
+      const u32x4 ca = qa[j & 3], cb = qb[j & 3];
+      const u32x4* xc = xr[j & 3];
+      const h2v sca = kside_sc(ka, j), scb = kside_sc(kb, j);
+      const h2v n64 = {(_Float16)-64.f, (_Float16)-64.f};
+      const h2v nsa = sca * n64, nsb2 = scb * n64;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
-        const uint2 wa = scaled_codes(st ? cur.q.z : cur.q.x, sc), wb = scaled_codes(st ? cur.q.w : cur.q.y, sc);
-        const h8v b = __builtin_bit_cast(h8v, make_uint4(wa.x, wa.y, wb.x, wb.y));
-        d10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x0[st]), b, d10, 0, 0, 0);
-        d10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x0[2 + st]), b, d10, 0, 0, 0);
-        d11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x1[st]), b, d11, 0, 0, 0);
-        d11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, cur.x1[2 + st]), b, d11, 0, 0, 0);
+        const uint2 a0 = scaled_codes16(ca[2 * st], sca, nsa), a1 = scaled_codes16(ca[2 * st + 1], sca, nsa);
+        const uint2 b0 = scaled_codes16(cb[2 * st], scb, nsb2), b1 = scaled_codes16(cb[2 * st + 1], scb, nsb2);
+        const h8v wa = __builtin_bit_cast(h8v, make_uint4(a0.x, a0.y, a1.x, a1.y));
+        const h8v wb = __builtin_bit_cast(h8v, make_uint4(b0.x, b0.y, b1.x, b1.y));
+        const h8v xh = __builtin_bit_cast(h8v, xc[st]), xl = __builtin_bit_cast(h8v, xc[2 + st]);
+        dA = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wa, dA, 0, 0, 0);
+        dB = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wb, dB, 0, 0, 0);
+        dA = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, wa, dA, 0, 0, 0);
+        dB = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, wb, dB, 0, 0, 0);
       }
-      cur = nxt;
     }
     // mins: A2 = the tokens' Sx over the super-block's 8 sub-blocks, B2 = the row's 8 mins
-    float mf[8];
-    side_mins(sw, mf);
-    h8v b2 = {};
-    if (h == 0)
-      b2 = h8v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3],
-               (_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
-    f16x16 d20 = {}, d21 = {};
-    d20 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s0h), b2, d20, 0, 0, 0);
-    d20 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s0l), b2, d20, 0, 0, 0);
-    d21 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s1h), b2, d21, 0, 0, 0);
-    d21 = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, s1l), b2, d21, 0, 0, 0);
+    h8v ma = {}, mb = {};
+    if (h == 0) {
+      ma = kside_mins(ka);
+      mb = kside_mins(kb);
+    }
+    f16x16 mA = {}, mB = {};
+    mA = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, sxh), ma, mA, 0, 0, 0);
+    mB = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, sxh), mb, mB, 0, 0, 0);
+    mA = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, sxl), ma, mA, 0, 0, 0);
+    mB = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, sxl), mb, mB, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      tot0[r] = fmaf(dA, d10[r], fmaf(-dB, d20[r], tot0[r]));
-      tot1[r] = fmaf(dA, d11[r], fmaf(-dB, d21[r], tot1[r]));
+      totA[r] = fmaf(ka.d16, dA[r], fmaf(-ka.dmin, mA[r], totA[r]));
+      totB[r] = fmaf(kb.d16, dB[r], fmaf(-kb.dmin, mB[r], totB[r]));
     }
   }
-  // partial tiles -> LDS as part[wave][tile][r][lane] (lane-contiguous, no bank conflicts), then each thread sums
-  // its outputs over the waves in order; consecutive threads take consecutive lanes = consecutive weight rows
+  // partial tiles -> LDS as part[wave][row tile][r][lane] (lane-contiguous, no bank conflicts), then each thread
+  // sums its outputs over the waves in order; consecutive threads take consecutive lanes = consecutive weight rows
   __shared__ float part[GEMM_WAVES][2][16][64];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    part[wave][0][r][lane] = tot0[r];
-    part[wave][1][r][lane] = tot1[r];
+    part[wave][0][r][lane] = totA[r];
+    part[wave][1][r][lane] = totB[r];
   }
   __syncthreads();
   for (int e = threadIdx.x; e < 2 * 16 * 64; e += 64 * GEMM_WAVES) {
-    const int tile = e >> 10, r = (e >> 6) & 15, l = e & 63;
+    const int half = e >> 10, r = (e >> 6) & 15, l = e & 63;
     float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < GEMM_WAVES; ++w) acc += part[w][tile][r][l];
-    const int t = tp * 64 + 32 * tile + 8 * (r / 4) + 4 * (l >> 5) + (r % 4);
-    if (t < m) Y[(size_t)t * ldy + row0 + rt * 32 + (l & 31)] = acc;
+    for (int w = 0; w < GEMM_WAVES; ++w) acc += part[w][half][r][l];
+    const int t = tt * 32 + 8 * (r / 4) + 4 * (l >> 5) + (r % 4);
+    if (t < m) Y[(size_t)t * ldy + row0 + rp * 64 + 32 * half + (l & 31)] = acc;
   }
 }
 
 // x of the prefill GEMM: fp32 X [m][K] -> XT (fp16 hi = fp16(x), lo = fp16(x - hi)) and SXT (per sub-block of 32
-// weights s = ((a0 + a1) + (a2 + a3)), a_i the in-order fp32 sum of its i-th 8 values, as fp16 hi / lo), tokens
-// padded with zeros to a multiple of 64. One thread per token and 8 consecutive weights; the 4 threads of a chunk are
-// consecutive lanes.
+// weights s = ((a0 + a1) + (a2 + a3)), a_q the in-order fp32 sum of its q-th 8 values, as fp16 hi / lo), tokens
+// padded with zeros to a multiple of 64. Thread = (chunk, q, token c of the tile): the 32 threads of one q write one
+// lane-linear 512-byte run of a piece; the chunk's four a_q meet in LDS.
 __global__ void __launch_bounds__(256) k_prefill_x(const float* __restrict__ X, uint16_t* __restrict__ XT,
                                                    uint16_t* __restrict__ SXT, int m, int K) {
-  const int G = K / 8, KC = K / 32, NB = K / 256;
-  const int i = (int)blockIdx.x * 256 + threadIdx.x;
-  const int t = i / G, g = i - t * G;                    // the grid covers the padded tokens exactly
+  const int KC = K / 32, NB = K / 256;
+  const int i = (int)blockIdx.x * 256 + threadIdx.x;     // the grid covers the padded tokens exactly
+  const int c = i & 31, q = (i >> 5) & 3, ci = i >> 7;
+  const int tt = ci / KC, kc = ci - tt * KC, t = tt * 32 + c, hh = q >> 1, st = q & 1;
   float v[8];
   if (t < m) {
-    const float4 a = *reinterpret_cast<const float4*>(X + (size_t)t * K + 8 * g);
-    const float4 b = *reinterpret_cast<const float4*>(X + (size_t)t * K + 8 * g + 4);
+    const float* x = X + (size_t)t * K + 32 * kc + 8 * q;
+    const float4 a = *reinterpret_cast<const float4*>(x), b = *reinterpret_cast<const float4*>(x + 4);
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
   } else {
 #pragma unroll
@@ -2711,19 +2840,19 @@ __global__ void __launch_bounds__(256) k_prefill_x(const float* __restrict__ X, 
     sum += v[e];
     sum += v[e + 1];
   }
-  const int tt = t >> 5, c = t & 31, kc = g >> 2, hh = (g >> 1) & 1, st = g & 1;
-  const size_t piece = ((size_t)tt * KC + kc) * 2;
-  uint4* o = reinterpret_cast<uint4*>(XT) + (piece * 2 + st) * 64 + 32 * hh + c;
+  uint4* o = reinterpret_cast<uint4*>(XT) + ((((size_t)tt * KC + kc) * 2) * 2 + st) * 64 + 32 * hh + c;
   o[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
   o[2 * 64] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  const float s01 = sum + __shfl_xor(sum, 1);
-  const float s = s01 + __shfl_xor(s01, 2);
-  if ((g & 3) == 0) {
+  __shared__ float part[2][4][32];                       // the block's two chunks
+  const int cb = (threadIdx.x >> 7) & 1;
+  part[cb][q][c] = sum;
+  __syncthreads();
+  if (q == 0) {
+    const float s = (part[cb][0][c] + part[cb][1][c]) + (part[cb][2][c] + part[cb][3][c]);
     const _Float16 hi = (_Float16)s;
-    const int sb = kc >> 3, j = kc & 7;
-    uint16_t* q = SXT + (((size_t)tt * NB + sb) * 2 * 32 + c) * 8 + j;
-    q[0] = __builtin_bit_cast(uint16_t, hi);
-    q[32 * 8] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hi));
+    uint16_t* sx = SXT + ((((size_t)tt * NB + (kc >> 3)) * 2) * 32 + c) * 8 + (kc & 7);
+    sx[0] = __builtin_bit_cast(uint16_t, hi);
+    sx[32 * 8] = __builtin_bit_cast(uint16_t, (_Float16)(s - (float)hi));
   }
 }
 
@@ -2741,8 +2870,8 @@ size_t prefill_sx_bytes(int m, int K) { return (size_t)((m + 63) / 64 * 64) * (K
 
 hipError_t launch_gemm_prefill(const DevMat& M, const uint8_t* CT, int row0, int nrows, const void* XT,
                                const void* SXT, int m, float* Y, int ldy, hipStream_t s) {
-  if (nrows < 1 || m < 1 || nrows % 32 || M.K % 256) return hipErrorInvalidValue;
-  const dim3 grid(nrows / 32, (m + 63) / 64), block(64 * GEMM_WAVES);
+  if (nrows < 1 || m < 1 || nrows % 64 || M.K % 256) return hipErrorInvalidValue;
+  const dim3 grid(nrows / 64, (m + 31) / 32), block(64 * GEMM_WAVES);
   const uint16_t* x = static_cast<const uint16_t*>(XT);
   const uint16_t* sx = static_cast<const uint16_t*>(SXT);
   switch (M.kqt) {

@@ -122,9 +122,9 @@ def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
-    """Prefill-shaped path 2 (m = 80: a full and a partial 64-token tile) through every prefill GEMM (the hand-written
-    matrix-core GEMMs over the codes, the default for Q4_K / Q5_K; rocBLAS over fp16 hi + lo weights in its forms)
-    against fp64, and against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
+    """Prefill-shaped path 2 (m = 80: two full 32-token tiles and a partial one) through every prefill GEMM (the
+    hand-written matrix-core GEMMs over the codes, the default for Q4_K / Q5_K; rocBLAS over fp16 hi + lo weights in
+    its forms) against fp64, and against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
     rt, mats = fmt_rt
     mat = mats[fmt]
     rng = np.random.default_rng(30 + kqt)
@@ -149,7 +149,8 @@ def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
 
 def test_gpu_prefill_gemm_row_chunks(gpu, tmp_path, orc, lib):
     """A matrix whose codes exceed the 64 MB decode scratch (17408 x 4096 Q4_K: two row chunks), m = 9 (auto path
-    2), through the rocBLAS prefill GEMM: every chunk lands in its own rows of y."""
+    2), through the default prefill GEMM (hand-written, tiled codes) and rocBLAS: every chunk lands in its own rows
+    of y."""
     from lazyweights_amd import Runtime, bundle
     mat = ("big", 1, 17408, 4096, 2.3, 91)
     bundle.write_synthetic_bundle(str(tmp_path), [mat], threads=8)
@@ -157,8 +158,13 @@ def test_gpu_prefill_gemm_row_chunks(gpu, tmp_path, orc, lib):
     X = rng.uniform(-1, 1, (9, 4096)).astype(np.float32)
     _, y64 = reference_y(orc, mat, X.astype(np.float64))
     with Runtime(tmp_path) as rt:
-        say("prefill row chunks m=9")
-        check_err(rt.test_matmul("big", X), y64, "big m=9 (two row chunks)")
+        for which, what in ((0, "default"), (4, "rocBLAS")):
+            say("prefill row chunks m=9", what)
+            assert rt.lib.lw_set_prefill_gemm(which) == 0
+            try:
+                check_err(rt.test_matmul("big", X), y64, "big m=9 (two row chunks, %s)" % what)
+            finally:
+                rt.lib.lw_set_prefill_gemm(0)
 
 
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
