@@ -97,6 +97,92 @@ def measure_traffic(layers):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps):
+    """A further configuration of the benchmark contract: `layers` copies of its matrices (own seeds, together beyond
+    the 256 MB Infinity Cache), one grouped call per layer and step, fp16 x resident. Per m: ms per step, GB/s of
+    algorithmic coded bytes (as the headline), and the kernels alone timed with HIP events (lw_bench_groups) against
+    the HBM peak; for m > 1 also the same tokens as m consecutive m = 1 steps."""
+    import ctypes
+    d = os.path.join(work, key)
+    lm = [("l%d.%s" % (l, nm), kqt, N, K, H, seed + 97 * l) for l in range(layers)
+          for nm, kqt, N, K, H, seed in mats]
+    bundle.write_synthetic_bundle(d, lm, threads=16)
+    rt = rt_cls(d)
+    try:
+        infos = [rt.info(mt[0]) for mt in lm]
+        n, per = len(lm), len(mats)
+        stream = torch.cuda.current_stream().cuda_stream
+        g = torch.Generator().manual_seed(11)
+        mmax = max(ms)
+        X = [torch.randn(mmax, inf["K"], generator=g).half().cuda() for inf in infos]
+        Y = [torch.zeros(mmax, inf["N"], device="cuda") for inf in infos]
+        names = (ctypes.c_char_p * n)(*[mt[0].encode() for mt in lm])
+        xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in X])
+        yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in Y])
+        groups = [slice(per * l, per * l + per) for l in range(layers)]
+        calls = [((ctypes.c_char_p * per)(*names[sl]), (ctypes.c_void_p * per)(*xp[sl]),
+                  (ctypes.c_void_p * per)(*yp[sl])) for sl in groups]
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / steps
+
+        res = {"layers": layers, "matrices": ["%s kqt %d %dx%d H=%.1f" % (nm, kqt, N, K, H)
+                                              for nm, kqt, N, K, H, _ in mats],
+               "coded_MB": round(sum(inf["blob_bytes"] + inf["side_bytes"] for inf in infos) / 1e6, 1)}
+        for m in ms:
+            def step():
+                for nm, xx, yy in calls:
+                    if lib.lw_group_matmul_dev(rt.h, per, nm, xx, m, yy, stream) != 0:
+                        raise RuntimeError(lib.lw_last_error().decode())
+            sms = timed(step)
+            sbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m + 4 * m * inf["N"]
+                               for inf in infos))
+            kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
+            sizes = (ctypes.c_int * layers)(*([per] * layers))
+            out = (ctypes.c_double * 3)()
+            if lib.lw_bench_groups(rt.h, layers, sizes, names, xp, m, yp, 1, max(3, steps // 2), out) != 0:
+                raise RuntimeError(lib.lw_last_error().decode())
+            rec = {"ms_per_step": round(sms, 4), "GBps_coded": round(sbytes / (sms * 1e-3) / 1e9, 1),
+                   "kernel_ms_per_pass": round(out[1], 4), "launches_per_pass": int(out[2]),
+                   "roofline_frac": round(kbytes / (out[1] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            if m > 1:  # the same m tokens as m steps at m = 1 (config 4's comparison)
+                singles = []
+                for t in range(m):
+                    for sl in groups:
+                        singles.append(((ctypes.c_char_p * per)(*names[sl]),
+                                        (ctypes.c_void_p * per)(*[X[i].data_ptr() + 2 * t * infos[i]["K"]
+                                                                  for i in range(sl.start, sl.stop)]),
+                                        (ctypes.c_void_p * per)(*[Y[i].data_ptr() + 4 * t * infos[i]["N"]
+                                                                  for i in range(sl.start, sl.stop)])))
+
+                def rep():
+                    for nm, xx, yy in singles:
+                        if lib.lw_group_matmul_dev(rt.h, per, nm, xx, 1, yy, stream) != 0:
+                            raise RuntimeError(lib.lw_last_error().decode())
+                rms = timed(rep)
+                rec["repeated_m1"] = {"ms_per_step": round(rms, 4), "gemm_over_repeated": round(sms / rms, 3),
+                                      "gemm_over_one_m1_step": None}
+            res["m%d" % m] = rec
+            log("bench: %s m=%d: %.3f ms per step (%d layers), %.1f GB/s coded, kernels %.1f%% of HBM peak%s"
+                % (key, m, sms, layers, rec["GBps_coded"], 100 * rec["roofline_frac"],
+                   "" if m == 1 else "; %d x m=1: %.3f ms" % (m, rec["repeated_m1"]["ms_per_step"])))
+        if 1 in ms:
+            for m in ms:
+                if m > 1:
+                    res["m%d" % m]["repeated_m1"]["gemm_over_one_m1_step"] = round(
+                        res["m%d" % m]["ms_per_step"] / res["m1"]["ms_per_step"], 3)
+        return res
+    finally:
+        rt.close()
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_share():
     """Threads for the CPU baseline: every core this process may run on (its affinity mask), capped by the cgroup's
     CPU quota when one is set (a share of a larger host); plus what the host reports, for the record."""
@@ -133,6 +219,9 @@ def main():
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--no-packed", action="store_true", help="skip the packed-twin control")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-shape (m = 128) figure")
+    ap.add_argument("--no-configs", action="store_true", help="skip configs 1, 3 and 4 (Q5_K)")
+    ap.add_argument("--only-configs", action="store_true",
+                    help="time configs 1, 3 and 4 (Q5_K) only (for a kernel trace of their kernels)")
     ap.add_argument("--kernel-mode", type=int, default=0, help="lw_set_kernel_mode for the whole run (0 = auto)")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
@@ -147,13 +236,27 @@ def main():
     import torch
 
     from lazyweights_amd import Runtime, bundle, load_library
-    from lazyweights_amd.configs import config2_layer
+    from lazyweights_amd.configs import CONFIG1, CONFIG3, CONFIG4, Q5_K, config2_layer
+
+    def further_configs(work):
+        steps = max(3, a.steps // 2)
+        return {"config1": time_config(lib, Runtime, bundle, torch, work, "config1", CONFIG1, 8, (1,), steps),
+                "config3": time_config(lib, Runtime, bundle, torch, work, "config3", CONFIG3, 4, (1,), steps),
+                "config4_q5k": time_config(lib, Runtime, bundle, torch, work, "config4_q5k",
+                                           [mt for mt in CONFIG4 if mt[1] == Q5_K], 3, (1, 5), steps)}
 
     lib = load_library()
     if lib.lw_set_kernel_mode(a.kernel_mode) != 0:
         raise SystemExit("bench.py: unknown kernel mode %d" % a.kernel_mode)
     work = a.workdir or tempfile.mkdtemp(prefix="lw_bench_")
     os.makedirs(work, exist_ok=True)
+    if a.only_configs:
+        try:
+            print(json.dumps(further_configs(work)), flush=True)
+        finally:
+            if not a.workdir:
+                shutil.rmtree(work, ignore_errors=True)
+        return
     try:
         t0 = time.time()
         mats = [m for l in range(a.layers) for m in config2_layer(l)]
@@ -308,8 +411,12 @@ def main():
                     vms = (time.perf_counter() - t0) * 1e3 / a.steps
                 finally:
                     lib.lw_set_act8(0)
-                verify[key] = {"ms_per_step": round(vms, 4), "GBps_coded": round(vbytes / (vms * 1e-3) / 1e9, 1)}
+                verify[key] = {"ms_per_step": round(vms, 4), "GBps_coded": round(vbytes / (vms * 1e-3) / 1e9, 1),
+                               "over_one_m1_step": round(vms / ms_per_step, 3)}
                 log("bench: verify m=%d (%s): %.3f ms per step, %.1f GB/s coded" % (vm, key, vms, verify[key]["GBps_coded"]))
+            # config 4's comparison: the 5 tokens as 5 m = 1 steps over the same layers (the headline step, timed above)
+            verify["five_m1_steps_ms"] = round(vm * ms_per_step, 4)
+            verify["fp16_x"]["over_five_m1_steps"] = round(verify["fp16_x"]["ms_per_step"] / (vm * ms_per_step), 3)
             del XV, YV
 
         # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
@@ -346,6 +453,8 @@ def main():
                 lib.lw_set_prefill_gemm(0)
                 prefill["runs"].append(run)
                 del XP, YP
+
+        configs = None if a.no_configs else further_configs(work)
 
         # packed-twin control: the same codes stored fixed-rate (pk4 / pk8), no decode chain; the achievable rate of
         # this access pattern and arithmetic without entropy decoding (the reference's pk4 baseline)
@@ -452,6 +561,7 @@ def main():
             "decode_only": decode_only,
             "verify_m5": verify,
             "prefill_path2": prefill,
+            "configs": configs,
         }
         print(json.dumps(res), flush=True)
         rt.close()
