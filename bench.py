@@ -10,7 +10,8 @@ seven GEMVs launched back to back (grouped per layer). value = algorithmic coded
 the algorithmic bytes of a GEMV are blob + side tensor + 2 K (x) + 4 m N (y) (the reference's own size
 accounting; device-layout padding is not credited).
 
-roofline: the dominant kernel (k_fused_flat, one grouped launch per layer that also sums the tile-column partials)
+roofline: the dominant kernel (k_fused_tiles: a tile per wave copied to LDS, 8 chains per lane; one grouped launch
+per layer that also sums the tile-column partials)
 timed with HIP events around each layer's launches on their stream; achieved = the layer's algorithmic bytes / mean
 duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view). traffic = HBM
 bytes per layer launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --profile`,
@@ -72,7 +73,7 @@ def counter_pass(counter, layers, tmp, timeout=240):
 
 
 def measure_traffic(layers):
-    """HBM bytes per full-layer k_fused_ring launch: calibrated FETCH_SIZE + WRITE_SIZE (see the module docstring)."""
+    """HBM bytes per full-layer fused launch: calibrated FETCH_SIZE + WRITE_SIZE (see the module docstring)."""
     tmp = tempfile.mkdtemp(prefix="lw_pmc_")
     try:
         res = {}
@@ -80,7 +81,8 @@ def measure_traffic(layers):
             rows = counter_pass(counter, layers, tmp)
             if not rows:
                 return None
-            ring = [v for k, vs in rows.items() if ("k_fused_ring" in k or "k_fused_flat" in k) for v in vs]
+            ring = [v for k, vs in rows.items() if any(n in k for n in ("k_fused_tiles", "k_fused_flat", "k_fused_ring"))
+                    for v in vs]
             copy = [v for k, vs in rows.items() if "copyBuffer" in k for v in vs]
             if not ring or not copy:
                 return None
@@ -550,7 +552,8 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic["bytes_per_layer_launch"] if traffic else None,
-                         "traffic_detail": traffic, "kernel": "k_fused_flat", "launch": "one grouped launch per layer",
+                         "traffic_detail": traffic, "kernel": "k_fused_tiles" if a.kernel_mode in (0, 6) else
+                         "k_fused_flat", "launch": "one grouped launch per layer",
                          "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
             "serial_per_matrix": {"ms_per_step": round(serial_ms, 4),
                                   "GBps": round(bytes_per_step / (serial_ms * 1e-3) / 1e9, 1)},

@@ -576,13 +576,15 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   }
   const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
   if (rows > 256) return 0;
-  int w = std::min(16, (160 * 1024 - tables) / (rows * 128));
-  if (w < 1) return 0;
-  if (w >= 4) w &= ~3;
+  const int wmax = std::min(16, (160 * 1024 - tables) / (rows * 128));
+  if (wmax < 1) return 0;
   per = (fp.ntiles + cus - 1) / cus;
   if (fp.n > 1) per = std::min(per, mintiles);
-  w = std::min(w, per);
-  return w;
+  // the fewest rounds of tiles the LDS allows, then the fewest waves that take the block's tiles in that many
+  // rounds: a last round with few waves busy leaves the CU idle for a whole tile (26 tiles per CU on 12 waves ran
+  // 12 + 12 + 2); the waves take tiles from a counter, so they need not spread evenly over the SIMDs
+  const int rounds = (per + wmax - 1) / wmax;
+  return std::min(wmax, (per + rounds - 1) / rounds);
 }
 
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
@@ -633,7 +635,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   const bool ring_ok = g_kernel_mode != 1;
   const bool flat = ring_ok && g_kernel_mode != 2 && (mt == 1 || (x8 && mt <= 8 && g_kernel_mode != 6));
   if (x8 && !flat) {
-    g_err = "int8 activations: a flat kernel mode (0, 3, 4, 5, or 6 for m = 1) and at most 8 tokens only";
+    g_err = "int8 activations: a flat kernel mode (0, 3, 4, 5, 7, or 6 for m = 1) and at most 8 tokens only";
     return -1;
   }
   for (int i = 0; x8 && mt > 1 && i < count; ++i)
@@ -731,7 +733,9 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       done[j] = 1;
     }
     fp.ntiles = total;
-    if (g_kernel_mode == 6) {  // the whole-tile kernel: every tile, the reduction in the launch
+    if (mt == 1 && (g_kernel_mode == 0 || g_kernel_mode == 6)) {
+      // the whole-tile kernel (the m = 1 default: faster than the ring kernel on every configuration measured):
+      // every tile, the reduction in the launch; the ring kernel where the tiles do not fit its LDS
       int rounds = 0;  // tiles per block
       fp.W = tiles_width(fp, mintiles, rounds);
       if (fp.W > 0) {
@@ -1546,7 +1550,7 @@ int lw_set_act8(int on) {
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 6) return -1;
+  if (mode < 0 || mode > 7) return -1;
   g_kernel_mode = mode;
   return 0;
 }

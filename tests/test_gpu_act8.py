@@ -148,7 +148,8 @@ def group(rt, names, xs, m=1):
 
 def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
     """One grouped m = 1 call over matrices of every size (one shared x, quantized once, and distinct ones): the
-    ring kernels (mode 5), the low-latency kernel (mode 4), the whole-tile kernel (mode 6) and the packed twin give the
+    default (the whole-tile kernel for m = 1, mode 0), the ring kernels (modes 5, 7), the low-latency kernel (mode 4),
+    the whole-tile kernel with one pass per token (mode 6) and the packed twin give the
     same bits, within
     tolerance of the oracle."""
     import torch
@@ -158,25 +159,25 @@ def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
         shared = torch.randn(1, mats[fmt][3]).half().cuda()
         xs = [shared, torch.randn(1, 512).half().cuda(), shared, torch.randn(1, 512).half().cuda()]
         runs = {}
-        for mode in (0, 4, 5, 6):
+        for mode in (0, 4, 5, 6, 7):
             assert lib.lw_set_kernel_mode(mode) == 0
             runs[mode] = group(rc, names, xs)
         lib.lw_set_kernel_mode(0)
         runs["packed"] = group(rp, names, xs)
         say("act8 kernels same bits", fmt)
-        for k in (0, 4, 5, 6, "packed"):
+        for k in (0, 4, 5, 6, 7, "packed"):
             for nm, x, y in zip(names, xs, runs[k]):
                 y8, _ = y_act8(orc, mats[nm], x.float().cpu().numpy())
                 check(y, y8, TOL_ACT8, "%s act8 grouped (%s)" % (nm, k))
-        for k in (4, 5, 6, "packed"):
+        for k in (4, 5, 6, 7, "packed"):
             for a, b in zip(runs[0], runs[k]):
                 assert np.array_equal(a, b), (fmt, k)
-        # m = 5 in one pass (modes 0, 4, 5) or one pass per token (mode 6, packed): every token the bits of its own
+        # m = 5 in one pass (modes 0, 4, 5, 7) or one pass per token (mode 6, packed): every token the bits of its own
         # m = 1 call
         x5 = [torch.randn(5, mats[nm][3]).half().cuda() for nm in names]
         ones = [group(rc, names, [x[j:j + 1].contiguous() for x in x5]) for j in range(5)]
         say("act8 m=5 grouped", fmt)
-        for mode in (0, 4, 5, 6):
+        for mode in (0, 4, 5, 6, 7):
             assert lib.lw_set_kernel_mode(mode) == 0
             y5 = group(rc, names, x5, 5)
             for i in range(len(names)):
@@ -191,7 +192,8 @@ def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
 
 def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
     """Matrices with exception tiles (32-row schedules decoded in place or by the one-wave pass; tiles without a
-    ring schedule by the low-latency kernel; every tile by the whole-tile kernel): modes 0, 3-6 the same bits, within tolerance of the oracle."""
+    ring schedule by the low-latency kernel; every tile by the whole-tile kernel): modes 0, 3-7 the same bits, within
+    tolerance of the oracle."""
     import torch
     from lazyweights_amd import Runtime
     from lazyweights_amd.bundle import Writer
@@ -205,19 +207,19 @@ def test_gpu_act8_exception_tiles(gpu, tmp_path, orc, lib, act8):
         x = torch.randn(1, 8192).half().cuda()
         for nm, (codes, side) in cases.items():
             runs = {}
-            for mode in (0, 3, 4, 5, 6):
+            for mode in (0, 3, 4, 5, 6, 7):
                 assert lib.lw_set_kernel_mode(mode) == 0
                 runs[mode] = group(rt, [nm], [x])[0]
             lib.lw_set_kernel_mode(0)
             say("act8 exception tiles", nm)
-            for mode in (3, 4, 5, 6):
+            for mode in (3, 4, 5, 6, 7):
                 assert np.array_equal(runs[0], runs[mode]), (nm, mode)
             q, d, s = orc.quant_x8(x.float().cpu().numpy())
             check(runs[0], orc.gemv_act8_f64(2, codes, side, q, d, s), TOL_ACT8, nm + " act8")
-            # 4 tokens in one pass (modes 0, 3-5; mode 6 one pass per token): the bits of m = 1 calls
+            # 4 tokens in one pass (modes 0, 3-5, 7; mode 6 one pass per token): the bits of m = 1 calls
             x4 = torch.randn(4, 8192).half().cuda()
             ones = [group(rt, [nm], [x4[j:j + 1].contiguous()])[0][0] for j in range(4)]
-            for mode in (0, 3, 4, 5, 6):
+            for mode in (0, 3, 4, 5, 6, 7):
                 assert lib.lw_set_kernel_mode(mode) == 0
                 y4 = group(rt, [nm], [x4], 4)[0]
                 for j in range(4):

@@ -446,15 +446,16 @@ def test_gpu_exception_tiles_in_place(gpu, tmp_path, orc):
             return [y.cpu().numpy() for y in ys]
 
         runs = {}
-        for mode in (0, 3):
+        for mode in (7, 3, 0):  # ring with exceptions in place, ring with the exception pass, whole-tile kernel
             assert rt.lib.lw_set_kernel_mode(mode) == 0
             try:
                 say("in-place exceptions: mode %d" % mode)
                 runs[mode] = group(["mskew"], [X[:1]]) + group(["small", "mskew"], [xs, X[:1]])
             finally:
                 rt.lib.lw_set_kernel_mode(0)
-        for a, b in zip(runs[0], runs[3]):
-            assert np.array_equal(a, b)
+        for k in (3, 0):
+            for a, b in zip(runs[7], runs[k]):
+                assert np.array_equal(a, b), k
         check_err(runs[0][0], y64[:1], "in-place exceptions alone")
         check_err(runs[0][1], ys64, "in-place exceptions grouped: small")
         check_err(runs[0][2], y64[:1], "in-place exceptions grouped")
@@ -510,9 +511,9 @@ def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):
 
 
 def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
-    """The whole-tile flat kernel (a tile per wave in LDS, 4 chains per lane; mode 6) gives the ring kernels' bits
-    (mode 5) for every format, for single matrices and groups spanning several matrices (blocks over two tables),
-    and for matrices with exception tiles, which it decodes like any other tile."""
+    """The whole-tile flat kernel (a tile per wave in LDS, 8 chains per lane; the m = 1 default, mode 0) gives the
+    ring kernels' bits (mode 5) for every format, for single matrices and groups spanning several matrices (blocks over
+    two tables), and for matrices with exception tiles, which it decodes like any other tile."""
     import ctypes
 
     import torch
@@ -539,10 +540,11 @@ def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
         for names in ([fmt], [fmt + "_small"], [fmt + "_small", fmt, fmt + "_small"]):
             X = [torch.randn(1, mats[nm][3]).half() for nm in names]
             xs = [x.cuda() for x in X]
-            a, b = run(rt, names, xs, 6), run(rt, names, xs, 5)
+            a, b, c = run(rt, names, xs, 0), run(rt, names, xs, 5), run(rt, names, xs, 7)
             say("whole-tile flat kernel", fmt, len(names))
-            for nm, x, ya, yb in zip(names, X, a, b):
+            for nm, x, ya, yb, yc in zip(names, X, a, b, c):
                 assert torch.equal(ya, yb), nm
+                assert torch.equal(ya, yc), nm
                 _, y64 = reference_y(orc, mats[nm], x.double().numpy())
                 check_err(ya.numpy(), y64, "%s whole-tile kernel" % nm)
     w = Writer(str(tmp_path))
@@ -553,9 +555,10 @@ def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
     with Runtime(tmp_path) as rt2:
         x = torch.randn(1, 8192).half()
         for nm, (codes, side) in cases.items():
-            a, b = run(rt2, [nm], [x.cuda()], 6), run(rt2, [nm], [x.cuda()], 5)
+            a, b, c = run(rt2, [nm], [x.cuda()], 0), run(rt2, [nm], [x.cuda()], 5), run(rt2, [nm], [x.cuda()], 7)
             say("whole-tile flat kernel, exception tiles", nm)
             assert torch.equal(a[0], b[0]), nm
+            assert torch.equal(a[0], c[0]), nm
             check_err(a[0].numpy(), orc.gemv_f64(orc.dequant(2, codes, side), x.double().numpy()), nm)
 
 
