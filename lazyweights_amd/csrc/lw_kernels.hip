@@ -1645,13 +1645,17 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     const int u = T - e->tile0, NT = e->M.NT, KT = e->M.KT;
     t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : (u % NT) * KT + u / NT);
   };
-  // the tile's rows (and the 2 the last windows read past the longest lane) into the wave's buffer, 8 rows per
-  // copy instruction; the per-tile words are read through the scalar cache (read-only during the launch)
+  // the tile's rows into the wave's buffer, 8 rows per copy instruction (lane l: row l / 8, words 4 (l % 8) ..),
+  // the last one masked to the tile's own rows. The windows also read the 2 rows past the longest lane and the
+  // table index takes up to 11 bits past a code's start: those rows keep whatever the buffer held, which no decoded
+  // symbol depends on (every code lies within its lane's bits, a prefix code's entry ignores the bits after it).
+  // The per-tile words are read through the scalar cache (read-only during the launch).
   auto copy_tile = [&](KEntry* e, int t) {
-    const int nrow = (int)((KU16*)e->M.rows)[t] + 2;
+    const int nrow = (int)((KU16*)e->M.rows)[t];
     const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
     for (int i = 0; i < (nrow + 7) / 8; ++i)
-      __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+      if (lane < 8 * (nrow - 8 * i))
+        __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
   };
   // The in-launch reduction of a tile's row is deferred behind the next tile's copy and decode: its partial is
   // stored, and after the next copy's wait (which also covers the store) the row counter is incremented; the
