@@ -76,6 +76,9 @@ struct FlatEntry {
   const float* SX;
   // plan.mt > 1: P is [KT][mt][N] and token j's Y row starts at Y + j ldy
   int ldy;
+  // the matrix-core whole-tile kernel (fp16 activations, 2..8 tokens): per token and sub-block of 32 weights the
+  // sum of x as fp16 hi | lo << 16 ([mt][K / 32], launch_xsums16)
+  const uint32_t* XS;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];
@@ -115,6 +118,19 @@ int split_stage_rows(const FlatPlan& plan);
 // and the in-launch reduction for entries with Y
 hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
 int tiles_buf_rows(const FlatPlan& plan);
+// The whole-tile kernel for 2..8 tokens of fp16 activations (Q4_K / Q5_K, plan.mt tokens, entries' XS set): the
+// products on the matrix cores (4x4x4 blocks, x broadcast from one block), every token in one pass over the tiles
+hipError_t launch_fused_tiles_mma(const FlatPlan& plan, int per, hipStream_t s);
+// XS [m][K / 32] for launch_fused_tiles_mma: per token and sub-block the fp32 sum of X [m][K] (fp16) in quarter
+// order (q0 + q1) + (q2 + q3), as fp16 hi | fp16(sum - hi) << 16; up to MAX_GROUP matrices' x in one launch
+struct XSumJobs {
+  const uint32_t* X[MAX_GROUP];
+  uint32_t* XS[MAX_GROUP];
+  int K[MAX_GROUP];
+  int b0[MAX_GROUP];  // set by the launcher
+  int n, m;
+};
+hipError_t launch_xsums16(const XSumJobs& jobs, hipStream_t s);
 
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
 // K-quant types or ring sizes, or a matrix has no ring schedule).

@@ -15,6 +15,7 @@
 //   * partial sums per tile column go to P[tc][j][n] and are summed in tile-column order by k_reduce
 //     (deterministic, as the reference's k_sum_kt, llmrt.cu:1171-1180).
 #include <hip/hip_runtime.h>
+#include <type_traits>
 
 #include "lw_format.h"
 #include "lw_kernels.h"
@@ -1877,6 +1878,366 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   }
 }
 
+// ── whole-tile kernel on the matrix cores (2..8 tokens, fp16 activations, Q4_K / Q5_K) ─────────────────────
+// The decode of k_fused_tiles (a tile per wave in LDS, 8 chains per lane), with the products of MT tokens on
+// v_mfma_f32_4x4x4f16 (16 blocks of 4 lanes): block b computes D[i][j] = sum_k A[4 b' + i][k] B[4 b + j][k] into lane
+// 4 b + j, register i, where b' is the block named by the instruction's broadcast field (cbsz 4, abid b'). B = the
+// lane's own 4 weights of the pair (its row), A = the 4 x values of token i at those positions, broadcast from block
+// b' of a register that holds 16 position blocks: x of a tile column fits 8 (4-bit formats) or 4 register pairs per
+// 4 tokens, with no LDS traffic. The weights enter as sc q (Q5_K: fp16(q) sc; Q4_K: sc q / 16 from the 0x54 byte
+// permute and one fma, every step exact), so one accumulator per super-block and 4 tokens suffices; d (x 16 for
+// Q4_K) applies once per super-block. The mins term dmin sum_j m_j (sum x)_j runs on the same instruction with
+// A = the sub-block sums of x as fp16 hi and lo (XS) and B = the row's mins. Each token's values agree with its own
+// m = 1 launch to fp32 rounding (another order of the same products). Partials [KT][mt][N], the in-launch reduction.
+// at most 12 waves per block: the tile buffers leave room for no more per CU, and the register budget of 3 waves per
+// SIMD holds the 8 chains with 8 tokens' x and accumulators without spilling
+constexpr int TILES_MMA_WAVES = 12;
+
+// compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1 (indices that must be constants: MFMA
+// broadcast fields, register-array indices)
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_from(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_from<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_from<0, N>(f);
+}
+
+// v_mfma_f32_4x4x4f16 over 16 blocks with A broadcast from block ABID
+template <int ABID>
+__device__ __forceinline__ f4v mfma4_from(h4v a, h4v b, f4v c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 4, ABID, 0);
+}
+
+template <int KQ, int NTAB, int MT>
+__global__ void __launch_bounds__(64 * TILES_MMA_WAVES, 1)
+k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
+  static_assert(KQ == KQ_Q4_K || KQ == KQ_Q5_K, "scaled codes are exact in fp16 for Q4_K / Q5_K only");
+  static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int SB = kq_sbytes(KQ);
+  constexpr int NSB = TW / 256;   // super-blocks per tile row
+  constexpr int NQ = MT / 4;      // token quads
+  constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
+  constexpr int NC = 8, NG = 2;   // chains per lane, 16-symbol groups per chain
+  constexpr float DSCALE = SYMB == 4 ? 16.f : 1.f;
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  typedef __attribute__((address_space(4))) const uint16_t KU16;
+  __shared__ uint32_t lut4[NTAB * LUTN + 4];
+  extern __shared__ __align__(16) uint32_t tbuf[];
+
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * per, Tl = min(T0 + per, plan.ntiles) - 1, mt = plan.mt;
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  {
+    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.lut4);
+    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.lut4);
+    for (int i = threadIdx.x; i < LUTN / 4; i += W * 64) {
+      reinterpret_cast<uint4*>(lut4)[i] = ta[i];
+      if (NTAB > 1 && mb != ma) reinterpret_cast<uint4*>(lut4 + LUTN)[i] = tb[i];
+    }
+  }
+  uint32_t* next = lut4 + NTAB * LUTN;
+  if (threadIdx.x == 0) *next = (uint32_t)W;
+  __syncthreads();
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
+  const int qb = lane >> 2, qi = lane & 3;  // 4-lane block and the lane's place in it
+  uint32_t* buf = tbuf + (size_t)wave * buf_rows * 32;
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+  auto tile_of = [&](int n, int& sec, int& t) {
+    const int T = T0 + n;
+    sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
+    KEntry* e = sec ? eb : ea;
+    const int u = T - e->tile0, NT = e->M.NT, KT = e->M.KT;
+    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : (u % NT) * KT + u / NT);
+  };
+  auto copy_tile = [&](KEntry* e, int t) {  // as k_fused_tiles: the tile's own rows, the last copy masked
+    const int nrow = (int)((KU16*)e->M.rows)[t];
+    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+    for (int i = 0; i < (nrow + 7) / 8; ++i)
+      if (lane < 8 * (nrow - 8 * i))
+        __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+  };
+  int pend = -1;
+  int ptr = 0, pKT = 0, pN = 0;
+  uint32_t pold = 0;
+  auto finish_pending = [&]() {
+    if (pend < 0) return;
+    const uint32_t old = (uint32_t)__builtin_amdgcn_readlane((int)pold, 0);
+    if (old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
+    pend = -1;
+  };
+  int n = wave;
+  bool have = n < per && T0 + n < plan.ntiles;
+  int sec = 0, t = 0;
+  if (have) {
+    tile_of(n, sec, t);
+    copy_tile(sec ? eb : ea, t);
+  }
+#pragma unroll 1
+  while (have) {
+    const bool second = sec != 0;
+    KEntry* ep = second ? eb : ea;
+    const auto& E = *ep;
+    const auto& M = E.M;
+    const int KT = M.KT, N = M.N, K = M.K;
+    const int tc = t % KT, tr = t / KT;
+    const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+    uint32_t sw[NSB][5];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+    uint32_t P[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS + 64u;
+    const uint32_t tsel = second ? 4u * LUTN : 0u;
+    // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
+    // (zero for tokens >= mt); XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks, block b = (super-block,
+    // half, hi / lo) as 2 (2 sb + half) + (lo)
+    h4v xa[NQ][NPR], xs[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int tok = 4 * q + qi;
+      const bool ok = tok < mt;
+      const uint32_t* xrow = E.X2 + (size_t)(ok ? tok : 0) * (K / 2) + (size_t)tc * (TW / 2);
+#pragma unroll
+      for (int m = 0; m < NPR; ++m) {
+        const uint2 v = ok ? *reinterpret_cast<const uint2*>(xrow + 2 * (16 * m + qb)) : make_uint2(0u, 0u);
+        xa[q][m] = __builtin_bit_cast(h4v, v);
+      }
+      const int cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
+      uint2 sv = make_uint2(0u, 0u);
+      if (ok && qb < 4 * NSB) {
+        const uint32_t* xsr = E.XS + (size_t)tok * (K / 32) + (size_t)tc * (TW / 32) + 4 * sh;
+        const uint4 w4 = *reinterpret_cast<const uint4*>(xsr);
+        const uint32_t a0 = lo ? w4.x >> 16 : w4.x & 0xFFFFu, a1 = lo ? w4.y >> 16 : w4.y & 0xFFFFu;
+        const uint32_t a2 = lo ? w4.z >> 16 : w4.z & 0xFFFFu, a3 = lo ? w4.w >> 16 : w4.w & 0xFFFFu;
+        sv = make_uint2(a0 | a1 << 16, a2 | a3 << 16);
+      }
+      xs[q] = __builtin_bit_cast(h4v, sv);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
+    if (pend >= 0 && lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t slot[NC], A[NC], B[NC], C[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+      C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+    }
+    // the lane's sub-block scales (bytes, low first) per super-block
+    uint64_t scq[NSB];
+    float dA[NSB], dB[NSB];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      uint64_t q2;
+      side_packed<KQ>(sw[sb], scq[sb], q2, dA[sb], dB[sb]);
+    }
+    f4v acc[NSB][NQ];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) acc[sb][q] = f4v{0.f, 0.f, 0.f, 0.f};
+    uint32_t wprev[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) wprev[j] = 0;
+    static_for<NG>([&](auto gic) {
+      constexpr int gi = decltype(gic)::value;
+      // the scale of each chain's current sub-block as an fp16 pair (and -64 sc for the 4-bit form)
+      h2v scv[NC], nsc[NC];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        const int js = SYMB == 4 ? 2 * j + gi : j;  // sub-block within the tile row
+        const _Float16 v = (_Float16)(float)(uint32_t)((scq[js / 8] >> (8 * (js % 8))) & 255u);
+        scv[j] = h2v{v, v};
+        nsc[j] = scv[j] * h2v{(_Float16)-64.f, (_Float16)-64.f};
+      }
+      static_for<8>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        uint32_t w1[NC], e1[NC], e2[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
+          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          P[j] = P[j] + e1[j] + e2[j];
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+          const bool slide = nslot != slot[j];
+          A[j] = slide ? B[j] : A[j];
+          B[j] = slide ? C[j] : B[j];
+          slot[j] = nslot;
+          C[j] = *(LdsU32*)(rlb + (nslot << 7));
+        }
+        static_for<NC>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          if constexpr (SYMB == 4) {  // 4 codes: sc q / 16 each, in weight order
+            const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, e1[j], 0x04030402u));
+            const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, e2[j], 0x04030402u));
+            const uint2 wv = make_uint2(__builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(a, scv[j], nsc[j])),
+                                        __builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(b, scv[j], nsc[j])));
+            constexpr int pb = 16 * j + 8 * gi + p;  // position block of the 4 weights within the tile row
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+              acc[j / 4][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[j / 4][q]);
+          } else {  // 2 codes per pair (fp16(q) in the entries' upper halves), 4 per product
+            const uint32_t v = __builtin_bit_cast(uint32_t, (h2v)(__builtin_bit_cast(h2v, __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u)) * scv[j]));
+            if constexpr (p & 1) {
+              constexpr int pb = 8 * j + 4 * gi + p / 2;
+#pragma unroll
+              for (int q = 0; q < NQ; ++q)
+                acc[0][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[0][q]);
+            } else {
+              wprev[j] = v;
+            }
+          }
+        });
+      });
+    });
+    // mins: per super-block and token, sum_j m_j (sum x)_j from the hi and lo halves of the sums
+    f4v mac[NSB][NQ];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      float mf[8];
+      side_mins(sw[sb], mf);
+      const h4v m0 = h4v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3]};
+      const h4v m1 = h4v{(_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        f4v r = {0.f, 0.f, 0.f, 0.f};
+        if (sb == 0) {
+          r = mfma4_from<0>(xs[q], m0, r);
+          r = mfma4_from<1>(xs[q], m0, r);
+          r = mfma4_from<2>(xs[q], m1, r);
+          r = mfma4_from<3>(xs[q], m1, r);
+        } else {
+          r = mfma4_from<4>(xs[q], m0, r);
+          r = mfma4_from<5>(xs[q], m0, r);
+          r = mfma4_from<6>(xs[q], m1, r);
+          r = mfma4_from<7>(xs[q], m1, r);
+        }
+        mac[sb][q] = r;
+      }
+    }
+    float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float tot = 0.f;
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) tot = fmaf(dA[sb] * DSCALE, acc[sb][q][i], fmaf(-dB[sb], mac[sb][q][i], tot));
+        if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    finish_pending();
+    if (E.Y) {
+      pend = sec;
+      ptr = tr;
+      pKT = KT;
+      pN = N;
+    }
+    uint32_t nx = 0;
+    if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    n = __builtin_amdgcn_readfirstlane((int)nx);
+    have = n < per && T0 + n < plan.ntiles;
+    if (have) {
+      tile_of(n, sec, t);
+      copy_tile(sec ? eb : ea, t);
+    }
+  }
+  if (pend >= 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finish_pending();
+  }
+}
+
+// per token and sub-block of 32 weights: fp32 sum of fp16 x in quarter order, as fp16 hi | lo << 16; one launch
+// over up to MAX_GROUP jobs (blocks [b0[i], b0[i + 1]) take job i)
+__global__ void __launch_bounds__(256) k_xsums16(XSumJobs jobs) {
+  int jb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i)
+    if (i < jobs.n && (int)blockIdx.x >= jobs.b0[i]) jb = i;
+  const uint32_t* __restrict__ X2 = jobs.X[jb];
+  uint32_t* __restrict__ XS = jobs.XS[jb];
+  const int m = jobs.m, K = jobs.K[jb];
+  const int i = ((int)blockIdx.x - jobs.b0[jb]) * 256 + threadIdx.x;
+  if (i >= m * (K / 32)) return;
+  const int tk = i / (K / 32), j = i - tk * (K / 32);
+  const uint32_t* x = X2 + (size_t)tk * (K / 2) + 16 * j;
+  float q[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q[k] = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t v = x[4 * k + c];
+      q[k] += h2f(v) + h2f(v >> 16);
+    }
+  }
+  const float sum = (q[0] + q[1]) + (q[2] + q[3]);
+  const _Float16 hi = (_Float16)sum;
+  XS[i] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(sum - (float)hi)) << 16;
+}
+
+hipError_t launch_xsums16(const XSumJobs& jobs, hipStream_t s) {
+  if (jobs.n < 1 || jobs.n > MAX_GROUP || jobs.m < 1) return hipErrorInvalidValue;
+  XSumJobs q = jobs;
+  int blocks = 0;
+  for (int i = 0; i < q.n; ++i) {
+    if (q.K[i] % 32) return hipErrorInvalidValue;
+    q.b0[i] = blocks;
+    blocks += (q.m * (q.K[i] / 32) + 255) / 256;
+  }
+  hipLaunchKernelGGL(k_xsums16, dim3(blocks), dim3(256), 0, s, q);
+  return hipGetLastError();
+}
+
+template <int KQ, int NTAB, int MT>
+static hipError_t tiles_mma_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  const size_t smem = (size_t)p.W * buf_rows * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles_mma<KQ, NTAB, MT>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  const int blocks = (p.ntiles + per - 1) / per;
+  hipLaunchKernelGGL((k_fused_tiles_mma<KQ, NTAB, MT>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
+  return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t tiles_mma_launch(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  const bool one = p.n == 1;
+  if (p.mt <= 4) return one ? tiles_mma_launch_t<KQ, 1, 4>(p, per, buf_rows, s) : tiles_mma_launch_t<KQ, 2, 4>(p, per, buf_rows, s);
+  return one ? tiles_mma_launch_t<KQ, 1, 8>(p, per, buf_rows, s) : tiles_mma_launch_t<KQ, 2, 8>(p, per, buf_rows, s);
+}
+
 template <int KQ, int NTAB, bool I8>
 static hipError_t tiles_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128;
@@ -1923,6 +2284,25 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
     case KQ_IQ4_XS: return tiles_launch<KQ_IQ4_XS>(p, per, rows, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > TILES_MMA_WAVES || per < p.W || p.ntiles < 1 || p.mt < 1 ||
+      p.mt > 8 || p.i8)
+    return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  if (kqt != KQ_Q4_K && kqt != KQ_Q5_K) return hipErrorInvalidValue;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || e.M.packed || !e.XS || e.tile0 + e.ntile != end ||
+        e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
+        (i == 0 && e.tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  const int rows = tiles_buf_rows(p);
+  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  return kqt == KQ_Q4_K ? tiles_mma_launch<KQ_Q4_K>(p, per, rows, s) : tiles_mma_launch<KQ_Q5_K>(p, per, rows, s);
 }
 
 template <int KQ, int RS, int NTAB, bool I8, int MT = 1>

@@ -187,9 +187,10 @@ def test_gpu_fused_fp16_x_device(fmt_rt, orc, kqt, fmt, H):
 
 
 def test_gpu_verify_gemm_equals_repeated_gemv(fmt_rt, orc):
-    """One m = 5 launch (products on the matrix cores) against five m = 1 launches (v_dot2): the same values up
-    to fp32 rounding (2e-6 of max |y|), both within tolerance of fp64; tokens are independent (token 0 alone in
-    an m = 5 launch with zeroed others gives the same bits as in the full launch)."""
+    """One m = 5 launch (products on the matrix cores, sub-block scales folded into the weights: the same products
+    summed in another order) against five m = 1 launches (v_dot2): the same values up to the fp32 rounding of a
+    K-term sum (5e-6 of max |y|), both within tolerance of fp64; tokens are independent (token 0 alone in an m = 5
+    launch with zeroed others gives the same bits as in the full launch)."""
     import torch
     rt, mats = fmt_rt
     for kqt, fmt, H in FORMATS:
@@ -206,9 +207,12 @@ def test_gpu_verify_gemm_equals_repeated_gemv(fmt_rt, orc):
         Y0 = torch.zeros(5, N, device="cuda")
         rt.matmul_dev(fmt, X0, Y0)
         torch.cuda.synchronize()
-        say("verify vs 5 x gemv", fmt)
         a, b = Y5.cpu().numpy(), Y1.cpu().numpy()
-        assert np.abs(a - b).max() <= 2e-6 * np.abs(b).max(), (fmt, np.abs(a - b).max() / np.abs(b).max())
+        _, y64 = reference_y(orc, mats[fmt], X.double().numpy())
+        say("verify vs 5 x gemv", fmt, "diff %.3g" % (np.abs(a - b).max() / np.abs(b).max()))
+        check_err(a, y64, fmt + " m=5 in one launch")
+        check_err(b, y64, fmt + " m=5 as five m=1 launches")
+        assert np.abs(a - b).max() <= 5e-6 * np.abs(b).max(), (fmt, np.abs(a - b).max() / np.abs(b).max())
         assert torch.equal(Y0[0], Y5[0])
         _, y64 = reference_y(orc, mats[fmt], X.double().numpy())
         check_err(a, y64, fmt + " m=5")
@@ -312,7 +316,7 @@ def test_full_config1_layer(gpu, tmp_path):
 def test_full_config4_q4k_verify(gpu, tmp_path):
     """Config 4's Q4_K half: the Mistral-shaped layer (H = 2.3) verified with m = 5 tokens as one grouped call, each
     matrix against fp64 (the contract) and against five m = 1 calls token by token (fp32 rounding: the m = 5 kernel
-    forms its products on the matrix cores in another order)."""
+    forms its products on the matrix cores in another order; 5e-6 of max |y|)."""
     import torch
     from lazyweights_amd import Runtime, bundle
     from lazyweights_amd.configs import CONFIG4
@@ -333,7 +337,7 @@ def test_full_config4_q4k_verify(gpu, tmp_path):
             name, kqt, N, K, H, seed = mat
             a, b = y5[name].cpu().numpy(), y1[name].cpu().numpy()
             say("config 4", name, "m=5 vs 5 x m=1: %.3g" % (np.abs(a - b).max() / np.abs(b).max()))
-            assert np.abs(a - b).max() <= 2e-6 * np.abs(b).max(), name
+            assert np.abs(a - b).max() <= 5e-6 * np.abs(b).max(), name
             codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
             y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X[name].double().numpy())
             check_err(a, y64, "config 4 %s m=5" % name)
@@ -592,12 +596,21 @@ def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
             assert torch.equal(a, b), name
             codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
             assert np.array_equal(rp.test_decode(name), codes)
+            # m = 5: the ring kernel (mode 7) gives the packed twin's bits; the default for Q4_K / Q5_K (the
+            # matrix-core whole-tile kernel) the same values up to the fp32 order of its sums
             X5 = torch.randn(5, K).half().cuda()
-            y5c, y5p = torch.zeros(5, N, device="cuda"), torch.zeros(5, N, device="cuda")
-            rc.matmul_dev(name, X5, y5c)
+            y5c, y5p, y5d = (torch.zeros(5, N, device="cuda") for _ in range(3))
+            assert rc.lib.lw_set_kernel_mode(7) == 0
+            try:
+                rc.matmul_dev(name, X5, y5c)
+            finally:
+                rc.lib.lw_set_kernel_mode(0)
             rp.matmul_dev(name, X5, y5p)
+            rc.matmul_dev(name, X5, y5d)
             torch.cuda.synchronize()
             assert torch.equal(y5c, y5p), name
+            a5, b5 = y5d.cpu().numpy(), y5p.cpu().numpy()
+            assert np.abs(a5 - b5).max() <= 5e-6 * np.abs(b5).max(), name
             X3 = np.random.default_rng(kqt).standard_normal((3, K)).astype(np.float32)
             yc, yp = rc.test_matmul(name, X3), rp.test_matmul(name, X3)
             assert np.array_equal(yc, yp), name
