@@ -56,6 +56,95 @@ def _compile(src, kind):
     return obj
 
 
+OBJDUMP = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", "llvm-objdump")
+
+
+def _vregs(op):
+    """VGPR numbers named by one operand (v5, v[4:7]); empty for anything else."""
+    import re
+    m = re.match(r"v\[(\d+):(\d+)\]$", op)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", op)
+    return {int(m.group(1))} if m else set()
+
+
+def dpp_violations(disasm):
+    """DPP operations in an llvm-objdump disassembly of gfx950 code without their wait states: 2 after a VALU write
+    of the DPP source (src0), 5 after a write of EXEC. The walk goes back over the operation's basic block (branch
+    targets and function starts end it); at a block start the predecessor is unknown, so 5 wait states (s_nop) must
+    lie inside the block. Returns "function at 0xaddr" strings."""
+    import re
+    fn, base = "?", 0
+    ins, targets = [], set()
+    for line in disasm.splitlines():
+        m = re.match(r"([0-9a-f]+) <(.+)>:$", line)
+        if m:
+            fn, base = m.group(2), int(m.group(1), 16)
+            ins.append(None)  # function boundary
+            continue
+        m = re.match(r"\s+(\S+)\s*(.*?)\s*//\s*([0-9A-F]+):", line)
+        if not m:
+            continue
+        t = re.search(r"<(.+)\+0x([0-9a-f]+)>", line)
+        if t:
+            targets.add(base + int(t.group(2), 16))
+        ops = [o.strip() for o in m.group(2).split(",")] if m.group(2) else []
+        ins.append((int(m.group(3), 16), m.group(1), ops, fn))
+    bad = []
+    for i, it in enumerate(ins):
+        if it is None or "_dpp" not in it[1]:
+            continue
+        src = _vregs(it[2][1]) if len(it[2]) > 1 else set()
+        waits, j, ok = 0, i - 1, False
+        while True:
+            if j < 0 or ins[j] is None or ins[j + 1][0] in targets:  # the block starts at j + 1
+                ok = waits >= 5
+                break
+            mn, ops = ins[j][1], ins[j][2]
+            if mn.startswith("s_nop"):
+                waits += (int(ops[0], 0) if ops else 0) + 1
+            else:
+                if ops and ((mn.startswith("v_") and (_vregs(ops[0]) & src) and waits < 2) or
+                            (ops[0].startswith("exec") and waits < 5)):
+                    break
+                waits += 1
+            if waits >= 5:
+                ok = True
+                break
+            j -= 1
+        if not ok:
+            bad.append("%s at 0x%x" % (it[3], it[0]))
+    return bad
+
+
+def check_dpp_hazards(lib):
+    """The DPP operations of the built code objects (the v_dot2c_f32_f16_dpp broadcasts, written as inline assembly,
+    which the compiler's hazard recognizer does not see) must have their wait states (dpp_violations). The check
+    disassembles this build's own gfx950 code objects; raises RuntimeError naming each violation."""
+    import tempfile
+    if not os.path.exists(OBJDUMP):
+        raise RuntimeError("build: %s not found (needed to check DPP wait states)" % OBJDUMP)
+    tmp = tempfile.mkdtemp(prefix="lw_dpp_")
+    try:
+        shutil.copy(lib, os.path.join(tmp, "l.so"))
+        subprocess.run([OBJDUMP, "--offloading", "l.so"], cwd=tmp, stdout=subprocess.DEVNULL,
+                       stderr=subprocess.DEVNULL, check=True)
+        objs = [f for f in os.listdir(tmp) if "amdgcn" in f and ARCH in f]
+        if not objs:
+            raise RuntimeError("build: no %s code object found in %s" % (ARCH, lib))
+        bad = []
+        for obj in objs:
+            out = subprocess.run([OBJDUMP, "-d", "--mcpu=" + ARCH, os.path.join(tmp, obj)], stdout=subprocess.PIPE,
+                                 stderr=subprocess.DEVNULL, text=True, check=True).stdout
+            bad += dpp_violations(out)
+        if bad:
+            raise RuntimeError("build: DPP operations without their wait states: " + ", ".join(bad[:8]))
+        return len(objs)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def build(verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
@@ -63,6 +152,7 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs +
          ["-L" + ROCM_LIB, "-lrocblas", "-pthread", "-lm"])
+    check_dpp_hazards(tmp)
     os.replace(tmp, LIB)
     if verbose:
         print("built", LIB)

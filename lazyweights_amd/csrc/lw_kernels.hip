@@ -1544,11 +1544,13 @@ hipError_t launch_fused_split(const FlatPlan& p, hipStream_t s) {
 }
 
 // acc += dot2(x, w) with x = lane k of the lane's 16-lane row of xrow (DPP row_newbcast: x held the same in every
-// row, so the broadcast costs no v_readlane). The s_nop gives the DPP source the wait states it needs after a VALU
-// write, whatever the compiler placed before the statement (xrow itself comes from loads).
+// row, so the broadcast costs no v_readlane). xrow comes from loads, so no VALU write precedes the DPP read; the
+// compiler does not see the DPP inside the assembly, so the build disassembles its own code objects and refuses any
+// DPP operation with fewer than the required wait states (lazyweights_amd/build.py, check_dpp_hazards). A form the
+// compiler can see (update_dpp + fdot2) is not folded into one instruction: a v_mov_b32_dpp per product.
 template <int K>
 __device__ __forceinline__ void dot2_bcast(float& acc, uint32_t xrow, uint32_t w) {
-  asm("s_nop 1\n\tv_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+  asm("v_dot2c_f32_f16_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
       : "+v"(acc)
       : "v"(xrow), "v"(w), "n"(K));
 }
