@@ -1575,17 +1575,41 @@ __device__ __forceinline__ void dot2_row(float& acc, uint32_t xrow, int k, uint3
   }
 }
 
-// ── whole-tile kernel for flat launches (m = 1): a tile per wave, 4 chains per lane ───────────────────────
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 32] (the count is an immediate: one wait per value). The
+// compiler does not see which value ran, so it still waits for every vector load whose result a later
+// instruction reads; this is for loads whose results only LDS reads see (direct-to-LDS copies).
+template <int N = 32>
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  if constexpr (N == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (n >= N) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    else wait_vmcnt_upto<N - 1>(n);
+  }
+}
+
+// ── whole-tile kernel for flat launches (m = 1): a tile per wave, 8 chains per lane ───────────────────────
+// the most tile copies a block of the whole-tile kernel keeps in flight (measured on config 2: 3-6 alike, 2-4 %
+// faster than one per wave)
+#ifndef LW_TILES_COPIES
+#define LW_TILES_COPIES 4
+#endif
+constexpr int TILES_COPIES = LW_TILES_COPIES;
 // Block = W waves sharing the decode tables; the block decodes tiles [T0, T0 + per) (spanning at most two
-// matrices), wave w first tile T0 + w, then the next undecoded one from a counter in LDS, so each SIMD takes
-// tiles at its own rate.
+// matrices; a matrix's tiles in row-major order), wave w first tile T0 + w, then the next undecoded one from a
+// counter in LDS, so each SIMD takes tiles at its own rate. The tables arrive by direct-to-LDS loads issued
+// ahead of the waves' first tile copies, so a wave waits only for those before the block's barrier; at most
+// TILES_COPIES copies are in flight per block. The next tile's copy is issued as soon as a decode ends, before
+// the row partial is formed; the tiles' row counts and word offsets, read at that point, were brought into the
+// scalar cache at the start.
 // A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
 // lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 8 chains of 32 symbols that start at the
 // load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
 // chain keeps its window rows in registers and reads one new row word per pair (LDS instruction issue, about 4
 // cycles per wave-wide read, is what a tile costs: 2 table gathers and 1 row read per pair).
-// There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here. The lane keeps its row's sub-block dot products in registers and forms the row
-// partial in tile_gemv's order (tile_gemv_i8's for int8 activations), the bits of the other kernels.
+// There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here.
+// The lane keeps its row's sub-block dot products in registers and forms the row partial in tile_gemv's order
+// (tile_gemv_i8's for int8 activations), the bits of the other kernels.
 // (at most 16 waves per CU by the LDS of the tile buffers: 4 per SIMD, so the scheduler may spend up to 128 VGPRs on
 // keeping the 8 chains' reads in flight)
 template <int KQ, int NTAB, bool I8>
@@ -1608,7 +1632,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   typedef __attribute__((address_space(4))) const float KF32;
   typedef __attribute__((address_space(4))) const uint16_t KU16;
   // one static LDS object at address 0, so the tables sit at 0 and 8 KB (table_addr ORs its base into the index);
-  // the block's tile counter after them
+  // the block's tile counter and copy counters after them
   __shared__ uint32_t lut4[NTAB * LUTN + 4];
   extern __shared__ __align__(16) uint32_t tbuf[];  // W x buf_rows word rows of 32 words
 
@@ -1622,48 +1646,62 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   }
   KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
-  {
-    const uint4* ta = reinterpret_cast<const uint4*>(I8 ? ea->M.luti8 : ea->M.lut4);
-    const uint4* tb = reinterpret_cast<const uint4*>(I8 ? eb->M.luti8 : eb->M.lut4);
-    for (int i = threadIdx.x; i < LUTN / 4; i += W * 64) {
-      reinterpret_cast<uint4*>(lut4)[i] = ta[i];
-      if (NTAB > 1 && mb != ma) reinterpret_cast<uint4*>(lut4 + LUTN)[i] = tb[i];
-    }
-  }
-  uint32_t* next = lut4 + NTAB * LUTN;
-  if (threadIdx.x == 0) *next = (uint32_t)W;
-  __syncthreads();
-
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
+  {  // the tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W
+    const uint4* ta = reinterpret_cast<const uint4*>(I8 ? ea->M.luti8 : ea->M.lut4);
+    const uint4* tb = reinterpret_cast<const uint4*>(I8 ? eb->M.luti8 : eb->M.lut4);
+    const int nchunk = (NTAB > 1 && mb != ma) ? 16 : 8;
+    for (int c = wave; c < nchunk; c += W)
+      __builtin_amdgcn_global_load_lds((c < 8 ? ta : tb) + 64 * (c & 7) + lane,
+                                       (__attribute__((address_space(3))) void*)(lut4 + 256 * c), 16, 0, 0);
+  }
+  // Copies in flight are paced: copy k (in the order the waves ask) waits until copies 0 .. k - C have landed, so
+  // the launch's first tiles land early instead of every wave's at the end of one burst over all CUs.
+  uint32_t* next = lut4 + NTAB * LUTN;
+  uint32_t* asked = next + 1;   // copies asked for (the first W: wave w's first tile is copy w)
+  uint32_t* landed = next + 2;  // copies landed
+  const int C = min(W, TILES_COPIES);
+  if (threadIdx.x == 0) {
+    next[0] = (uint32_t)W;
+    asked[0] = (uint32_t)W;
+    landed[0] = 0u;
+  }
+  auto ask = [&](uint32_t k) {  // wait for copy k's turn
+    while (k >= (uint32_t)C + __hip_atomic_load(landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+      __builtin_amdgcn_s_sleep(2);
+  };
   uint32_t* buf = tbuf + (size_t)wave * buf_rows * 32;
   const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
   uint32_t tmask = 0x1FFCu;
   asm volatile("" : "+v"(tmask));
-  // tile n of the block: the second entry or not, and the tile index (wave-uniform values)
+  // tile n of the block: the second entry or not, and the tile index (wave-uniform values; row-major)
   auto tile_of = [&](int n, int& sec, int& t) {
     const int T = T0 + n;
     sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
     KEntry* e = sec ? eb : ea;
-    const int u = T - e->tile0, NT = e->M.NT, KT = e->M.KT;
-    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : (u % NT) * KT + u / NT);
+    const int u = T - e->tile0;
+    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
   };
   // the tile's rows into the wave's buffer, 8 rows per copy instruction (lane l: row l / 8, words 4 (l % 8) ..),
   // the last one masked to the tile's own rows. The windows also read the 2 rows past the longest lane and the
   // table index takes up to 11 bits past a code's start: those rows keep whatever the buffer held, which no decoded
   // symbol depends on (every code lies within its lane's bits, a prefix code's entry ignores the bits after it).
-  // The per-tile words are read through the scalar cache (read-only during the launch).
-  auto copy_tile = [&](KEntry* e, int t) {
+  // The per-tile words are read through the scalar cache (read-only during the launch). Returns the number of
+  // copy instructions.
+  auto copy_tile = [&](KEntry* e, int t) -> int {
     const int nrow = (int)((KU16*)e->M.rows)[t];
     const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
-    for (int i = 0; i < (nrow + 7) / 8; ++i)
+    const int nc = (nrow + 7) / 8;
+    for (int i = 0; i < nc; ++i)
       if (lane < 8 * (nrow - 8 * i))
         __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+    return nc;
   };
   // The in-launch reduction of a tile's row is deferred behind the next tile's copy and decode: its partial is
   // stored, and after the next copy's wait (which also covers the store) the row counter is incremented; the
-  // counter's old value is read after the next decode, and the row's last tile sums the row. The next copy is
-  // issued as soon as a decode ends, so its latency hides behind the combine and the reduction.
+  // counter's old value is read after the next decode (before the next copy is issued: a read after it would wait
+  // for the copy), and the row's last tile sums the row once its own partial is stored.
   int pend = -1;  // the pending tile's entry: 0 = first, 1 = second, -1 = none
   int ptr = 0, pKT = 0, pN = 0;
   uint32_t pold = 0;
@@ -1675,13 +1713,31 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   };
   int n = wave;
   bool have = n < per && T0 + n < plan.ntiles;
-  int sec = 0, t = 0;
-  if (have) {
-    tile_of(n, sec, t);
+  int sec = 0, t = 0, ncopy = 0;
+  if (have) tile_of(n, sec, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  // this wave's table chunks, issued before its copy, are in LDS; the counters too; then every wave's
+  // (a bare barrier: the copies stay in flight)
+  wait_vmcnt_upto(ncopy);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (have && wave >= C) {
+    ask((uint32_t)wave);
     copy_tile(sec ? eb : ea, t);
+  }
+  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+    uint32_t warm = 0;
+    auto touch = [&](KEntry* e, int u0, int u1) {
+      if (e->list) return;
+      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
+      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+    };
+    touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
+    if (mb != ma) touch(eb, 0, Tl - eb->tile0);
+    asm volatile("" ::"s"(warm));
   }
 #pragma unroll 1
   while (have) {
+    const int cur = sec;
     const bool second = sec != 0;
     KEntry* ep = second ? eb : ea;
     const auto& E = *ep;
@@ -1715,6 +1771,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     }
     auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
+    if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (pend >= 0 && lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // register windows: rows r, r + 1 (A, B) of each chain, row r + 2 (C) read after every pair (P = bit
@@ -1800,6 +1857,27 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       }
     }
 
+    // the sub-block sums are formed here, not sunk past the claim and the copy below (the int8 products would be,
+    // holding every table entry of the tile in scratch)
+#pragma unroll
+    for (int k = 0; k < NSUBT; ++k) asm volatile("" : "+v"(sub[k]));
+    // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
+    // so the buffer is free); the pending row first
+    {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      n = __builtin_amdgcn_readfirstlane((int)nx);
+    }
+    // the pending row's counter value (arrived during the decode)
+    const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
+    have = n < per && T0 + n < plan.ntiles;
+    if (have) {
+      tile_of(n, sec, t);
+      uint32_t k = 0;
+      if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
+      copy_tile(sec ? eb : ea, t);
+    }
     // the row partial in tile_gemv's order (tile_gemv_i8's for int8 activations)
     float tot = 0.f;
     if (I8) {
@@ -1855,21 +1933,13 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     }
     float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
     __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    finish_pending();  // the counter's old value has arrived during the decode
+    if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
+    pend = -1;
     if (E.Y) {
-      pend = sec;
+      pend = cur;
       ptr = tr;
       pKT = KT;
       pN = N;
-    }
-    // the next tile's copy into the buffer (free: every read of the decode has returned)
-    uint32_t nx = 0;
-    if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    n = __builtin_amdgcn_readfirstlane((int)nx);
-    have = n < per && T0 + n < plan.ntiles;
-    if (have) {
-      tile_of(n, sec, t);
-      copy_tile(sec ? eb : ea, t);
     }
   }
   if (pend >= 0) {  // the last tile's reduction
