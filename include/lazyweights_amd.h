@@ -98,14 +98,18 @@ int lw_matmul_dev_noalloc(void* h, const char* name, const void* X, int x_f16, i
 int lw_group_matmul_dev(void* h, int count, const char* const* names, const void* const* X, int m,
                         float* const* Y, void* stream);
 
-/* Fused-kernel selection for all handles: 0 (default) = for m = 1 the whole-tile-per-wave flat kernel (each tile
- * copied to LDS, 8 chains per lane, every tile including exception tiles), for m > 1 the ring-staged kernels wherever
- * a matrix has a ring schedule (the flat kernel for int8 activations, the block-per-column kernel otherwise);
- * 1 = the whole-tile kernel everywhere (the fallback path); 2 = the block-per-column ring kernel for every m;
- * 7 = the ring-staged kernels for every m (for m = 1 the flat, load-balanced ring kernel); 3 = as 7, but exception
- * tiles are never decoded inside the flat launch (always by the separate exception pass); 4 = as 7, with the
- * low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 7, never the low-latency kernel; 6 = as 0,
- * but int8 activations take one m = 1 pass per token. Returns 0 or -1. */
+/* Fused-kernel selection for all handles. 0 (default): m = 1 with fp16 activations, the whole-tile kernel (a tile
+ * per wave copied to LDS, 8 chains per lane, every tile including exception tiles), or the half-tile kernel (two
+ * buffered half-tile units per wave, the next one's copy in flight while one decodes) where a launch's blocks would
+ * give the whole-tile waves fewer than two tiles each; m = 1 with int8 activations, the whole-tile kernel;
+ * 2 <= m <= 8 with fp16 activations and Q4_K / Q5_K, the whole-tile kernel with its products on the matrix cores;
+ * otherwise the ring-staged kernels wherever a matrix has a ring schedule (the flat kernel for int8 activations, the
+ * block-per-column kernel otherwise). 1 = the whole-tile fallback kernel everywhere; 2 = the block-per-column ring
+ * kernel for every m; 7 = the ring-staged kernels for every m (for m = 1 the flat, load-balanced ring kernel);
+ * 3 = as 7, but exception tiles are never decoded inside the flat launch (always by the separate exception pass);
+ * 4 = as 7, with the low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 7, never the low-latency
+ * kernel; 6 = as 0, but m = 1 always through the whole-tile kernel and int8 activations one m = 1 pass per token;
+ * 8 = as 0, but m = 1 with fp16 activations always through the half-tile kernel. Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
 /* Prefill GEMM (path 2, and fp32 X with m > 8) for every handle. The reference dequantizes to fp32 and runs its own

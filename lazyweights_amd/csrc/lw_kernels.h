@@ -23,6 +23,10 @@ struct DevMat {
   const uint16_t* mid;
   const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency and whole-tile kernels (Layout::split)
   const uint16_t* rows;
+  const uint32_t* hrow;  // [T] the half-tile units' rows (Layout::hrow)
+  // [T][2 f][64 lanes][4] the half-tile kernel's chain starts: lane 32 h + s of unit (t, f) starts its chain j at
+  // split offset 8 f + 4 h + j of lane stream s
+  const uint16_t* hsplit;
   const uint32_t* words;
   const uint8_t* side;
   const uint4* sched;
@@ -31,6 +35,7 @@ struct DevMat {
   int symbits;      // 4 (huf4p) or 8 (huf8)
   int KT, NT;       // tile columns, tile rows
   int max_rows;     // max over tiles of rows[t]
+  int max_hrows;    // max over tiles and halves of a half-tile unit's rows
   int ring_rows;    // 16 / 32: ring kernel usable with that ring; 0: whole-tile kernel only
   // tiles the ring kernel skips (no schedule for ring_rows): the first nexc32 have a 32-row ring schedule (decoded
   // by the flat ring kernel from this list), the rest go through the whole-tile kernel
@@ -117,6 +122,12 @@ int split_stage_rows(const FlatPlan& plan);
 // wave in LDS at a time (tiles_buf_rows rows), 8 chains per lane; every tile of the entries (exceptions included)
 // and the in-launch reduction for entries with Y
 hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
+// The half-tile kernel (m = 1, fp16 activations, no int8): as launch_fused_tiles, but a wave decodes half-tile units
+// (a tile's rows 32 f .. 32 f + 31) with two LDS buffers, the next unit's copy in flight while one decodes; the
+// in-launch reduction per tile row and half (each entry's cnt holds 2 NT counters). W waves per block, each with two
+// buffers of halves_buf_rows word rows.
+hipError_t launch_fused_halves(const FlatPlan& plan, int per, hipStream_t s);
+int halves_buf_rows(const FlatPlan& plan);
 int tiles_buf_rows(const FlatPlan& plan);
 // The whole-tile kernel for 2..8 tokens of fp16 activations (Q4_K / Q5_K, plan.mt tokens, entries' XS set): the
 // products on the matrix cores (4x4x4 blocks, x broadcast from one block), every token in one pass over the tiles

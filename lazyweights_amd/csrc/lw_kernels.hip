@@ -26,6 +26,7 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 // leading zero bits of every device lane stream (lw_layout.h GUARD)
 constexpr int GUARD_BITS = 2;
+constexpr int kBufferRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw dword loads on CDNA (32-bit data format)
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
@@ -1575,10 +1576,10 @@ __device__ __forceinline__ void dot2_row(float& acc, uint32_t xrow, int k, uint3
   }
 }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 32] (the count is an immediate: one wait per value). The
-// compiler does not see which value ran, so it still waits for every vector load whose result a later
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 63] (the count is an immediate: one wait per value; larger n wait
+// for 63). The compiler does not see which value ran, so it still waits for every vector load whose result a later
 // instruction reads; this is for loads whose results only LDS reads see (direct-to-LDS copies).
-template <int N = 32>
+template <int N = 63>
 __device__ __forceinline__ void wait_vmcnt_upto(int n) {
   if constexpr (N == 0) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -1948,6 +1949,439 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_pending();
   }
+}
+
+// ── half-tile kernel for flat launches (m = 1, fp16 activations): a wave decodes half-tile units, two buffered ─────
+// Unit (tile t, half f) = the tile's rows 32 f .. 32 f + 31 (lane stream s, its row f). Lane l decodes symbols
+// 128 (l / 32) .. + 127 of row 32 f + (l % 32) as 4 chains of 32 symbols from the load-time split offsets; the two
+// lanes of a row then hand their sub-block dot products to the lower one, which forms the row partial in
+// tile_gemv's order (the bits of the other kernels).
+// A unit's word rows are copied into one of the wave's two LDS buffers: rows [0, hrow & 0xFFFF) for f = 0, rows
+// [hrow >> 16, rows[t]) for f = 1 (Layout::hrow). While a unit decodes, the next unit's copy and its loads (chain
+// starts, x, the x words of the sub-block sums, side records) are in flight into the other buffer and a second
+// register set: the wait at a unit's start is for data asked for one unit earlier. Values loaded for the next unit
+// are only moved or computed on after that wait (an earlier use would make the compiler wait for the copy too).
+// The block takes units [0, 2 n) of its tiles [T0, T0 + n) from a counter in LDS; the in-launch reduction is per
+// tile row and half (counter 2 tr + f), its atomic issued one unit after the partial's store and its result read
+// one unit later still. Tables as k_fused_tiles.
+// The in-launch reduction of half a tile row (lanes 0..31: row 64 tr + 32 f + lane) in tile-column order, as
+// row_sum; its counter (2 tr + f) is reset for the next launch.
+template <class KEntryRef>
+__device__ __forceinline__ void row_sum_half(const KEntryRef& E, int tr, int f, int KT, int N, int lane) {
+  if (lane == 0) __hip_atomic_store(E.cnt + 2 * tr + f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane >= 32) return;
+  const float* pr = E.P + (size_t)tr * TN + (uint32_t)(32 * f + lane);
+  float a = 0.f;
+  for (int c0 = 0; c0 < KT; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c0 + c < KT) a += v[c];
+  }
+  E.Y[(size_t)tr * TN + (uint32_t)(32 * f + lane)] = a;
+}
+
+template <int KQ>
+struct HalfRegs {
+  static constexpr int SYMB = kq_symbits(KQ);
+  static constexpr int XR = SYMB == 4 ? 8 : 4;  // x dwords of the lane's half row: 16 lanes x XR consecutive
+  // the side record's words as loaded (Q6_K: the 5 aligned dwords holding the 2-byte aligned 18-byte record)
+  static constexpr int SR = KQ == KQ_Q6_K ? 5 : (KQ == KQ_IQ4_XS ? 2 : 4);
+  uint32_t sp[2];   // the lane's 4 chain starts (u16 pairs)
+  uint32_t xr[XR];
+  uint32_t xq[4];   // the x dwords of one quarter sub-block (lane 4 g + k: quarter k of sub-block g)
+  uint32_t sr[SR];  // the side record of the lane's super-block (both lanes of a row: the row's only one)
+  int t, sec, f;    // the unit (wave-uniform)
+};
+
+template <int KQ, int NTAB>
+__global__ void __launch_bounds__(1024, 1)
+k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
+  typedef HalfRegs<KQ> R;
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+  constexpr int NSUBT = TW / GW;                          // sub-blocks per tile row
+  constexpr int NSUBH = NSUBT / 2;                        // per lane (half a row)
+  constexpr int NSB = TW / 256;                           // super-blocks per tile row (2: one per lane)
+  constexpr int NSUB = 256 / GW;                          // sub-blocks per super-block
+  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
+  constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
+  constexpr int NC = 4;                                   // chains per lane (32 symbols each)
+  constexpr int NG = 2;                                   // 16-symbol groups per chain
+  constexpr int XR = R::XR, SR = R::SR;
+  constexpr int Q = GW / 8;                               // x dwords per quarter sub-block (4)
+  static_assert(KQ == KQ_Q6_K || Q == 4, "quarter sub-blocks of 4 dwords");
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  __shared__ uint32_t lut4[NTAB * LUTN + 4];
+  extern __shared__ __align__(16) uint32_t tbuf[];  // W x 2 x ubuf_rows word rows of 32 words
+
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * per, Tl = min(T0 + per, plan.ntiles) - 1;
+  const int units = 2 * (Tl - T0 + 1);
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, s = lane & 31, h = lane >> 5;
+  {  // the tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W, ahead of the first unit's
+    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.lut4);
+    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.lut4);
+    const int nchunk = (NTAB > 1 && mb != ma) ? 16 : 8;
+    for (int c = wave; c < nchunk; c += W)
+      __builtin_amdgcn_global_load_lds((c < 8 ? ta : tb) + 64 * (c & 7) + lane,
+                                       (__attribute__((address_space(3))) void*)(lut4 + 256 * c), 16, 0, 0);
+  }
+  uint32_t* next = lut4 + NTAB * LUTN;
+  if (threadIdx.x == 0) *next = (uint32_t)W;
+  uint32_t* const buf0 = tbuf + (size_t)(2 * wave) * ubuf_rows * 32;
+  uint32_t* const buf1 = buf0 + (size_t)ubuf_rows * 32;
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+
+  // unit v of the block: tile T0 + v / 2 (row-major in its matrix), half v % 2
+  auto unit_of = [&](int v, R& U) {
+    const int T = T0 + (v >> 1);
+    U.sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
+    KEntry* e = U.sec ? eb : ea;
+    const int u = T - e->tile0;
+    U.t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
+    U.f = v & 1;
+  };
+  // the unit's loads (kept as loaded); its rows' copy (8 rows per instruction, the last masked) is described in
+  // (src, nrow) and issued two instructions per pair step of the decode that runs meanwhile (copy_part)
+  // (buffer loads: the rows as a wave-uniform resource, instruction i at scalar offset 1 KB i, so the copy holds no
+  // per-lane addresses through the decode)
+  __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, kBufferRsrcWord3);
+  int crow = 0;
+  auto copy_part = [&](uint32_t* buf, int i0) {
+#pragma unroll
+    for (int i = i0; i < i0 + 2; ++i)
+      if (8 * i < crow && lane < 8 * (crow - 8 * i))
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(crs, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16,
+                                                 lane * 16, 1024 * i, 0, 0);
+  };
+  auto ask = [&](R& U, uint32_t* buf) {
+    KEntry* e = U.sec ? eb : ea;
+    const auto& M = e->M;
+    const int t = U.t, f = U.f, KT = M.KT, tc = t % KT, tr = t / KT;
+    const uint2 sp = reinterpret_cast<const uint2*>(M.hsplit)[((size_t)t * 2 + f) * 64 + (uint32_t)lane];
+    U.sp[0] = sp.x;
+    U.sp[1] = sp.y;
+    const uint32_t* xcol = e->X2 + (size_t)tc * (TW / 2);
+    const uint4* xs = reinterpret_cast<const uint4*>(xcol + (uint32_t)(h * (TW / 4) + XR * (lane & 15)));
+#pragma unroll
+    for (int k = 0; k < XR / 4; ++k) {
+      const uint4 v = xs[k];
+      U.xr[4 * k] = v.x;
+      U.xr[4 * k + 1] = v.y;
+      U.xr[4 * k + 2] = v.z;
+      U.xr[4 * k + 3] = v.w;
+    }
+    if (KQ != KQ_Q6_K) {  // lanes past the tile column's sub-blocks re-read its last quarter
+      const uint4 v = reinterpret_cast<const uint4*>(xcol)[min(lane, 4 * NSUBT - 1)];
+      U.xq[0] = v.x;
+      U.xq[1] = v.y;
+      U.xq[2] = v.z;
+      U.xq[3] = v.w;
+    }
+    const uint8_t* p = M.side + (side_record(tr * TN, tc * NSB, KT, NSB) + (uint32_t)(NSB > 1 ? h * TN : 0) +
+                                 (uint32_t)(32 * f + s)) * SB;
+    if (KQ == KQ_Q6_K) {
+      const uint32_t* a = reinterpret_cast<const uint32_t*>((uintptr_t)p & ~(uintptr_t)3);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) U.sr[i] = a[i];
+    } else if (KQ == KQ_IQ4_XS) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      U.sr[0] = v.x;
+      U.sr[1] = v.y;
+    } else {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      U.sr[0] = v.x;
+      U.sr[1] = v.y;
+      U.sr[2] = v.z;
+      U.sr[3] = v.w;
+    }
+    // (rows[t] through a scalar dword read: a 16-bit read would be a vector load waited for at once)
+    const uint32_t hr = ((KU32*)M.hrow)[t];
+    const uint32_t rw = ((KU32*)M.rows)[t >> 1] >> (16 * (t & 1)) & 0xFFFFu;
+    const int r0 = f ? (int)(hr >> 16) : 0, nrow = f ? (int)rw - r0 : (int)(hr & 0xFFFFu);
+    crs = __builtin_amdgcn_make_buffer_rsrc((void*)(M.words + ((KU32*)M.tbase)[t] + 32u * (uint32_t)r0), 0,
+                                            nrow * 128, kBufferRsrcWord3);
+    crow = nrow;
+    for (int i = 8; 8 * i < crow; i += 2) copy_part(buf, i);  // rows past 64: up front
+  };
+
+  R RA;  // the unit asked for last
+  const bool have = wave < units;
+  if (have) {
+    unit_of(wave, RA);
+    ask(RA, buf0);
+    for (int i = 0; i < 8; i += 2) copy_part(buf0, i);
+  }
+  // this wave's table chunks (issued before its first unit's loads and copy) are in LDS; the counter too; then
+  // every wave's (a bare barrier: the copies stay in flight)
+  wait_vmcnt_upto((crow + 7) / 8);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (wave == 0) {  // the block's row counts, half rows and word offsets into the scalar cache (read at each ask)
+    uint32_t warm = 0;
+    auto touch = [&](KEntry* e, int u0, int u1) {
+      if (e->list) return;
+      for (int u = u0; u <= u1; u += 16)
+        warm += ((KU32*)e->M.tbase)[u] + ((KU32*)e->M.hrow)[u] + ((KU32*)e->M.rows)[u >> 1];
+      warm += ((KU32*)e->M.tbase)[u1] + ((KU32*)e->M.hrow)[u1] + ((KU32*)e->M.rows)[u1 >> 1];
+    };
+    touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
+    if (mb != ma) touch(eb, 0, Tl - eb->tile0);
+    asm volatile("" ::"s"(warm));
+  }
+
+  // in-launch reduction state: pa = a stored partial whose counter is not yet incremented, pb = a counter increment
+  // whose old value has not been read
+  int pa_sec = -1, pa_tr = 0, pa_f = 0;
+  int pb_sec = -1, pb_tr = 0, pb_f = 0;
+  uint32_t pold = 0;
+  auto reduce_pending = [&]() {  // after a vmcnt(0) wait
+    if (pb_sec >= 0) {
+      const auto& E = *(pb_sec ? eb : ea);
+      const uint32_t old = (uint32_t)__builtin_amdgcn_readlane((int)pold, 0);
+      if (old == (uint32_t)(E.M.KT - 1)) row_sum_half(E, pb_tr, pb_f, E.M.KT, E.M.N, lane);
+      pb_sec = -1;
+    }
+    if (pa_sec >= 0) {
+      const auto& E = *(pa_sec ? eb : ea);
+      if (lane == 0)
+        pold = __hip_atomic_fetch_add(E.cnt + 2 * pa_tr + pa_f, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pb_sec = pa_sec;
+      pb_tr = pa_tr;
+      pb_f = pa_f;
+      pa_sec = -1;
+    }
+  };
+
+  // One unit per iteration: the unit asked for last (in Y, its rows in buffer `cur`) becomes X and decodes while the
+  // next one is asked for into Y and the other buffer (X = Y only after the wait: moving values still being loaded
+  // would wait for them).
+  R X;
+  int cur = 0;
+#pragma unroll 1
+  for (bool more = have; more;) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): X's rows and loads, the last partial's store
+    X = RA;
+    uint32_t* const bx = cur ? buf1 : buf0;
+    uint32_t* const by = cur ? buf0 : buf1;
+    R& Y = RA;
+    reduce_pending();
+    // the next unit is claimed ahead (its copy overlaps this decode) while more units are left than waves; the
+    // last ones are claimed by whichever waves free up first, after their decode
+    more = false;
+    crow = 0;
+    const bool ahead = (int)__hip_atomic_load(next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) + W < units;
+    if (ahead) {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int v = __builtin_amdgcn_readfirstlane((int)nx);
+      more = v < units;
+      if (more) {
+        unit_of(v, Y);
+        ask(Y, by);
+      }
+    }
+    const bool second = X.sec != 0;
+    const auto& E = *(second ? eb : ea);
+    const auto& M = E.M;
+    const int t = X.t, f = X.f, KT = M.KT, N = M.N;
+    const int tc = t % KT, tr = t / KT;
+    const uint32_t hr = ((KU32*)M.hrow)[t];
+    const uint32_t r0 = f ? hr >> 16 : 0u;
+    const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(bx + s) - (r0 << 7);
+    const uint32_t tsel = second ? 4u * LUTN : 0u;
+    uint32_t P[NC], slot[NC], A[NC], B[NC], C[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      P[j] = (X.sp[j >> 1] >> (16 * (j & 1)) & 0xFFFFu) - GUARD_BITS + 64u;
+      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+      C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+    }
+    float sub[NSUBH];
+    float acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        if (gi == 0 && p < 4) copy_part(by, 2 * p);  // the next unit's first 64 rows, spread over the decode
+        uint32_t w1[NC], e1[NC], e2[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
+          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          P[j] = P[j] + e1[j] + e2[j];
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+          const bool slide = nslot != slot[j];  // a pair advances at most 22 bits: at most one row
+          A[j] = slide ? B[j] : A[j];
+          B[j] = slide ? C[j] : B[j];
+          slot[j] = nslot;
+          C[j] = *(LdsU32*)(rlb + (nslot << 7));
+        }
+        // x dword c of the lane's half row is register c % XR of lane c / XR of its 16-lane row (DPP broadcast)
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const int g = NG * j + gi;  // 16-symbol group within the lane's half row
+          if (SYMB == 4) {
+            const uint32_t v1 = __builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u);
+            const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u);
+            const int c = 16 * g + 2 * p;
+            dot2_row(acc[j], X.xr[c % XR], c / XR, v1);
+            dot2_row(acc[j], X.xr[(c + 1) % XR], (c + 1) / XR, v2);
+          } else {
+            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
+            const int c = 8 * g + p;
+            dot2_row(acc[j], X.xr[c % XR], c / XR, v);
+          }
+        }
+      }
+      if (GPSUB == 1 || (gi & 1)) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          sub[(NG * j + gi) / GPSUB] = acc[j];
+          acc[j] = 0.f;
+        }
+      }
+    }
+    // x sums of the tile column's sub-blocks (as column_xsums, from the words asked for with X)
+    // (xg[g]: the sum over sub-block g of the lane's super-block, or of the row's one super-block)
+    float xg[8];
+    if (KQ != KQ_Q6_K) {
+      float a = 0.f;
+#pragma unroll
+      for (int c = 0; c < Q; ++c) a += h2f(X.xq[c]) + h2f(X.xq[c] >> 16);
+      a += __shfl_xor(a, 1);
+      a += __shfl_xor(a, 2);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const float v0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * g));
+        const float v1 = NSB == 2 ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 4 * (g + 8)))
+                                  : v0;
+        xg[g] = h ? v1 : v0;
+      }
+    }
+    // The row partial in tile_gemv's order, its terms split over the row's two lanes: with two super-blocks per row
+    // each lane forms its super-block's terms and the upper lane applies them after the lower lane's partial; with
+    // one, the lower lane runs the first half of the sub-block sum and the upper lane the rest and the total.
+    uint32_t sw[5];
+    if (KQ == KQ_Q6_K) {  // 18-byte records from a 256-byte aligned array: odd rows start 2 bytes into a dword
+      const uint32_t sh = (s & 1) ? 16u : 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sw[i] = __builtin_amdgcn_alignbit(X.sr[i + 1], X.sr[i], sh);
+      sw[4] = X.sr[4] >> sh & 0xFFFFu;
+    } else {
+#pragma unroll
+      for (int i = 0; i < SR; ++i) sw[i] = X.sr[i];
+    }
+    float dA, dB;
+    uint64_t scq, scq2;
+    side_packed<KQ>(sw, scq, scq2, dA, dB);
+    float tot;
+    if (NSB == 2) {  // Q4_K, IQ4_XS: lane h holds super-block h's sub-blocks
+      float pre = 0.f;  // msum (Q4_K) or csum (IQ4_XS) of the lane's super-block
+      if (KQ == KQ_Q4_K) {
+        float mf[8];
+        side_mins(sw, mf);
+  #pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj) pre = fmaf(mf[jj], xg[jj], pre);
+      }
+      if (KQ == KQ_IQ4_XS) {
+  #pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj)
+          pre = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xg[jj], pre);
+      }
+      float tsum = 0.f;
+  #pragma unroll
+      for (int jj = 0; jj < NSUB; ++jj) {
+        const float scv = KQ == KQ_IQ4_XS ? (float)(int)(int8_t)(uint8_t)scq : (float)(uint32_t)(scq & 255u);
+        scq >>= 8;
+        tsum = fmaf(scv, sub[jj], tsum);
+      }
+      // super-block 0's terms from 0 (the lower lane's), then super-block 1's after them (the upper lane's)
+      auto terms = [&](float t) {
+        if (KQ == KQ_Q4_K) t = fmaf(-dB, pre, t);
+        if (KQ == KQ_IQ4_XS) t = fmaf(-128.f * dA, pre, t);
+        return fmaf(dA * VSCALE, tsum, t);
+      };
+      tot = terms(__shfl_xor(terms(0.f), 32));
+    } else {  // Q5_K, Q6_K: one super-block per row, lane h holds its sub-blocks NSUBH h .. NSUBH h + NSUBH - 1
+      uint64_t sq = h ? (KQ == KQ_Q6_K ? scq2 : scq >> (8 * NSUBH)) : scq;  // the lane's sub-blocks' scales
+      auto half_sum = [&](float t) {
+        uint64_t q = sq;
+  #pragma unroll
+        for (int jj = 0; jj < NSUBH; ++jj) {
+          const float scv = KQ == KQ_Q6_K ? (float)(int)(int8_t)(uint8_t)q : (float)(uint32_t)(q & 255u);
+          q >>= 8;
+          t = fmaf(scv, sub[jj], t);
+        }
+        return t;
+      };
+      // the sum over the lower lane's sub-blocks from 0, continued over the upper lane's
+      const float tsum = half_sum(__shfl_xor(half_sum(0.f), 32));
+      tot = 0.f;
+      if (KQ == KQ_Q5_K) {
+        float mf[8], msum = 0.f;
+        side_mins(sw, mf);
+  #pragma unroll
+        for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xg[jj], msum);
+        tot = fmaf(-dB, msum, tot);
+      }
+      tot = fmaf(dA * VSCALE, tsum, tot);
+    }
+    if (lane >= 32) {
+      float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)(32 * f + s);
+      __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (E.Y) {
+      pa_sec = X.sec;
+      pa_tr = tr;
+      pa_f = f;
+    }
+    if (!ahead) {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int v = __builtin_amdgcn_readfirstlane((int)nx);
+      more = v < units;
+      if (more) {
+        unit_of(v, Y);
+        ask(Y, by);
+        for (int i = 0; i < 8; i += 2) copy_part(by, i);
+      }
+    }
+    cur ^= 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  reduce_pending();  // the last counter's old value read, the last partial's counter incremented
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  reduce_pending();
 }
 
 // ── whole-tile kernel on the matrix cores (2..8 tokens, fp16 activations, Q4_K / Q5_K) ─────────────────────
@@ -2354,6 +2788,53 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
     case KQ_Q5_K: return tiles_launch<KQ_Q5_K>(p, per, rows, s);
     case KQ_Q6_K: return tiles_launch<KQ_Q6_K>(p, per, rows, s);
     case KQ_IQ4_XS: return tiles_launch<KQ_IQ4_XS>(p, per, rows, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int KQ, int NTAB>
+static hipError_t halves_launch_t(const FlatPlan& p, int per, int ubuf_rows, hipStream_t s) {
+  const size_t smem = (size_t)p.W * 2 * ubuf_rows * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_halves<KQ, NTAB>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  const int blocks = (p.ntiles + per - 1) / per;
+  hipLaunchKernelGGL((k_fused_halves<KQ, NTAB>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, ubuf_rows);
+  return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t halves_launch(const FlatPlan& p, int per, int ubuf_rows, hipStream_t s) {
+  return p.n == 1 ? halves_launch_t<KQ, 1>(p, per, ubuf_rows, s) : halves_launch_t<KQ, 2>(p, per, ubuf_rows, s);
+}
+
+int halves_buf_rows(const FlatPlan& p) {
+  int r = 0;
+  for (int i = 0; i < p.n; ++i) r = std::max(r, p.e[i].M.max_hrows + 2);
+  return r;
+}
+
+hipError_t launch_fused_halves(const FlatPlan& p, int per, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || 2 * per < p.W || p.ntiles < 1 || p.mt > 1 || p.i8)
+    return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    // a block (`per` consecutive tiles) spans at most two matrices
+    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || !e.M.hrow || e.M.packed || !e.X2 || !e.P ||
+        (e.Y && !e.cnt) || e.tile0 + e.ntile != end || e.ntile < 1 || (p.n > 1 && e.ntile < per) ||
+        (!e.list && e.ntile != e.M.NT * e.M.KT) || (i == 0 && e.tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  const int rows = halves_buf_rows(p);
+  if (rows > 256 || (size_t)p.W * 2 * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024)
+    return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return halves_launch<KQ_Q4_K>(p, per, rows, s);
+    case KQ_Q5_K: return halves_launch<KQ_Q5_K>(p, per, rows, s);
+    case KQ_Q6_K: return halves_launch<KQ_Q6_K>(p, per, rows, s);
+    case KQ_IQ4_XS: return halves_launch<KQ_IQ4_XS>(p, per, rows, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -3100,7 +3581,6 @@ hipError_t launch_gemm_codes_mfma(const DevMat& M, const uint8_t* codes, int row
 constexpr int GEMM_WAVES = 8;
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kBufferRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for raw dword loads on CDNA (32-bit data format)
 
 // codes q0..q3 (bytes of qw) -> sc q / 16 as 4 fp16 in two words (nsc = -64 sc)
 __device__ __forceinline__ uint2 scaled_codes16(uint32_t qw, h2v sc, h2v nsc) {

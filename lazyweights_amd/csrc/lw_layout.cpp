@@ -239,7 +239,9 @@ template <class B>
 void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits, B bits32, int threads) {
   L.rows.assign(T, 0);
   L.tbase.assign(T, 0);
+  L.hrow.assign(T, 0);
   L.max_rows = 0;
+  L.max_hrows = 0;
   uint64_t total = 0, nwords = 0;
   for (int t = 0; t < T; ++t) {
     uint32_t r = 0;
@@ -252,6 +254,16 @@ void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits, B b
     L.tbase[t] = (uint32_t)nwords;
     nwords += (uint64_t)32 * r;
     L.max_rows = std::max<int>(L.max_rows, (int)r);
+    // half-tile units: the first rows' bits end before each lane's mid (device bits, guard included); the second
+    // rows' windows start at the row of mid - 2
+    uint32_t r1 = 0, r0 = 1u << 30;
+    for (int l = 0; l < LANES; ++l) {
+      const uint32_t m = L.mid[(size_t)t * LANES + l];
+      r1 = std::max<uint32_t>(r1, ((m - 1) >> 5) + 1);
+      r0 = std::min<uint32_t>(r0, (m - 2) >> 5);
+    }
+    L.hrow[t] = r1 | r0 << 16;
+    L.max_hrows = std::max<int>(L.max_hrows, (int)std::max<uint32_t>(r1, r - r0));
   }
   L.payload_bits = total;
   L.words.assign(nwords + (uint64_t)32 * TAIL_ROWS, 0);

@@ -30,6 +30,10 @@ struct Layout {
   // of the low-latency kernel (every second one) and the whole-tile kernel
   std::vector<uint16_t> split;
   std::vector<uint16_t> rows;   // [T]
+  // [T] the half-tile units' word rows: bits 0-15 = rows [0, r) hold every bit of the lanes' first rows (symbols
+  // 0..255), bits 16-31 = the first row the second rows' windows read (the row of each lane's bit mid - 2; their
+  // last row is rows[t] - 1)
+  std::vector<uint32_t> hrow;
   std::vector<uint32_t> words;  // tiles' word rows + zero tail
   // ring staging schedule per tile, 2 x u64: word 0 = 2-bit counts of 2-row chunks that front 0 (bits 2g) and
   // front 1 (bits 32 + 2g) load at group g; word 1 = base row of front 1 (bits 0-7), initial chunks of front 0
@@ -42,6 +46,7 @@ struct Layout {
   std::vector<uint32_t> exc;
   int nexc32 = 0;  // the first nexc32 exception tiles have a 32-row ring schedule (in sched)
   int max_rows = 0;
+  int max_hrows = 0;  // max over tiles and halves of a half-tile unit's rows
   uint64_t payload_bits = 0;    // coded bits of all lanes
 };
 

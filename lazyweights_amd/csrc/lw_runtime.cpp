@@ -244,10 +244,12 @@ bool upload_side(Model& M, Tensor& t) {
     for (int b = 0; b < nb; ++b)
       memcpy(sb.data() + lw::side_record(n, b, dm.KT, nsb) * SB, raw.data() + ((size_t)n * nb + b) * SB, SB);
   std::vector<uint8_t>().swap(raw);
-  if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes) != hipSuccess) {
+  // 16 bytes past the records: the half-tile kernel reads a Q6_K record as the 5 aligned dwords holding it
+  if (hipMalloc(reinterpret_cast<void**>(&t.dside), t.side_bytes + 16) != hipSuccess) {
     (void)hipGetLastError();
     return fail(t.name + ": device allocation failed (side)");
   }
+  if (hipMemset(t.dside + t.side_bytes, 0, 16) != hipSuccess) return fail(t.name + ": upload failed (side)");
   if (hipMemcpy(t.dside, sb.data(), t.side_bytes, hipMemcpyHostToDevice) != hipSuccess)
     return fail(t.name + ": upload failed (side)");
   dm.side = t.dside;
@@ -265,13 +267,14 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][tbase 4T][mid 64T][split 512T][rows 2T]
-  // [sched 16T (16-aligned)][exception tiles 4E] padded to 256 B, then the words
+  // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][tbase 4T][mid 64T][split 1024T][rows 2T]
+  // [sched 16T (16-aligned)][hrow 4T][hsplit 1024T][exception tiles 4E] padded to 256 B, then the words
   const size_t nexc = L.exc.size();
   const size_t o_lut4 = 2 * lw::LUTN, o_luti8 = o_lut4 + 4 * lw::LUTN, o_tb = o_luti8 + 4 * lw::LUTN;
   const size_t o_mid = o_tb + 4ull * T;
   const size_t o_split = o_mid + 64ull * T, o_rows = o_split + 64ull * lw::SPLITS * T;
-  const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_exc = o_sched + 16ull * T;
+  const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_hrow = o_sched + 16ull * T;
+  const size_t o_hsplit = (o_hrow + 4ull * T + 15) & ~(size_t)15, o_exc = o_hsplit + 1024ull * T;
   const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
@@ -285,6 +288,16 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   memcpy(host.data() + o_split, L.split.data(), 64ull * lw::SPLITS * T);
   memcpy(host.data() + o_rows, L.rows.data(), 2ull * T);
   memcpy(host.data() + o_sched, L.sched.data(), 16ull * T);
+  memcpy(host.data() + o_hrow, L.hrow.data(), 4ull * T);
+  {  // the half-tile kernel's chain starts: unit (t, f), lane 32 h + s, chains j = the split offsets 8 f + 4 h + j
+    uint16_t* hs = reinterpret_cast<uint16_t*>(host.data() + o_hsplit);
+    for (size_t t = 0; t < (size_t)T; ++t)
+      for (int f = 0; f < 2; ++f)
+        for (int h = 0; h < 2; ++h)
+          for (int s = 0; s < lw::LANES; ++s)
+            for (int j = 0; j < 4; ++j)
+              hs[((t * 2 + f) * 64 + 32 * h + s) * 4 + j] = L.split[(t * lw::SPLITS + 8 * f + 4 * h + j) * lw::LANES + s];
+  }
   if (nexc) memcpy(host.data() + o_exc, L.exc.data(), 4 * nexc);
   void* d = nullptr;
   if (hipMalloc(&d, bytes) != hipSuccess) {
@@ -309,6 +322,8 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
   dm.split = reinterpret_cast<const uint16_t*>(b + o_split);
   dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
+  dm.hrow = reinterpret_cast<const uint32_t*>(b + o_hrow);
+  dm.hsplit = reinterpret_cast<const uint16_t*>(b + o_hsplit);
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
   dm.sched = reinterpret_cast<const uint4*>(b + o_sched);
   dm.ring_rows = L.ring_rows;
@@ -324,6 +339,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.KT = t.KS() / lw::TK;
   dm.NT = (int)(t.N / lw::TN);
   dm.max_rows = L.max_rows;
+  dm.max_hrows = L.max_hrows;
   if (t.kqt && !upload_side(M, t)) return false;
   t.resident = true;
   M.resident_bytes += bytes + t.side_bytes;
@@ -437,12 +453,8 @@ int check_matmul(Tensor* t, const char* name) {
 // 1 = whole-tile kernel everywhere (kept as the fallback and for tests).
 int g_kernel_mode = 0;
 
-// Cost model of a flat launch: every block is w waves of one tile each and stays resident until its slowest wave
-// ends. The blocks spread evenly over the CUs; a CU runs its share in rounds of as many blocks as fit at once (LDS:
-// `lds` bytes per block of 160 KB; waves: wcu, 32 unless registers allow fewer), and a round takes about
-// max(its waves, 16) tile times (below 16 waves a CU is no longer issue-bound). Returns the busiest CU's sum over
-// rounds, in tile times.
-long long flat_cost(int total, int w, int lds, int wcu = 32) {
+// CUs of the current device (256 if it cannot be read), read once
+int cu_count() {
   static int cus = 0;
   if (!cus) {
     int dev = 0;
@@ -450,6 +462,16 @@ long long flat_cost(int total, int w, int lds, int wcu = 32) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
       cus = 256;
   }
+  return cus;
+}
+
+// Cost model of a flat launch: every block is w waves of one tile each and stays resident until its slowest wave
+// ends. The blocks spread evenly over the CUs; a CU runs its share in rounds of as many blocks as fit at once (LDS:
+// `lds` bytes per block of 160 KB; waves: wcu, 32 unless registers allow fewer), and a round takes about
+// max(its waves, 16) tile times (below 16 waves a CU is no longer issue-bound). Returns the busiest CU's sum over
+// rounds, in tile times.
+long long flat_cost(int total, int w, int lds, int wcu = 32) {
+  const int cus = cu_count();
   const long long per_cu = std::max(1, std::min(160 * 1024 / lds, wcu / w));
   const long long blocks = (total + w - 1) / w, b = (blocks + cus - 1) / cus;
   const long long full = b / per_cu, rest = b % per_cu;
@@ -482,13 +504,7 @@ int flat_width(int total, int rs, int mintiles, int spare_bytes, int wcu = 32) {
 // after staging (counted as 8 more) and a combine step.
 long long ring_cost(int total, int w, int lds, int wcu = 32) { return flat_cost(total, w, lds, wcu) * 128; }
 long long split_cost(int total, int stage_rows, int kqt) {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-      cus = 256;
-  }
+  const int cus = cu_count();
   const int nsubt = lw::kq_symbits(kqt) == 4 ? 2 * lw::TK / lw::kq_gw(kqt) : lw::TK / lw::kq_gw(kqt);
   const int lds = 4 * lw::LUTN + lw::TN * nsubt * 4 + stage_rows * 128;
   const long long per_cu = std::max(1, std::min(160 * 1024 / lds, 8));
@@ -570,13 +586,7 @@ int quant_x8_dev(Model& M, Tensor* const* ts, const void* const* X, int x_f16, i
 // (the waves of a block then share the 4 SIMDs evenly); `per` = the tiles that spread the plan over every CU once,
 // at most the smallest matrix's tile count (a block spans at most two matrices). Returns 0 if no width fits.
 int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-      cus = 256;
-  }
+  const int cus = cu_count();
   const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
   if (rows > 256) return 0;
   const int wmax = std::min(16, (160 * 1024 - tables) / (rows * 128));
@@ -588,6 +598,20 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   // 12 + 12 + 2); the waves take tiles from a counter, so they need not spread evenly over the SIMDs
   const int rounds = (per + wmax - 1) / wmax;
   return std::min(wmax, (per + rounds - 1) / rounds);
+}
+
+// Waves per block and tiles per block of the half-tile kernel: two unit buffers per wave (halves_buf_rows) next to
+// one or two 8 KB tables; `per` as tiles_width; every wave starts on a unit (at most 2 per waves). Returns 0 if no
+// width fits.
+int halves_width(const lw::FlatPlan& fp, int mintiles, int& per) {
+  const int rows = lw::halves_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
+  if (rows > 256) return 0;
+  const int wmax = std::min(16, (160 * 1024 - tables) / (2 * rows * 128));
+  if (wmax < 1) return 0;
+  const int cus = cu_count();
+  per = (fp.ntiles + cus - 1) / cus;
+  if (fp.n > 1) per = std::min(per, mintiles);
+  return std::min(wmax, 2 * per);
 }
 
 // Fused GEMV / skinny GEMM of `count` matrices with fp16 activations X16[i] ([m * per][K_i] pseudo-tokens):
@@ -604,7 +628,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   std::vector<size_t> off(count + 1, 0);
   for (int i = 0; i < count; ++i) off[i + 1] = off[i] + (size_t)ts[i]->dm.KT * mt * ts[i]->N;
   std::vector<size_t> coff(count + 1, 0);  // tile-row counters per entry (in-launch reduction)
-  for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + (size_t)ts[i]->dm.NT;
+  for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + 2 * (size_t)ts[i]->dm.NT;  // per tile row and half
   // partials and counters: the model's (grown on demand) or a caller's fixed scratch (nothing allocated; its counters
   // are cleared by a fill kernel on the stream, since the last call on that scratch may have left anything there)
   // 2..8 tokens of fp16 activations, Q4_K / Q5_K: the whole-tile kernel with its products on the matrix cores (its
@@ -683,6 +707,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   std::vector<char> done(count, 0), exc_in(count, 0), whole(count, 0);  // whole: every tile in a low-latency launch
   std::vector<lw::FlatPlan> flat_plans, split_plans;
   std::vector<std::pair<lw::FlatPlan, int>> tile_plans;  // whole-tile kernel launches and their tiles per block
+  std::vector<std::pair<lw::FlatPlan, int>> half_plans;  // half-tile kernel launches and their tiles per block
   // packed (fixed-rate) matrices: the decode-free kernels, one launch per K-quant type and MAX_GROUP matrices
   // (m = 1: the flat one, which also reduces)
   for (int i = 0; mt == 1 && i < count; ++i) {
@@ -801,6 +826,30 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       done[j] = 1;
     }
     fp.ntiles = total;
+    if (mt == 1 && (g_kernel_mode == 0 || g_kernel_mode == 8) && !x8) {
+      // the half-tile kernel (kernel mode 8; the m = 1 default with fp16 activations where the whole-tile kernel
+      // would run fewer than 10 waves per block, i.e. few tiles per CU: half tiles keep more waves busy and balance
+      // better; measured faster on config 1, equal on config 3, slower on config 2's 13 waves): every tile, the
+      // reduction in the launch
+      bool ok = true;
+      for (int k = 0; k < fp.n; ++k) ok = ok && fp.e[k].M.hrow && fp.e[k].M.hsplit;
+      if (ok && g_kernel_mode == 0) {
+        int tper = 0;
+        const int tw = tiles_width(fp, mintiles, tper);
+        ok = tw < 10;
+      }
+      int hper = 0;
+      fp.W = ok ? halves_width(fp, mintiles, hper) : 0;
+      if (fp.W > 0) {
+        for (int k = 0; k < fp.n; ++k) {
+          fp.e[k].Y = Y[sel[k]];
+          fp.e[k].cnt = Cb + coff[sel[k]];
+          reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
+        }
+        half_plans.emplace_back(fp, hper);
+        continue;
+      }
+    }
     if (mt == 1 && (g_kernel_mode == 0 || g_kernel_mode == 6)) {
       // the whole-tile kernel (the m = 1 default: faster than the ring kernel on every configuration measured):
       // every tile, the reduction in the launch; the ring kernel where the tiles do not fit its LDS
@@ -926,6 +975,10 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   }
   for (const auto& tp : tile_plans) {
     HIPCHECK(lw::launch_fused_tiles(tp.first, tp.second, s));
+    if (launches) ++*launches;
+  }
+  for (const auto& hp : half_plans) {
+    HIPCHECK(lw::launch_fused_halves(hp.first, hp.second, s));
     if (launches) ++*launches;
   }
   for (int i = 0; i < count; ++i) {
@@ -1618,7 +1671,7 @@ int lw_set_act8(int on) {
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 7) return -1;
+  if (mode < 0 || mode > 8) return -1;
   g_kernel_mode = mode;
   return 0;
 }

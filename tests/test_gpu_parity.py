@@ -566,6 +566,57 @@ def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
             check_err(a[0].numpy(), orc.gemv_f64(orc.dequant(2, codes, side), x.double().numpy()), nm)
 
 
+def test_gpu_half_tile_kernel_same_bits(gpu, tmp_path, orc):
+    """The half-tile kernel (kernel mode 8; the m = 1 default where whole tiles would give a block's waves fewer than
+    two each) gives the whole-tile (mode 6) and ring (mode 7) kernels' bits for every format, on matrices with 7 tiles
+    per block, so that waves decode second units claimed when a wave frees up, and on a group of two (14 tiles per
+    block), whose waves claim units one ahead; and mode 0 picks it for the single matrix, with the same bits."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime, bundle
+
+    mats = []
+    for kqt, fmt, H in FORMATS:
+        K = 4096 if kqt in (1, 4) else 2048  # 8 tile columns
+        mats.append((fmt, kqt, 14336, K, H, 70 + kqt))
+    bundle.write_synthetic_bundle(str(tmp_path), mats, threads=16)
+
+    def run(rt, names, xs, mode):
+        assert rt.lib.lw_set_kernel_mode(mode) == 0
+        try:
+            ys = [torch.zeros(1, rt.info(nm)["N"], device="cuda") for nm in names]
+            n = len(names)
+            rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                            (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                            (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+            assert rc == 0, rt.lib.lw_last_error()
+            torch.cuda.synchronize()
+            return [y.cpu() for y in ys]
+        finally:
+            rt.lib.lw_set_kernel_mode(0)
+
+    with Runtime(tmp_path) as rt:
+        for name, kqt, N, K, H, seed in mats:
+            x = torch.randn(1, K).half()
+            xs = [x.cuda()]
+            h, t, r, d = (run(rt, [name], xs, mode)[0] for mode in (8, 6, 7, 0))
+            say("half-tile kernel", name)
+            assert torch.equal(h, t), name
+            assert torch.equal(h, r), name
+            assert torch.equal(h, d), name
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            check_err(h.numpy(), orc.gemv_f64(orc.dequant(kqt, codes, side), x.double().numpy()), name)
+            del codes, side
+            pair = [name, name]
+            xs2 = [x.cuda(), torch.randn(1, K).half().cuda()]
+            g8, g6 = run(rt, pair, xs2, 8), run(rt, pair, xs2, 6)
+            say("half-tile kernel, group of two", name)
+            for a, b in zip(g8, g6):
+                assert torch.equal(a, b), name
+            assert torch.equal(g8[0], h), name
+
+
 def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
     """The packed twin (pk4 / pk8) of every format gives the coded matrix's bits: m = 1 (grouped, several matrices,
     with a one-tile IQ4_XS matrix so the flat launch runs one-wave blocks that use all 256 table entries), m = 5, the
