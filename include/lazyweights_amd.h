@@ -88,7 +88,7 @@ int lw_matmul_dev(void* h, const char* name, const void* X, int x_f16, int m, fl
  * tile-row counters and (fp32 x) split activations live in a static 16 MiB device array held by every GPU the library
  * runs on until the process ends; the counters are cleared by a kernel on `stream` at each call. Fused path only:
  * fp16 X with 1 <= m <= 16 or fp32 X with 1 <= m <= 8, int8 activations off; -1 with an error text when the call
- * needs more than the 16 MiB (KT * m * N * 4 bytes of partials, 8 with fp32 X, + 4 * N / 64 of counters + 4 m K of
+ * needs more than the 16 MiB (KT * m * N * 4 bytes of partials, 8 with fp32 X, + 8 * N / 64 of counters + 4 m K of
  * split x). Calls that overlap on one GPU (several streams or threads) race on the array. */
 int lw_matmul_dev_noalloc(void* h, const char* name, const void* X, int x_f16, int m, float* Y, int ldy,
                           void* stream);

@@ -27,6 +27,9 @@ struct DevMat {
   // [T][2 f][64 lanes][4] the half-tile kernel's chain starts: lane 32 h + s of unit (t, f) starts its chain j at
   // split offset 8 f + 4 h + j of lane stream s
   const uint16_t* hsplit;
+  // [T][2 f][32 s] the whole-tile kernels' chain starts of lane stream s, row f: after the first (mid for f = 1, the
+  // guard for f = 0) 7 deltas of 32 symbols each, less 32, 9 bits each
+  const uint64_t* dsplit;
   const uint32_t* words;
   const uint8_t* side;
   const uint4* sched;

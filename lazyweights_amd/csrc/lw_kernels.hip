@@ -1589,6 +1589,17 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
   }
 }
 
+// The 8 chain starts (P form: bit position - GUARD_BITS + 64) of row f of lane stream s of tile t in the whole-tile
+// kernels: the first at mid (f = 1) or the guard (f = 0), the others from the 9-bit deltas of dsplit.
+template <class DevMatRef>
+__device__ __forceinline__ void tile_chain_starts(const DevMatRef& M, int t, int f, int s, uint32_t* P) {
+  const uint64_t d = M.dsplit[((size_t)t * 2 + f) * 32 + (uint32_t)s];
+  const uint32_t mid = M.mid[(size_t)t * 32 + (uint32_t)s];
+  P[0] = (f ? mid : (uint32_t)GUARD_BITS) - GUARD_BITS + 64u;
+#pragma unroll
+  for (int j = 1; j < 8; ++j) P[j] = P[j - 1] + 32u + (uint32_t)(d >> (9 * (j - 1)) & 511u);
+}
+
 // ── whole-tile kernel for flat launches (m = 1): a tile per wave, 8 chains per lane ───────────────────────
 // the most tile copies a block of the whole-tile kernel keeps in flight (measured on config 2: 3-6 alike, 2-4 %
 // faster than one per wave)
@@ -1753,8 +1764,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     XgRegs xgr;
     if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
     uint32_t P[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS + 64u;
+    tile_chain_starts(M, t, f, s, P);
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
     // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
@@ -2512,8 +2522,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
     uint32_t P[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) P[j] = (uint32_t)M.split[((size_t)t * SPLITS + NC * f + j) * 32 + (uint32_t)s] - GUARD_BITS + 64u;
+    tile_chain_starts(M, t, f, s, P);
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
     // (zero for tokens >= mt); XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks, block b = (super-block,

@@ -268,13 +268,14 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
   // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][tbase 4T][mid 64T][split 1024T][rows 2T]
-  // [sched 16T (16-aligned)][hrow 4T][hsplit 1024T][exception tiles 4E] padded to 256 B, then the words
+  // [sched 16T (16-aligned)][hrow 4T][hsplit 1024T][dsplit 512T][exception tiles 4E] padded to 256 B, then the words
   const size_t nexc = L.exc.size();
   const size_t o_lut4 = 2 * lw::LUTN, o_luti8 = o_lut4 + 4 * lw::LUTN, o_tb = o_luti8 + 4 * lw::LUTN;
   const size_t o_mid = o_tb + 4ull * T;
   const size_t o_split = o_mid + 64ull * T, o_rows = o_split + 64ull * lw::SPLITS * T;
   const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_hrow = o_sched + 16ull * T;
-  const size_t o_hsplit = (o_hrow + 4ull * T + 15) & ~(size_t)15, o_exc = o_hsplit + 1024ull * T;
+  const size_t o_hsplit = (o_hrow + 4ull * T + 15) & ~(size_t)15, o_dsplit = o_hsplit + 1024ull * T;
+  const size_t o_exc = o_dsplit + 512ull * T;
   const size_t o_words = (o_exc + 4 * nexc + 255) & ~(size_t)255;
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
@@ -297,6 +298,22 @@ bool make_resident(Model& M, Tensor& t, int threads) {
           for (int s = 0; s < lw::LANES; ++s)
             for (int j = 0; j < 4; ++j)
               hs[((t * 2 + f) * 64 + 32 * h + s) * 4 + j] = L.split[(t * lw::SPLITS + 8 * f + 4 * h + j) * lw::LANES + s];
+  }
+  {  // the whole-tile kernels' chain starts of (t, f, lane stream s) after the first (mid or the guard): 7 deltas of
+     // 32 symbols each (32 .. 352 bits), less 32, in 9 bits each
+    uint64_t* ds = reinterpret_cast<uint64_t*>(host.data() + o_dsplit);
+    for (size_t u = 0; u < (size_t)T; ++u)
+      for (int f = 0; f < 2; ++f)
+        for (int s = 0; s < lw::LANES; ++s) {
+          uint64_t v = 0;
+          for (int j = 0; j < 7; ++j) {
+            const int a = L.split[(u * lw::SPLITS + 8 * f + j) * lw::LANES + s];
+            const int b = L.split[(u * lw::SPLITS + 8 * f + j + 1) * lw::LANES + s];
+            if (b - a < 32 || b - a > 32 + 511) return fail(t.name + ": chain start delta out of range");
+            v |= (uint64_t)(b - a - 32) << (9 * j);
+          }
+          ds[(u * 2 + f) * lw::LANES + s] = v;
+        }
   }
   if (nexc) memcpy(host.data() + o_exc, L.exc.data(), 4 * nexc);
   void* d = nullptr;
@@ -324,6 +341,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.rows = reinterpret_cast<const uint16_t*>(b + o_rows);
   dm.hrow = reinterpret_cast<const uint32_t*>(b + o_hrow);
   dm.hsplit = reinterpret_cast<const uint16_t*>(b + o_hsplit);
+  dm.dsplit = reinterpret_cast<const uint64_t*>(b + o_dsplit);
   dm.words = reinterpret_cast<const uint32_t*>(b + o_words);
   dm.sched = reinterpret_cast<const uint4*>(b + o_sched);
   dm.ring_rows = L.ring_rows;
