@@ -2395,7 +2395,7 @@ k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
 }
 
 // ── whole-tile kernel on the matrix cores (2..8 tokens, fp16 activations, Q4_K / Q5_K) ─────────────────────
-// The decode of k_fused_tiles (a tile per wave in LDS, 8 chains per lane), with the products of MT tokens on
+// The decode of k_fused_tiles (a tile per wave in LDS; 4 chains per lane), with the products of MT tokens on
 // v_mfma_f32_4x4x4f16 (16 blocks of 4 lanes): block b computes D[i][j] = sum_k A[4 b' + i][k] B[4 b + j][k] into lane
 // 4 b + j, register i, where b' is the block named by the instruction's broadcast field (cbsz 4, abid b'). B = the
 // lane's own 4 weights of the pair (its row), A = the 4 x values of token i at those positions, broadcast from block
@@ -2405,9 +2405,10 @@ k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
 // Q4_K) applies once per super-block. The mins term dmin sum_j m_j (sum x)_j runs on the same instruction with
 // A = the sub-block sums of x as fp16 hi and lo (XS) and B = the row's mins. Each token's values agree with its own
 // m = 1 launch to fp32 rounding (another order of the same products). Partials [KT][mt][N], the in-launch reduction.
-// at most 12 waves per block: the tile buffers leave room for no more per CU, and the register budget of 3 waves per
-// SIMD holds the 8 chains with 8 tokens' x and accumulators without spilling
-constexpr int TILES_MMA_WAVES = 12;
+// The tile pipeline is k_fused_tiles': tables by direct-to-LDS loads, paced first copies, row-major tiles, the next
+// tile's copy issued as soon as a decode ends.
+// at most 16 waves per block (4 per SIMD: 128 VGPRs hold the 8 chains with 8 tokens' x and accumulators)
+constexpr int TILES_MMA_WAVES = 16;
 
 // compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1 (indices that must be constants: MFMA
 // broadcast fields, register-array indices)
@@ -2440,7 +2441,8 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   constexpr int NSB = TW / 256;   // super-blocks per tile row
   constexpr int NQ = MT / 4;      // token quads
   constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
-  constexpr int NC = 8, NG = 2;   // chains per lane, 16-symbol groups per chain
+  constexpr int NC = 4, NG = 16 / NC;  // chains per lane (64 symbols each: 8 tokens' x and accumulators leave no
+                                       // registers for 8 chains at 4 waves per SIMD), 16-symbol groups per chain
   constexpr float DSCALE = SYMB == 4 ? 16.f : 1.f;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   typedef __attribute__((address_space(4))) const char KChar;
@@ -2460,38 +2462,50 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
   KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
-  {
-    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.lut4);
-    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.lut4);
-    for (int i = threadIdx.x; i < LUTN / 4; i += W * 64) {
-      reinterpret_cast<uint4*>(lut4)[i] = ta[i];
-      if (NTAB > 1 && mb != ma) reinterpret_cast<uint4*>(lut4 + LUTN)[i] = tb[i];
-    }
-  }
-  uint32_t* next = lut4 + NTAB * LUTN;
-  if (threadIdx.x == 0) *next = (uint32_t)W;
-  __syncthreads();
-
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
   const int qb = lane >> 2, qi = lane & 3;  // 4-lane block and the lane's place in it
+  {  // the tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W
+    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.lut4);
+    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.lut4);
+    const int nchunk = (NTAB > 1 && mb != ma) ? 16 : 8;
+    for (int c = wave; c < nchunk; c += W)
+      __builtin_amdgcn_global_load_lds((c < 8 ? ta : tb) + 64 * (c & 7) + lane,
+                                       (__attribute__((address_space(3))) void*)(lut4 + 256 * c), 16, 0, 0);
+  }
+  // copies paced as in k_fused_tiles: copy k (in the order the waves ask) waits for copies 0 .. k - C to land
+  uint32_t* next = lut4 + NTAB * LUTN;
+  uint32_t* asked = next + 1;
+  uint32_t* landed = next + 2;
+  const int C = min(W, TILES_COPIES);
+  if (threadIdx.x == 0) {
+    next[0] = (uint32_t)W;
+    asked[0] = (uint32_t)W;
+    landed[0] = 0u;
+  }
+  auto ask = [&](uint32_t k) {
+    while (k >= (uint32_t)C + __hip_atomic_load(landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+      __builtin_amdgcn_s_sleep(2);
+  };
   uint32_t* buf = tbuf + (size_t)wave * buf_rows * 32;
   const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
   uint32_t tmask = 0x1FFCu;
   asm volatile("" : "+v"(tmask));
-  auto tile_of = [&](int n, int& sec, int& t) {
+  auto tile_of = [&](int n, int& sec, int& t) {  // row-major, as k_fused_tiles
     const int T = T0 + n;
     sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
     KEntry* e = sec ? eb : ea;
-    const int u = T - e->tile0, NT = e->M.NT, KT = e->M.KT;
-    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : (u % NT) * KT + u / NT);
+    const int u = T - e->tile0;
+    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
   };
-  auto copy_tile = [&](KEntry* e, int t) {  // as k_fused_tiles: the tile's own rows, the last copy masked
+  auto copy_tile = [&](KEntry* e, int t) -> int {  // as k_fused_tiles: the tile's own rows, the last copy masked
     const int nrow = (int)((KU16*)e->M.rows)[t];
     const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
-    for (int i = 0; i < (nrow + 7) / 8; ++i)
+    const int nc = (nrow + 7) / 8;
+    for (int i = 0; i < nc; ++i)
       if (lane < 8 * (nrow - 8 * i))
         __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+    return nc;
   };
   int pend = -1;
   int ptr = 0, pKT = 0, pN = 0;
@@ -2504,13 +2518,30 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   };
   int n = wave;
   bool have = n < per && T0 + n < plan.ntiles;
-  int sec = 0, t = 0;
-  if (have) {
-    tile_of(n, sec, t);
+  int sec = 0, t = 0, ncopy = 0;
+  if (have) tile_of(n, sec, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  // this wave's table chunks and the counters are in place; then every wave's (a bare barrier: copies stay in flight)
+  wait_vmcnt_upto(ncopy);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (have && wave >= C) {
+    ask((uint32_t)wave);
     copy_tile(sec ? eb : ea, t);
+  }
+  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+    uint32_t warm = 0;
+    auto touch = [&](KEntry* e, int u0, int u1) {
+      if (e->list) return;
+      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
+      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+    };
+    touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
+    if (mb != ma) touch(eb, 0, Tl - eb->tile0);
+    asm volatile("" ::"s"(warm));
   }
 #pragma unroll 1
   while (have) {
+    const int cur = sec;
     const bool second = sec != 0;
     KEntry* ep = second ? eb : ea;
     const auto& E = *ep;
@@ -2522,7 +2553,12 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
     uint32_t P[NC];
-    tile_chain_starts(M, t, f, s, P);
+    {
+      uint32_t P8[8];
+      tile_chain_starts(M, t, f, s, P8);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) P[j] = P8[j * (8 / NC)];
+    }
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
     // (zero for tokens >= mt); XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks, block b = (super-block,
@@ -2550,6 +2586,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       xs[q] = __builtin_bit_cast(h4v, sv);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
+    if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (pend >= 0 && lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t slot[NC], A[NC], B[NC], C[NC];
@@ -2582,7 +2619,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       h2v scv[NC], nsc[NC];
 #pragma unroll
       for (int j = 0; j < NC; ++j) {
-        const int js = SYMB == 4 ? 2 * j + gi : j;  // sub-block within the tile row
+        const int js = SYMB == 4 ? NG * j + gi : (NG * j + gi) / 2;  // sub-block within the tile row
         const _Float16 v = (_Float16)(float)(uint32_t)((scq[js / 8] >> (8 * (js % 8))) & 255u);
         scv[j] = h2v{v, v};
         nsc[j] = scv[j] * h2v{(_Float16)-64.f, (_Float16)-64.f};
@@ -2616,14 +2653,15 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
             const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, e2[j], 0x04030402u));
             const uint2 wv = make_uint2(__builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(a, scv[j], nsc[j])),
                                         __builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(b, scv[j], nsc[j])));
-            constexpr int pb = 16 * j + 8 * gi + p;  // position block of the 4 weights within the tile row
+            constexpr int g = NG * j + gi;           // 16-symbol group within the tile row
+            constexpr int pb = 8 * g + p;            // position block of the 4 weights within the tile row
 #pragma unroll
             for (int q = 0; q < NQ; ++q)
-              acc[j / 4][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[j / 4][q]);
+              acc[g / 8][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[g / 8][q]);
           } else {  // 2 codes per pair (fp16(q) in the entries' upper halves), 4 per product
             const uint32_t v = __builtin_bit_cast(uint32_t, (h2v)(__builtin_bit_cast(h2v, __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u)) * scv[j]));
             if constexpr (p & 1) {
-              constexpr int pb = 8 * j + 4 * gi + p / 2;
+              constexpr int pb = 4 * (NG * j + gi) + p / 2;
 #pragma unroll
               for (int q = 0; q < NQ; ++q)
                 acc[0][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[0][q]);
@@ -2634,6 +2672,27 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         });
       });
     });
+    // the products are formed here, not sunk past the claim and the copy below
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(acc[sb][q]));
+    // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
+    // so the buffer is free); the pending row's counter value arrived during the decode
+    {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      n = __builtin_amdgcn_readfirstlane((int)nx);
+    }
+    const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
+    have = n < per && T0 + n < plan.ntiles;
+    if (have) {
+      tile_of(n, sec, t);
+      uint32_t k = 0;
+      if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
+      copy_tile(sec ? eb : ea, t);
+    }
     // mins: per super-block and token, sum_j m_j (sum x)_j from the hi and lo halves of the sums
     f4v mac[NSB][NQ];
 #pragma unroll
@@ -2669,20 +2728,13 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         for (int sb = 0; sb < NSB; ++sb) tot = fmaf(dA[sb] * DSCALE, acc[sb][q][i], fmaf(-dB[sb], mac[sb][q][i], tot));
         if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-    finish_pending();
+    if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
+    pend = -1;
     if (E.Y) {
-      pend = sec;
+      pend = cur;
       ptr = tr;
       pKT = KT;
       pN = N;
-    }
-    uint32_t nx = 0;
-    if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    n = __builtin_amdgcn_readfirstlane((int)nx);
-    have = n < per && T0 + n < plan.ntiles;
-    if (have) {
-      tile_of(n, sec, t);
-      copy_tile(sec ? eb : ea, t);
     }
   }
   if (pend >= 0) {
@@ -2785,7 +2837,7 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
     // a block (`per` consecutive tiles) spans at most two matrices
-    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
+    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
         (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
       return hipErrorInvalidValue;
@@ -2857,7 +2909,7 @@ hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
-    if (e.M.kqt != kqt || !e.M.split || !e.M.lut4 || !e.M.rows || e.M.packed || !e.XS || e.tile0 + e.ntile != end ||
+    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || !e.XS || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
         (i == 0 && e.tile0 != 0))
       return hipErrorInvalidValue;

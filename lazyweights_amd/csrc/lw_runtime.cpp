@@ -652,7 +652,7 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   // 2..8 tokens of fp16 activations, Q4_K / Q5_K: the whole-tile kernel with its products on the matrix cores (its
   // per-sub-block x sums, XS, live next to the partials)
   auto mma_ok = [&](const lw::DevMat& dm) {
-    return (dm.kqt == lw::KQ_Q4_K || dm.kqt == lw::KQ_Q5_K) && !dm.packed && dm.split && dm.lut4 && dm.rows &&
+    return (dm.kqt == lw::KQ_Q4_K || dm.kqt == lw::KQ_Q5_K) && !dm.packed && dm.dsplit && dm.lut4 && dm.rows &&
            dm.max_rows + 2 <= 256;
   };
   const bool mma = !x8 && per == 1 && mt >= 2 && mt <= 8 && g_kernel_mode == 0;
@@ -801,10 +801,6 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
       }
       int tpb = 0;
       fp.W = tiles_width(fp, mintiles, tpb);
-      if (fp.W > 12) {  // the kernel's block limit (12 waves): the same tiles per block in more rounds
-        const int rounds = (tpb + 11) / 12;
-        fp.W = (tpb + rounds - 1) / rounds;
-      }
       if (fp.W < 1) continue;
       lw::XSumJobs xj{};
       xj.m = mt;
