@@ -72,7 +72,9 @@ struct FlatEntry {
   DevMat M;
   const uint32_t* X2;
   float* P;
-  const uint32_t* list;  // null: the matrix's tiles in column-major order; else these tile indices (exception pass)
+  // null: every tile of the matrix (the ring and packed kernels take them column-major, the whole-tile kernels
+  // row-major); else these tile indices (exception pass)
+  const uint32_t* list;
   int tile0, ntile;
   // Y non-null (the launch decodes every tile of the matrix): Y[n] = the ordered sum of P over tile columns, formed
   // in the launch by the last wave of each tile row; cnt = NT zeroed counters (left zeroed)
@@ -84,9 +86,6 @@ struct FlatEntry {
   const float* SX;
   // plan.mt > 1: P is [KT][mt][N] and token j's Y row starts at Y + j ldy
   int ldy;
-  // the matrix-core whole-tile kernel (fp16 activations, 2..8 tokens): per token and sub-block of 32 weights the
-  // sum of x as fp16 hi | lo << 16 ([mt][K / 32], launch_xsums16)
-  const uint32_t* XS;
 };
 struct FlatPlan {
   FlatEntry e[MAX_GROUP];
@@ -132,19 +131,12 @@ hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
 hipError_t launch_fused_halves(const FlatPlan& plan, int per, hipStream_t s);
 int halves_buf_rows(const FlatPlan& plan);
 int tiles_buf_rows(const FlatPlan& plan);
-// The whole-tile kernel for 2..8 tokens of fp16 activations (Q4_K / Q5_K, plan.mt tokens, entries' XS set): the
-// products on the matrix cores (4x4x4 blocks, x broadcast from one block), every token in one pass over the tiles
+// The whole-tile kernel for 2..8 tokens of fp16 activations (Q4_K / Q5_K, plan.mt tokens, every tile of each entry):
+// the products on the matrix cores (4x4x4 blocks, x broadcast from one block), every token in one pass over the
+// tiles; each block forms the x sums of its tile columns in LDS (tiles_mma_xs_bytes beside W tile buffers of
+// tiles_buf_rows word rows)
 hipError_t launch_fused_tiles_mma(const FlatPlan& plan, int per, hipStream_t s);
-// XS [m][K / 32] for launch_fused_tiles_mma: per token and sub-block the fp32 sum of X [m][K] (fp16) in quarter
-// order (q0 + q1) + (q2 + q3), as fp16 hi | fp16(sum - hi) << 16; up to MAX_GROUP matrices' x in one launch
-struct XSumJobs {
-  const uint32_t* X[MAX_GROUP];
-  uint32_t* XS[MAX_GROUP];
-  int K[MAX_GROUP];
-  int b0[MAX_GROUP];  // set by the launcher
-  int n, m;
-};
-hipError_t launch_xsums16(const XSumJobs& jobs, hipStream_t s);
+size_t tiles_mma_xs_bytes(const FlatPlan& plan, int per);
 
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
 // K-quant types or ring sizes, or a matrix has no ring schedule).

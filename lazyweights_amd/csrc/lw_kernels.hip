@@ -2477,11 +2477,13 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   uint32_t* next = lut4 + NTAB * LUTN;
   uint32_t* asked = next + 1;
   uint32_t* landed = next + 2;
+  uint32_t* xs_done = next + 3;  // waves done with their share of the x sums
   const int C = min(W, TILES_COPIES);
   if (threadIdx.x == 0) {
     next[0] = (uint32_t)W;
     asked[0] = (uint32_t)W;
     landed[0] = 0u;
+    xs_done[0] = 0u;
   }
   auto ask = [&](uint32_t k) {
     while (k >= (uint32_t)C + __hip_atomic_load(landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
@@ -2524,6 +2526,54 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   // this wave's table chunks and the counters are in place; then every wave's (a bare barrier: copies stay in flight)
   wait_vmcnt_upto(ncopy);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // The x sums of every tile column the block decodes, in LDS after the tile buffers (tiles_mma_xs_bytes): per
+  // column slot, token and group of 4 sub-blocks their sums in xsum_sub's order as 4 fp16 hi halves, then 4 fp16 lo
+  // halves. Column slots: the first entry's columns from ca0 (mod KT), then the second entry's from cb0. Formed by
+  // the waves that wait for their first copy's turn (all waves when none waits) before they ask for it; read once
+  // the block's counter shows every share stored.
+  constexpr int GPC = TW / 128;  // groups of 4 sub-blocks per tile column
+  auto cols = [&](KEntry* e, int u0, int u1, int& c0) {  // the columns of the entry's tiles u0 .. u1 (row-major)
+    const int KT = e->M.KT;
+    c0 = u1 - u0 + 1 >= KT ? 0 : u0 % KT;
+    return min(KT, u1 - u0 + 1);
+  };
+  int ca0 = 0, cb0 = 0;
+  const int nca = cols(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0, ca0);
+  const int ncb = (NTAB > 1 && mb != ma) ? cols(eb, 0, Tl - eb->tile0, cb0) : 0;
+  uint64_t* xsb = reinterpret_cast<uint64_t*>(tbuf + (size_t)W * buf_rows * 32);
+  const int xw0 = W > C ? C : 0, xnw = W - xw0;
+  if (wave >= xw0) {
+    const int na = nca * mt * GPC, ntot = na + ncb * mt * GPC;
+    for (int i = (wave - xw0) * 64 + lane; i < ntot; i += xnw * 64) {
+      const bool second = i >= na;
+      KEntry* e = second ? eb : ea;
+      const int ii = second ? i - na : i;
+      const int gq = ii % GPC, r = ii / GPC, tok = r % mt, lc = r / mt;
+      const int KT = e->M.KT, K = e->M.K;
+      int c = (second ? cb0 : ca0) + lc;
+      if (c >= KT) c -= KT;
+      const uint4* x4 = reinterpret_cast<const uint4*>(e->X2 + (size_t)tok * (K / 2) + (size_t)c * (TW / 2) + 64 * gq);
+      uint64_t hi4 = 0, lo4 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {  // sub-block 4 gq + k: 32 fp16 = 4 uint4
+        uint4 v[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v[w] = x4[4 * k + w];
+        const float sum = xsum_sub<32>([&](int d) {
+          const uint4& u = v[d >> 2];
+          return (d & 3) == 0 ? u.x : (d & 3) == 1 ? u.y : (d & 3) == 2 ? u.z : u.w;
+        });
+        const _Float16 hi = (_Float16)sum;
+        hi4 |= (uint64_t)__builtin_bit_cast(uint16_t, hi) << (16 * k);
+        lo4 |= (uint64_t)__builtin_bit_cast(uint16_t, (_Float16)(sum - (float)hi)) << (16 * k);
+      }
+      uint64_t* xs = xsb + ((size_t)((second ? nca : 0) + lc) * mt + tok) * (GPC * 2) + 2 * gq;
+      xs[0] = hi4;
+      xs[1] = lo4;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the stores are done
+    if (lane == 0) __hip_atomic_fetch_add(xs_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
   if (have && wave >= C) {
     ask((uint32_t)wave);
     copy_tile(sec ? eb : ea, t);
@@ -2539,8 +2589,16 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     if (mb != ma) touch(eb, 0, Tl - eb->tile0);
     asm volatile("" ::"s"(warm));
   }
+  // every share of the x sums stored: checked at each tile start until it holds; a tile that starts earlier (a
+  // first tile) reads its sums after its decode instead
+  bool xs_ready = false;
 #pragma unroll 1
   while (have) {
+    if (!xs_ready)
+      xs_ready = __builtin_amdgcn_readfirstlane((int)__hip_atomic_load(xs_done, __ATOMIC_RELAXED,
+                                                                        __HIP_MEMORY_SCOPE_WORKGROUP)) >= xnw;
+    asm volatile("" ::: "memory");
+    const bool xs_late = !xs_ready;
     const int cur = sec;
     const bool second = sec != 0;
     KEntry* ep = second ? eb : ea;
@@ -2561,8 +2619,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     }
     const uint32_t tsel = second ? 4u * LUTN : 0u;
     // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
-    // (zero for tokens >= mt); XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks, block b = (super-block,
-    // half, hi / lo) as 2 (2 sb + half) + (lo)
+    // (zero for tokens >= mt)
     h4v xa[NQ][NPR], xs[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
@@ -2574,17 +2631,21 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         const uint2 v = ok ? *reinterpret_cast<const uint2*>(xrow + 2 * (16 * m + qb)) : make_uint2(0u, 0u);
         xa[q][m] = __builtin_bit_cast(h4v, v);
       }
-      const int cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
-      uint2 sv = make_uint2(0u, 0u);
-      if (ok && qb < 4 * NSB) {
-        const uint32_t* xsr = E.XS + (size_t)tok * (K / 32) + (size_t)tc * (TW / 32) + 4 * sh;
-        const uint4 w4 = *reinterpret_cast<const uint4*>(xsr);
-        const uint32_t a0 = lo ? w4.x >> 16 : w4.x & 0xFFFFu, a1 = lo ? w4.y >> 16 : w4.y & 0xFFFFu;
-        const uint32_t a2 = lo ? w4.z >> 16 : w4.z & 0xFFFFu, a3 = lo ? w4.w >> 16 : w4.w & 0xFFFFu;
-        sv = make_uint2(a0 | a1 << 16, a2 | a3 << 16);
-      }
-      xs[q] = __builtin_bit_cast(h4v, sv);
     }
+    // XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks (hi or lo halves), block b = 2 (2 sb + half) + (lo)
+    auto load_xs = [&]() {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int tok = 4 * q + qi, cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
+        uint64_t sv = 0;
+        if (tok < mt && qb < 4 * NSB) {
+          const int lc = second ? nca + (tc - cb0 + KT) % KT : (tc - ca0 + KT) % KT;  // the column's slot
+          sv = xsb[((size_t)lc * mt + tok) * (GPC * 2) + 2 * sh + lo];
+        }
+        xs[q] = __builtin_bit_cast(h4v, sv);
+      }
+    };
+    if (!xs_late) load_xs();
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
     if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (pend >= 0 && lane == 0)
@@ -2674,9 +2735,17 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     });
     // the products are formed here, not sunk past the claim and the copy below
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb)
+    for (int sb = 0; sb < NSB; ++sb) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(acc[sb][q]));
+    }
+    if (xs_late) {  // this tile's sums, now that every share is stored
+      while (__hip_atomic_load(xs_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)xnw)
+        __builtin_amdgcn_s_sleep(2);
+      asm volatile("" ::: "memory");
+      load_xs();
+      xs_ready = true;
+    }
     // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
     // so the buffer is free); the pending row's counter value arrived during the decode
     {
@@ -2745,51 +2814,9 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
 }
 
-// per token and sub-block of 32 weights: fp32 sum of fp16 x in quarter order, as fp16 hi | lo << 16; one launch
-// over up to MAX_GROUP jobs (blocks [b0[i], b0[i + 1]) take job i)
-__global__ void __launch_bounds__(256) k_xsums16(XSumJobs jobs) {
-  int jb = 0;
-#pragma unroll
-  for (int i = 1; i < MAX_GROUP; ++i)
-    if (i < jobs.n && (int)blockIdx.x >= jobs.b0[i]) jb = i;
-  const uint32_t* __restrict__ X2 = jobs.X[jb];
-  uint32_t* __restrict__ XS = jobs.XS[jb];
-  const int m = jobs.m, K = jobs.K[jb];
-  const int i = ((int)blockIdx.x - jobs.b0[jb]) * 256 + threadIdx.x;
-  if (i >= m * (K / 32)) return;
-  const int tk = i / (K / 32), j = i - tk * (K / 32);
-  const uint32_t* x = X2 + (size_t)tk * (K / 2) + 16 * j;
-  float q[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    q[k] = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t v = x[4 * k + c];
-      q[k] += h2f(v) + h2f(v >> 16);
-    }
-  }
-  const float sum = (q[0] + q[1]) + (q[2] + q[3]);
-  const _Float16 hi = (_Float16)sum;
-  XS[i] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(sum - (float)hi)) << 16;
-}
-
-hipError_t launch_xsums16(const XSumJobs& jobs, hipStream_t s) {
-  if (jobs.n < 1 || jobs.n > MAX_GROUP || jobs.m < 1) return hipErrorInvalidValue;
-  XSumJobs q = jobs;
-  int blocks = 0;
-  for (int i = 0; i < q.n; ++i) {
-    if (q.K[i] % 32) return hipErrorInvalidValue;
-    q.b0[i] = blocks;
-    blocks += (q.m * (q.K[i] / 32) + 255) / 256;
-  }
-  hipLaunchKernelGGL(k_xsums16, dim3(blocks), dim3(256), 0, s, q);
-  return hipGetLastError();
-}
-
 template <int KQ, int NTAB, int MT>
 static hipError_t tiles_mma_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
-  const size_t smem = (size_t)p.W * buf_rows * 128;
+  const size_t smem = (size_t)p.W * buf_rows * 128 + tiles_mma_xs_bytes(p, per);
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles_mma<KQ, NTAB, MT>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
@@ -2823,10 +2850,12 @@ static hipError_t tiles_launch(const FlatPlan& p, int per, int buf_rows, hipStre
   return one ? tiles_launch_t<KQ, 1, false>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, false>(p, per, buf_rows, s);
 }
 
+// word rows of a whole-tile kernel's tile buffer: the longest tile of the plan and the 2 rows its windows read past
+// a lane's end (copies are masked to a tile's own rows, so no rounding to whole 1 KB copies is needed)
 int tiles_buf_rows(const FlatPlan& p) {
   int r = 0;
   for (int i = 0; i < p.n; ++i) r = std::max(r, p.e[i].M.max_rows + 2);
-  return (r + 7) / 8 * 8;
+  return r;
 }
 
 hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
@@ -2900,6 +2929,11 @@ hipError_t launch_fused_halves(const FlatPlan& p, int per, hipStream_t s) {
   }
 }
 
+size_t tiles_mma_xs_bytes(const FlatPlan& p, int per) {
+  // a block's tiles lie in at most per tile columns; per column and token 4 bytes per sub-block
+  return (size_t)std::max(per, 0) * std::max(p.mt, 0) * (kq_symbits(p.e[0].M.kqt) == 4 ? 2 * TK : TK) / 32 * 4;
+}
+
 hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > TILES_MMA_WAVES || per < p.W || p.ntiles < 1 || p.mt < 1 ||
       p.mt > 8 || p.i8)
@@ -2909,13 +2943,15 @@ hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
-    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || !e.XS || e.tile0 + e.ntile != end ||
-        e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
+    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
+        e.ntile < 1 || (p.n > 1 && e.ntile < per) || e.list || e.ntile != e.M.NT * e.M.KT ||
         (i == 0 && e.tile0 != 0))
       return hipErrorInvalidValue;
   }
   const int rows = tiles_buf_rows(p);
-  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  if (rows > 256 ||
+      (size_t)p.W * rows * 128 + tiles_mma_xs_bytes(p, per) + (p.n > 1 ? 2 : 1) * 4 * LUTN + 16 > 160 * 1024)
+    return hipErrorInvalidValue;
   return kqt == KQ_Q4_K ? tiles_mma_launch<KQ_Q4_K>(p, per, rows, s) : tiles_mma_launch<KQ_Q5_K>(p, per, rows, s);
 }
 

@@ -121,8 +121,6 @@ struct Model {
   size_t X16_cap = 0;
   uint16_t* SX = nullptr;  // per-sub-block activation sums (prefill GEMM)
   size_t SX_cap = 0;
-  uint32_t* XSb = nullptr;  // per-sub-block activation sums as fp16 hi | lo (the m = 2..8 matrix-core kernel)
-  size_t XSb_cap = 0;
   uint8_t* x8 = nullptr;  // int8 activations: per vector [K int8][K / 32 d][K / 32 d sum q], 256-B aligned parts
   size_t x8_cap = 0;
   uint8_t* codes = nullptr;
@@ -437,7 +435,6 @@ void release(Model* M) {
   if (M->cnt) (void)hipFree(M->cnt);
   if (M->X16) (void)hipFree(M->X16);
   if (M->SX) (void)hipFree(M->SX);
-  if (M->XSb) (void)hipFree(M->XSb);
   if (M->x8) (void)hipFree(M->x8);
   if (M->codes) (void)hipFree(M->codes);
   if (M->W16) (void)hipFree(M->W16);
@@ -618,6 +615,22 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   return std::min(wmax, (per + rounds - 1) / rounds);
 }
 
+// Waves per block and tiles per block of the matrix-core whole-tile kernel (2..8 tokens): the tiles as tiles_width,
+// each block's x sums (tiles_mma_xs_bytes) beside the tile buffers, and as many waves as the LDS holds (measured at
+// m = 2..8 on config 2: 12 waves taking 26 tiles in rounds of 12, 12 and 2 ran 6-9 % faster than 9 waves in 3
+// rounds, unlike the m = 1 kernel). Returns 0 if no width fits.
+int tiles_mma_width(const lw::FlatPlan& fp, int mintiles, int& per) {
+  const int cus = cu_count();
+  const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
+  if (rows > 256) return 0;
+  per = (fp.ntiles + cus - 1) / cus;
+  if (fp.n > 1) per = std::min(per, mintiles);
+  const long room = 160L * 1024 - tables - 16 - (long)lw::tiles_mma_xs_bytes(fp, per);
+  const int wmax = (int)std::min<long>(16, room / (rows * 128L));
+  if (wmax < 1) return 0;
+  return std::min(wmax, per);
+}
+
 // Waves per block and tiles per block of the half-tile kernel: two unit buffers per wave (halves_buf_rows) next to
 // one or two 8 KB tables; `per` as tiles_width; every wave starts on a unit (at most 2 per waves). Returns 0 if no
 // width fits.
@@ -649,23 +662,52 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + 2 * (size_t)ts[i]->dm.NT;  // per tile row and half
   // partials and counters: the model's (grown on demand) or a caller's fixed scratch (nothing allocated; its counters
   // are cleared by a fill kernel on the stream, since the last call on that scratch may have left anything there)
-  // 2..8 tokens of fp16 activations, Q4_K / Q5_K: the whole-tile kernel with its products on the matrix cores (its
-  // per-sub-block x sums, XS, live next to the partials)
+  // 2..8 tokens of fp16 activations, Q4_K / Q5_K: the whole-tile kernel with its products on the matrix cores
   auto mma_ok = [&](const lw::DevMat& dm) {
     return (dm.kqt == lw::KQ_Q4_K || dm.kqt == lw::KQ_Q5_K) && !dm.packed && dm.dsplit && dm.lut4 && dm.rows &&
            dm.max_rows + 2 <= 256;
   };
   const bool mma = !x8 && per == 1 && mt >= 2 && mt <= 8 && g_kernel_mode == 0;
-  size_t xs_words = 0;
-  for (int i = 0; mma && i < count; ++i)
-    if (mma_ok(ts[i]->dm)) xs_words += (size_t)mt * (ts[i]->K / 32);
+  // its launches: matrices of one K-quant type, up to MAX_GROUP each
+  struct MmaLaunch {
+    lw::FlatPlan fp;
+    int tpb;
+    std::vector<int> sel;
+  };
+  std::vector<MmaLaunch> mma_plans;
+  if (mma) {
+    std::vector<char> mdone(count, 0);
+    for (int i = 0; i < count; ++i) {
+      if (mdone[i] || !mma_ok(ts[i]->dm)) continue;
+      MmaLaunch L{};
+      L.fp.mt = mt;
+      int mintiles = 1 << 30;
+      for (int j = i; j < count && L.fp.n < lw::MAX_GROUP; ++j) {
+        const lw::DevMat& dm = ts[j]->dm;
+        if (mdone[j] || !mma_ok(dm) || dm.kqt != ts[i]->dm.kqt) continue;
+        lw::FlatEntry& e = L.fp.e[L.fp.n++];
+        e.M = dm;
+        e.X2 = static_cast<const uint32_t*>(X16[j]);
+        e.tile0 = L.fp.ntiles;
+        e.ntile = dm.NT * dm.KT;
+        e.Y = Y[j];
+        e.ldy = ldy[j];
+        L.fp.ntiles += e.ntile;
+        mintiles = std::min(mintiles, e.ntile);
+        L.sel.push_back(j);
+      }
+      L.fp.W = tiles_mma_width(L.fp, mintiles, L.tpb);
+      if (L.fp.W < 1) continue;
+      for (int j : L.sel) mdone[j] = 1;
+      mma_plans.push_back(std::move(L));
+    }
+  }
   float* Pb = nullptr;
   uint32_t* Cb = nullptr;
-  uint32_t* XSb = nullptr;
   if (fixed) {
     const size_t cnt_bytes = (coff[count] * sizeof(uint32_t) + 255) & ~(size_t)255;
     const size_t p_bytes = (off[count] * sizeof(float) + 255) & ~(size_t)255;
-    const size_t need = cnt_bytes + p_bytes + xs_words * sizeof(uint32_t);
+    const size_t need = cnt_bytes + p_bytes;
     if (need > fixed->bytes) {
       g_err = "scratch of " + std::to_string(fixed->bytes) + " bytes is too small: this call needs " +
               std::to_string(need);
@@ -673,15 +715,12 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     Cb = reinterpret_cast<uint32_t*>(fixed->base);
     Pb = reinterpret_cast<float*>(fixed->base + cnt_bytes);
-    XSb = reinterpret_cast<uint32_t*>(fixed->base + cnt_bytes + p_bytes);
     HIPCHECK(lw::launch_fill_u32(Cb, coff[count], 0u, s));
   } else {
     if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
     if (grow_zeroed(M.cnt, M.cnt_cap, coff[count] * sizeof(uint32_t))) return -1;
-    if (xs_words && grow(M.XSb, M.XSb_cap, xs_words * sizeof(uint32_t))) return -1;
     Pb = M.P;
     Cb = M.cnt;
-    XSb = M.XSb;
   }
   std::vector<char> reduced(count, 0);  // entries whose reduction runs inside their flat launch
   lw::GroupPlan plan{};
@@ -773,48 +812,15 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   }
   // the matrix-core whole-tile launches: every tile of their matrices and the reduction in the launch (the ring
   // kernel for the other formats and kernel modes)
-  if (mma) {
-    size_t xoff = 0;
-    for (int i = 0; i < count; ++i) {
-      if (done[i] || !mma_ok(ts[i]->dm)) continue;
-      lw::FlatPlan fp{};
-      fp.mt = mt;
-      std::vector<int> sel;
-      int mintiles = 1 << 30;
-      for (int j = i; j < count && fp.n < lw::MAX_GROUP; ++j) {
-        const lw::DevMat& dm = ts[j]->dm;
-        if (done[j] || !mma_ok(dm) || dm.kqt != ts[i]->dm.kqt) continue;
-        lw::FlatEntry& e = fp.e[fp.n++];
-        e.M = dm;
-        e.X2 = static_cast<const uint32_t*>(X16[j]);
-        e.P = Pb + off[j];
-        e.tile0 = fp.ntiles;
-        e.ntile = dm.NT * dm.KT;
-        e.Y = Y[j];
-        e.cnt = Cb + coff[j];
-        e.ldy = ldy[j];
-        e.XS = XSb + xoff;
-        xoff += (size_t)mt * (ts[j]->K / 32);
-        fp.ntiles += e.ntile;
-        mintiles = std::min(mintiles, e.ntile);
-        sel.push_back(j);
-      }
-      int tpb = 0;
-      fp.W = tiles_width(fp, mintiles, tpb);
-      if (fp.W < 1) continue;
-      lw::XSumJobs xj{};
-      xj.m = mt;
-      for (int k = 0; k < fp.n; ++k) {
-        xj.X[xj.n] = fp.e[k].X2;
-        xj.XS[xj.n] = const_cast<uint32_t*>(fp.e[k].XS);
-        xj.K[xj.n++] = fp.e[k].M.K;
-        done[sel[k]] = reduced[sel[k]] = exc_in[sel[k]] = whole[sel[k]] = 1;
-      }
-      HIPCHECK(lw::launch_xsums16(xj, s));
-      if (launches) ++*launches;
-      HIPCHECK(lw::launch_fused_tiles_mma(fp, tpb, s));
-      if (launches) ++*launches;
+  for (MmaLaunch& L : mma_plans) {
+    for (int k = 0; k < L.fp.n; ++k) {
+      const int j = L.sel[k];
+      L.fp.e[k].P = Pb + off[j];
+      L.fp.e[k].cnt = Cb + coff[j];
+      done[j] = reduced[j] = exc_in[j] = whole[j] = 1;
     }
+    HIPCHECK(lw::launch_fused_tiles_mma(L.fp, L.tpb, s));
+    if (launches) ++*launches;
   }
   for (int i = 0; flat && i < count; ++i) {
     if (done[i]) continue;
