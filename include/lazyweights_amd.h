@@ -100,8 +100,8 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
 
 /* Fused-kernel selection for all handles. 0 (default): m = 1 with fp16 activations, the whole-tile kernel (a tile
  * per wave copied to LDS, 8 chains per lane, every tile including exception tiles), or the half-tile kernel (two
- * buffered half-tile units per wave, the next one's copy in flight while one decodes) where a launch's blocks would
- * give the whole-tile waves fewer than two tiles each; m = 1 with int8 activations, the whole-tile kernel;
+ * buffered half-tile units per wave, the next one's copy in flight while one decodes) where the whole-tile kernel's
+ * blocks would have fewer than 10 waves (few tiles per CU); m = 1 with int8 activations, the whole-tile kernel;
  * 2 <= m <= 8 with fp16 activations and Q4_K / Q5_K, the whole-tile kernel with its products on the matrix cores;
  * otherwise the ring-staged kernels wherever a matrix has a ring schedule (the flat kernel for int8 activations, the
  * block-per-column kernel otherwise). 1 = the whole-tile fallback kernel everywhere; 2 = the block-per-column ring
