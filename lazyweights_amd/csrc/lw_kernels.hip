@@ -30,6 +30,7 @@ constexpr int kBufferRsrcWord3 = 0x00020000;  // buffer descriptor word 3 for ra
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef int v4i32 __attribute__((ext_vector_type(4)));
 typedef float f16x16 __attribute__((ext_vector_type(16)));
 
 // Activations of MT pseudo-tokens staged in LDS as fp16 pairs: pair c (weights 2c, 2c + 1) of token j. With
@@ -2832,6 +2833,369 @@ static hipError_t tiles_mma_launch(const FlatPlan& p, int per, int buf_rows, hip
   return one ? tiles_mma_launch_t<KQ, 1, 8>(p, per, buf_rows, s) : tiles_mma_launch_t<KQ, 2, 8>(p, per, buf_rows, s);
 }
 
+// ── whole-tile kernel on the matrix cores for int8 activations (2..8 tokens, every format) ─────────────────
+// The decode and tile pipeline of k_fused_tiles_mma; the products on v_mfma_i32_4x4x4i8 over the int8 grid values
+// of the load-time int8 table (Q4_K q, Q5_K q, Q6_K q - 32, IQ4_XS kv[q]) and x quantized per block of 32
+// (launch_quant_x8: XQ, and per block DX = d, SX = d sum q). Block b of the instruction computes
+// D[i][j] = sum_k A[4 b' + i][k] B[4 b + j][k] into lane 4 b + j, register i (checked on the GPU): B = the lane's own
+// 4 weights of a position block, A = 4 tokens' int8 x there, broadcast from block b' of a register that holds 16
+// position blocks (one dword per lane). Each chain's integer sums per sub-block (exact) are folded into fp32 when
+// the sub-block ends: y_t += dA s_j d_x(t, block) acc; the Q4_K / Q5_K offset term dB sum_j m_j SX(t, j) runs on
+// v_mfma_f32_4x4x4f16 with SX split into fp16 hi and lo, as the fp16 kernel's mins term. Each token's values agree
+// with its own m = 1 int8 launch to fp32 rounding (another order of the same exact sub-block sums).
+// at most 16 waves per block; 12 (3 per SIMD) for 8 tokens of the 4-bit formats, whose 8 tokens' x, 4 chains'
+// integer accumulators per token quad and the chains take more than 128 VGPRs
+constexpr int tiles_mma8_waves(int kqt, int mt) { return mt == 8 && kq_symbits(kqt) == 4 ? 12 : TILES_MMA_WAVES; }
+template <int KQ, int NTAB, int MT>
+__global__ void __launch_bounds__(64 * tiles_mma8_waves(KQ, MT), 1)
+k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
+  static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
+  constexpr int SYMB = kq_symbits(KQ);
+  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+  constexpr int SB = kq_sbytes(KQ), GW = kq_gw(KQ);
+  constexpr int NSB = TW / 256;                          // super-blocks per tile row
+  constexpr int NSUB = 256 / GW;                         // sub-blocks per super-block
+  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
+  constexpr bool MINS = KQ == KQ_Q4_K || KQ == KQ_Q5_K;
+  constexpr bool SIGNED = KQ == KQ_Q6_K || KQ == KQ_IQ4_XS;  // signed sub-block scales
+  constexpr int XB = TW / 32;                            // x blocks of 32 per tile column
+  constexpr int NQ = MT / 4;                             // token quads
+  constexpr int NPR = TW / 64;                           // x registers per quad (16 position blocks of 4 each)
+  constexpr int NC = 4, NG = 16 / NC;                    // chains per lane (64 symbols each), groups per chain
+  typedef __attribute__((address_space(3))) const uint32_t LdsU32;
+  typedef __attribute__((address_space(4))) const char KChar;
+  typedef __attribute__((address_space(4))) const FlatEntry KEntry;
+  typedef __attribute__((address_space(4))) const uint32_t KU32;
+  typedef __attribute__((address_space(4))) const uint16_t KU16;
+  __shared__ uint32_t lut4[NTAB * LUTN + 4];
+  extern __shared__ __align__(16) uint32_t tbuf[];
+
+  KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int W = plan.W, T0 = (int)blockIdx.x * per, Tl = min(T0 + per, plan.ntiles) - 1, mt = plan.mt;
+  int ma = 0, mb = 0;
+#pragma unroll
+  for (int i = 1; i < MAX_GROUP; ++i) {
+    if (i < plan.n && T0 >= plan.e[i].tile0) ma = i;
+    if (i < plan.n && Tl >= plan.e[i].tile0) mb = i;
+  }
+  KEntry* ea = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)ma * sizeof(FlatEntry));
+  KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
+  const int qb = lane >> 2, qi = lane & 3;  // 4-lane block and the lane's place in it
+  {  // the int8 tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W
+    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.luti8);
+    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.luti8);
+    const int nchunk = (NTAB > 1 && mb != ma) ? 16 : 8;
+    for (int c = wave; c < nchunk; c += W)
+      __builtin_amdgcn_global_load_lds((c < 8 ? ta : tb) + 64 * (c & 7) + lane,
+                                       (__attribute__((address_space(3))) void*)(lut4 + 256 * c), 16, 0, 0);
+  }
+  // copies paced as in k_fused_tiles
+  uint32_t* next = lut4 + NTAB * LUTN;
+  uint32_t* asked = next + 1;
+  uint32_t* landed = next + 2;
+  const int C = min(W, TILES_COPIES);
+  if (threadIdx.x == 0) {
+    next[0] = (uint32_t)W;
+    asked[0] = (uint32_t)W;
+    landed[0] = 0u;
+  }
+  auto ask = [&](uint32_t k) {
+    while (k >= (uint32_t)C + __hip_atomic_load(landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+      __builtin_amdgcn_s_sleep(2);
+  };
+  uint32_t* buf = tbuf + (size_t)wave * buf_rows * 32;
+  const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(buf + s);
+  uint32_t tmask = 0x1FFCu;
+  asm volatile("" : "+v"(tmask));
+  auto tile_of = [&](int n, int& sec, int& t) {  // row-major, as k_fused_tiles
+    const int T = T0 + n;
+    sec = __builtin_amdgcn_readfirstlane((NTAB > 1 && mb != ma && T >= eb->tile0) ? 1 : 0);
+    KEntry* e = sec ? eb : ea;
+    const int u = T - e->tile0;
+    t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
+  };
+  auto copy_tile = [&](KEntry* e, int t) -> int {  // as k_fused_tiles: the tile's own rows, the last copy masked
+    const int nrow = (int)((KU16*)e->M.rows)[t];
+    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+    const int nc = (nrow + 7) / 8;
+    for (int i = 0; i < nc; ++i)
+      if (lane < 8 * (nrow - 8 * i))
+        __builtin_amdgcn_global_load_lds(src + 64 * i, (__attribute__((address_space(3))) void*)(buf + 256 * i), 16, 0, 0);
+    return nc;
+  };
+  int pend = -1;
+  int ptr = 0, pKT = 0, pN = 0;
+  uint32_t pold = 0;
+  auto finish_pending = [&]() {
+    if (pend < 0) return;
+    const uint32_t old = (uint32_t)__builtin_amdgcn_readlane((int)pold, 0);
+    if (old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
+    pend = -1;
+  };
+  int n = wave;
+  bool have = n < per && T0 + n < plan.ntiles;
+  int sec = 0, t = 0, ncopy = 0;
+  if (have) tile_of(n, sec, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  wait_vmcnt_upto(ncopy);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (have && wave >= C) {
+    ask((uint32_t)wave);
+    copy_tile(sec ? eb : ea, t);
+  }
+  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+    uint32_t warm = 0;
+    auto touch = [&](KEntry* e, int u0, int u1) {
+      if (e->list) return;
+      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
+      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+    };
+    touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
+    if (mb != ma) touch(eb, 0, Tl - eb->tile0);
+    asm volatile("" ::"s"(warm));
+  }
+#pragma unroll 1
+  while (have) {
+    const int cur = sec;
+    const bool second = sec != 0;
+    KEntry* ep = second ? eb : ea;
+    const auto& E = *ep;
+    const auto& M = E.M;
+    const int KT = M.KT, N = M.N, K = M.K;
+    const int tc = t % KT, tr = t / KT;
+    const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+    uint32_t sw[NSB][5];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+    uint32_t P[NC];
+    {
+      uint32_t P8[8];
+      tile_chain_starts(M, t, f, s, P8);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) P[j] = P8[j * (8 / NC)];
+    }
+    const uint32_t tsel = second ? 4u * LUTN : 0u;
+    // x of the tile column: register m of quad q, lane 4 b + i = token 4 q + i's int8 x at positions 4 (16 m + b) ..
+    // + 3 (zero for tokens >= mt); its block scales d as two lane-distributed registers (value i = token i / XB,
+    // block i % XB: read back with v_readlane)
+    uint32_t xa[NQ][NPR];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int tok = 4 * q + qi;
+      const bool ok = tok < mt;
+      const uint32_t* xrow = reinterpret_cast<const uint32_t*>(E.XQ + (size_t)(ok ? tok : 0) * K + (size_t)tc * TW);
+#pragma unroll
+      for (int m = 0; m < NPR; ++m) xa[q][m] = ok ? xrow[16 * m + qb] : 0u;
+    }
+    float dxv[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int v = 64 * r + lane, tok = v / XB;
+      dxv[r] = tok < mt ? E.DX[(size_t)tok * (K / 32) + (size_t)tc * XB + v % XB] : 0.f;
+    }
+    // the offset term's A operand: lane 4 b + i = token 4 q + i's SX of 4 sub-blocks as fp16 hi or lo halves,
+    // block b = 2 (2 sb + half) + (lo) (Q4_K / Q5_K: a sub-block is one x block)
+    h4v xs[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int tok = 4 * q + qi, cb = qb & 7, lo = cb & 1, sh = cb >> 1;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (MINS && tok < mt && qb < 4 * NSB) v = *reinterpret_cast<const float4*>(E.SX + (size_t)tok * (K / 32) + (size_t)tc * XB + 4 * sh);
+      xs[q] = h4v{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+      if (lo)
+        xs[q] = h4v{(_Float16)(v.x - (float)xs[q][0]), (_Float16)(v.y - (float)xs[q][1]),
+                    (_Float16)(v.z - (float)xs[q][2]), (_Float16)(v.w - (float)xs[q][3])};
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
+    if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (pend >= 0 && lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t slot[NC], A[NC], B[NC], Cw[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+      Cw[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+    }
+    uint64_t scq[NSB], scq2[NSB];
+    float dA[NSB], dB[NSB];
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) side_packed<KQ>(sw[sb], scq[sb], scq2[sb], dA[sb], dB[sb]);
+    v4i32 ia[NC][NQ];
+    float fa[NQ][4];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[q][i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) ia[j][q] = v4i32{0, 0, 0, 0};
+    }
+    uint32_t wprev[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) wprev[j] = 0;
+    static_for<NG>([&](auto gic) {
+      constexpr int gi = decltype(gic)::value;
+      static_for<8>([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        uint32_t w1[NC], e1[NC], e2[NC];
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
+          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          P[j] = P[j] + e1[j] + e2[j];
+          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+          const bool slide = nslot != slot[j];
+          A[j] = slide ? B[j] : A[j];
+          B[j] = slide ? Cw[j] : B[j];
+          slot[j] = nslot;
+          Cw[j] = *(LdsU32*)(rlb + (nslot << 7));
+        }
+        static_for<NC>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          constexpr int g = NG * j + gi;  // 16-symbol group within the tile row
+          if constexpr (SYMB == 4) {      // 4 weights: the grid bytes of both entries, in weight order
+            constexpr int pb = 8 * g + p;
+            const int w = (int)__builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+              ia[j][q] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)xa[q][pb >> 4], w, ia[j][q], 4, pb & 15, 0);
+          } else {  // 2 weights per pair, 4 per product
+            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x0C0C0602u);
+            if constexpr (p & 1) {
+              constexpr int pb = 4 * g + p / 2;
+#pragma unroll
+              for (int q = 0; q < NQ; ++q)
+                ia[j][q] = __builtin_amdgcn_mfma_i32_4x4x4i8((int)xa[q][pb >> 4], (int)(wprev[j] | v << 16), ia[j][q],
+                                                              4, pb & 15, 0);
+            } else {
+              wprev[j] = v;
+            }
+          }
+        });
+      });
+      // sub-blocks ending with this group: y_t += dA s_j d_x(t, block) acc, then acc = 0
+      if constexpr ((gi + 1) % GPSUB == 0) {
+        static_for<NC>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          constexpr int js = (NG * j + gi) / GPSUB;  // sub-block within the tile row
+          constexpr int sb = js / NSUB, jj = js % NSUB, xb = js * GW / 32;
+          const uint64_t sq = jj < 8 ? scq[sb] : scq2[sb];
+          const uint32_t byte = (uint32_t)(sq >> (8 * (jj % 8))) & 255u;
+          const float sa = dA[sb] * (SIGNED ? (float)(int)(int8_t)(uint8_t)byte : (float)byte);
+#pragma unroll
+          for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int v = (4 * q + i) * XB + xb;  // a constant after unrolling
+              const float dx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dxv[v >> 6]), v & 63));
+              fa[q][i] = fmaf((float)ia[j][q][i], sa * dx, fa[q][i]);
+              ia[j][q][i] = 0;
+            }
+        });
+      }
+    });
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[q][i]));
+    // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode)
+    {
+      uint32_t nx = 0;
+      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      n = __builtin_amdgcn_readfirstlane((int)nx);
+    }
+    const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
+    have = n < per && T0 + n < plan.ntiles;
+    if (have) {
+      tile_of(n, sec, t);
+      uint32_t k = 0;
+      if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
+      copy_tile(sec ? eb : ea, t);
+    }
+    float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
+    f4v mac[NSB][NQ];
+    if constexpr (MINS) {  // per super-block and token, sum_j m_j SX_j from the hi and lo halves
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) {
+        float mf[8];
+        side_mins(sw[sb], mf);
+        const h4v m0 = h4v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3]};
+        const h4v m1 = h4v{(_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          f4v r = {0.f, 0.f, 0.f, 0.f};
+          if (sb == 0) {
+            r = mfma4_from<0>(xs[q], m0, r);
+            r = mfma4_from<1>(xs[q], m0, r);
+            r = mfma4_from<2>(xs[q], m1, r);
+            r = mfma4_from<3>(xs[q], m1, r);
+          } else {
+            r = mfma4_from<4>(xs[q], m0, r);
+            r = mfma4_from<5>(xs[q], m0, r);
+            r = mfma4_from<6>(xs[q], m1, r);
+            r = mfma4_from<7>(xs[q], m1, r);
+          }
+          mac[sb][q] = r;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float tot = fa[q][i];
+        if constexpr (MINS) {
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb) tot = fmaf(-dB[sb], mac[sb][q][i], tot);
+        }
+        if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
+    pend = -1;
+    if (E.Y) {
+      pend = cur;
+      ptr = tr;
+      pKT = KT;
+      pN = N;
+    }
+  }
+  if (pend >= 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0)
+      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finish_pending();
+  }
+}
+
+template <int KQ, int NTAB, int MT>
+static hipError_t tiles_mma8_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  const size_t smem = (size_t)p.W * buf_rows * 128;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles_mma8<KQ, NTAB, MT>),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+  if (e != hipSuccess) return e;
+  const int blocks = (p.ntiles + per - 1) / per;
+  hipLaunchKernelGGL((k_fused_tiles_mma8<KQ, NTAB, MT>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
+  return hipGetLastError();
+}
+
+template <int KQ>
+static hipError_t tiles_mma8_launch(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  const bool one = p.n == 1;
+  if (p.mt <= 4) return one ? tiles_mma8_launch_t<KQ, 1, 4>(p, per, buf_rows, s) : tiles_mma8_launch_t<KQ, 2, 4>(p, per, buf_rows, s);
+  return one ? tiles_mma8_launch_t<KQ, 1, 8>(p, per, buf_rows, s) : tiles_mma8_launch_t<KQ, 2, 8>(p, per, buf_rows, s);
+}
+
 template <int KQ, int NTAB, bool I8>
 static hipError_t tiles_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128;
@@ -2930,8 +3294,37 @@ hipError_t launch_fused_halves(const FlatPlan& p, int per, hipStream_t s) {
 }
 
 size_t tiles_mma_xs_bytes(const FlatPlan& p, int per) {
-  // a block's tiles lie in at most per tile columns; per column and token 4 bytes per sub-block
+  // a block's tiles lie in at most per tile columns; per column and token 4 bytes per sub-block (int8 activations
+  // bring their block sums: none)
+  if (p.i8) return 0;
   return (size_t)std::max(per, 0) * std::max(p.mt, 0) * (kq_symbits(p.e[0].M.kqt) == 4 ? 2 * TK : TK) / 32 * 4;
+}
+
+int tiles_mma8_max_waves(int kqt, int mt) { return tiles_mma8_waves(kqt, mt <= 4 ? 4 : 8); }
+
+hipError_t launch_fused_tiles_mma8(const FlatPlan& p, int per, hipStream_t s) {
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || per < p.W || p.ntiles < 1 || p.mt < 1 || p.mt > 8 || !p.i8 ||
+      p.W > tiles_mma8_max_waves(p.e[0].M.kqt, p.mt))
+    return hipErrorInvalidValue;
+  const int kqt = p.e[0].M.kqt;
+  for (int i = 0; i < p.n; ++i) {
+    const FlatEntry& e = p.e[i];
+    const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
+    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.luti8 || !e.M.rows || e.M.packed || !e.XQ || !e.DX ||
+        !e.SX || e.tile0 + e.ntile != end || e.ntile < 1 || (p.n > 1 && e.ntile < per) || e.list ||
+        e.ntile != e.M.NT * e.M.KT || (i == 0 && e.tile0 != 0))
+      return hipErrorInvalidValue;
+  }
+  const int rows = tiles_buf_rows(p);
+  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN + 16 > 160 * 1024)
+    return hipErrorInvalidValue;
+  switch (kqt) {
+    case KQ_Q4_K: return tiles_mma8_launch<KQ_Q4_K>(p, per, rows, s);
+    case KQ_Q5_K: return tiles_mma8_launch<KQ_Q5_K>(p, per, rows, s);
+    case KQ_Q6_K: return tiles_mma8_launch<KQ_Q6_K>(p, per, rows, s);
+    case KQ_IQ4_XS: return tiles_mma8_launch<KQ_IQ4_XS>(p, per, rows, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {

@@ -822,6 +822,37 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     HIPCHECK(lw::launch_fused_tiles_mma(L.fp, L.tpb, s));
     if (launches) ++*launches;
   }
+  // int8 activations, 2..8 tokens (kernel mode 0): the whole-tile kernel with its integer products on the matrix
+  // cores, every format, one launch per K-quant type and MAX_GROUP matrices; the reduction in the launch
+  for (int i = 0; x8 && mt >= 2 && mt <= 8 && g_kernel_mode == 0 && i < count; ++i) {
+    auto ok8 = [&](const lw::DevMat& dm) { return !dm.packed && dm.dsplit && dm.luti8 && dm.rows && dm.max_rows + 2 <= 256; };
+    if (done[i] || !ok8(ts[i]->dm)) continue;
+    lw::FlatPlan fp{};
+    std::vector<int> sel;
+    int mintiles = 1 << 30;
+    for (int j = i; j < count && fp.n < lw::MAX_GROUP; ++j) {
+      const lw::DevMat& dm = ts[j]->dm;
+      if (done[j] || !ok8(dm) || dm.kqt != ts[i]->dm.kqt) continue;
+      lw::FlatEntry& e = fp.e[fp.n++];
+      e.M = dm;
+      set8(fp, e, j);
+      e.P = Pb + off[j];
+      e.tile0 = fp.ntiles;
+      e.ntile = dm.NT * dm.KT;
+      e.Y = Y[j];
+      e.cnt = Cb + coff[j];
+      fp.ntiles += e.ntile;
+      mintiles = std::min(mintiles, e.ntile);
+      sel.push_back(j);
+    }
+    int tpb = 0;
+    fp.W = tiles_mma_width(fp, mintiles, tpb);  // (plan.i8: no x sums in LDS)
+    fp.W = std::min(fp.W, lw::tiles_mma8_max_waves(fp.e[0].M.kqt, mt));
+    if (fp.W < 1) continue;
+    for (int j : sel) done[j] = reduced[j] = exc_in[j] = whole[j] = 1;
+    HIPCHECK(lw::launch_fused_tiles_mma8(fp, tpb, s));
+    if (launches) ++*launches;
+  }
   for (int i = 0; flat && i < count; ++i) {
     if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
