@@ -140,7 +140,7 @@ size_t tiles_mma_xs_bytes(const FlatPlan& plan, int per);
 // The same for int8 activations (plan.i8, 2..8 tokens, every format; the entries' XQ / DX / SX from
 // launch_quant_x8): integer products on the matrix cores per sub-block, folded with the block scales in fp32
 hipError_t launch_fused_tiles_mma8(const FlatPlan& plan, int per, hipStream_t s);
-int tiles_mma8_max_waves(int kqt, int mt);  // its block limit
+int tiles_mma_max_waves(int kqt, int mt);  // the block limit of both matrix-core whole-tile kernels
 
 // One launch of the ring kernel over all matrices of the plan (returns hipErrorInvalidValue if the plan mixes
 // K-quant types or ring sizes, or a matrix has no ring schedule).

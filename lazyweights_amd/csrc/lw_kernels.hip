@@ -2408,8 +2408,10 @@ k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
 // m = 1 launch to fp32 rounding (another order of the same products). Partials [KT][mt][N], the in-launch reduction.
 // The tile pipeline is k_fused_tiles': tables by direct-to-LDS loads, paced first copies, row-major tiles, the next
 // tile's copy issued as soon as a decode ends.
-// at most 16 waves per block (4 per SIMD: 128 VGPRs hold the 8 chains with 8 tokens' x and accumulators)
+// at most 16 waves per block (4 per SIMD: 128 VGPRs); 12 (3 per SIMD) for 8 tokens of the 4-bit formats, whose
+// 8 tokens' x, the 4 chains' accumulators per token quad and the chains take more than 128 VGPRs
 constexpr int TILES_MMA_WAVES = 16;
+constexpr int tiles_mma_waves(int kqt, int mt) { return mt == 8 && kq_symbits(kqt) == 4 ? 12 : TILES_MMA_WAVES; }
 
 // compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1 (indices that must be constants: MFMA
 // broadcast fields, register-array indices)
@@ -2432,7 +2434,7 @@ __device__ __forceinline__ f4v mfma4_from(h4v a, h4v b, f4v c) {
 }
 
 template <int KQ, int NTAB, int MT>
-__global__ void __launch_bounds__(64 * TILES_MMA_WAVES, 1)
+__global__ void __launch_bounds__(64 * tiles_mma_waves(KQ, MT), 1)
 k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   static_assert(KQ == KQ_Q4_K || KQ == KQ_Q5_K, "scaled codes are exact in fp16 for Q4_K / Q5_K only");
   static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
@@ -2444,7 +2446,10 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
   constexpr int NC = 4, NG = 16 / NC;  // chains per lane (64 symbols each: 8 tokens' x and accumulators leave no
                                        // registers for 8 chains at 4 waves per SIMD), 16-symbol groups per chain
-  constexpr float DSCALE = SYMB == 4 ? 16.f : 1.f;
+  constexpr int GPSUB = SYMB == 4 ? 1 : 2;  // 16-symbol groups per sub-block of 32 weights
+  // the weights enter unscaled: 4-bit codes as fp16 denormals q 2^-24 (one byte permute per entry), 8-bit formats as
+  // fp16(q) from the table; each chain's sums per sub-block are scaled by dA s_j (2^24 s_j) when the sub-block ends
+  constexpr float WSCALE = SYMB == 4 ? 16777216.f : 1.f;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   typedef __attribute__((address_space(4))) const char KChar;
   typedef __attribute__((address_space(4))) const FlatEntry KEntry;
@@ -2667,25 +2672,20 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       uint64_t q2;
       side_packed<KQ>(sw[sb], scq[sb], q2, dA[sb], dB[sb]);
     }
-    f4v acc[NSB][NQ];
+    f4v acc[NC][NQ];  // per chain: its current sub-block's sums, 4 tokens per register quad
+    float fa[NQ][4];  // scaled sums of the finished sub-blocks
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb)
+    for (int q = 0; q < NQ; ++q) {
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) acc[sb][q] = f4v{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 4; ++i) fa[q][i] = 0.f;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
+    }
     uint32_t wprev[NC];
 #pragma unroll
     for (int j = 0; j < NC; ++j) wprev[j] = 0;
     static_for<NG>([&](auto gic) {
       constexpr int gi = decltype(gic)::value;
-      // the scale of each chain's current sub-block as an fp16 pair (and -64 sc for the 4-bit form)
-      h2v scv[NC], nsc[NC];
-#pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const int js = SYMB == 4 ? NG * j + gi : (NG * j + gi) / 2;  // sub-block within the tile row
-        const _Float16 v = (_Float16)(float)(uint32_t)((scq[js / 8] >> (8 * (js % 8))) & 255u);
-        scv[j] = h2v{v, v};
-        nsc[j] = scv[j] * h2v{(_Float16)-64.f, (_Float16)-64.f};
-      }
       static_for<8>([&](auto pc) {
         constexpr int p = decltype(pc)::value;
         uint32_t w1[NC], e1[NC], e2[NC];
@@ -2710,36 +2710,47 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         }
         static_for<NC>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
-          if constexpr (SYMB == 4) {  // 4 codes: sc q / 16 each, in weight order
-            const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, e1[j], 0x04030402u));
-            const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x54545454u, e2[j], 0x04030402u));
-            const uint2 wv = make_uint2(__builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(a, scv[j], nsc[j])),
-                                        __builtin_bit_cast(uint32_t, (h2v)__builtin_elementwise_fma(b, scv[j], nsc[j])));
+          if constexpr (SYMB == 4) {  // 4 codes as fp16 denormals q 2^-24, in weight order
+            const uint2 wv = make_uint2(__builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u),
+                                        __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u));
             constexpr int g = NG * j + gi;           // 16-symbol group within the tile row
             constexpr int pb = 8 * g + p;            // position block of the 4 weights within the tile row
 #pragma unroll
             for (int q = 0; q < NQ; ++q)
-              acc[g / 8][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[g / 8][q]);
+              acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[j][q]);
           } else {  // 2 codes per pair (fp16(q) in the entries' upper halves), 4 per product
-            const uint32_t v = __builtin_bit_cast(uint32_t, (h2v)(__builtin_bit_cast(h2v, __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u)) * scv[j]));
+            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
             if constexpr (p & 1) {
               constexpr int pb = 4 * (NG * j + gi) + p / 2;
 #pragma unroll
               for (int q = 0; q < NQ; ++q)
-                acc[0][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[0][q]);
+                acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[j][q]);
             } else {
               wprev[j] = v;
             }
           }
         });
       });
+      // sub-blocks ending with this group: y += dA s_j acc (2^24 s_j for the denormal form), then acc = 0
+      if constexpr ((gi + 1) % GPSUB == 0) {
+        static_for<NC>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          constexpr int js = (NG * j + gi) / GPSUB;  // sub-block within the tile row
+          const float sa = dA[js / 8] * WSCALE * (float)(uint32_t)((scq[js / 8] >> (8 * (js % 8))) & 255u);
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[q][i] = fmaf(acc[j][q][i], sa, fa[q][i]);
+            acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
+          }
+        });
+      }
     });
     // the products are formed here, not sunk past the claim and the copy below
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) {
+    for (int q = 0; q < NQ; ++q)
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(acc[sb][q]));
-    }
+      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[q][i]));
     if (xs_late) {  // this tile's sums, now that every share is stored
       while (__hip_atomic_load(xs_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)xnw)
         __builtin_amdgcn_s_sleep(2);
@@ -2793,9 +2804,9 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float tot = 0.f;
+        float tot = fa[q][i];
 #pragma unroll
-        for (int sb = 0; sb < NSB; ++sb) tot = fmaf(dA[sb] * DSCALE, acc[sb][q][i], fmaf(-dB[sb], mac[sb][q][i], tot));
+        for (int sb = 0; sb < NSB; ++sb) tot = fmaf(-dB[sb], mac[sb][q][i], tot);
         if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
@@ -2843,11 +2854,8 @@ static hipError_t tiles_mma_launch(const FlatPlan& p, int per, int buf_rows, hip
 // the sub-block ends: y_t += dA s_j d_x(t, block) acc; the Q4_K / Q5_K offset term dB sum_j m_j SX(t, j) runs on
 // v_mfma_f32_4x4x4f16 with SX split into fp16 hi and lo, as the fp16 kernel's mins term. Each token's values agree
 // with its own m = 1 int8 launch to fp32 rounding (another order of the same exact sub-block sums).
-// at most 16 waves per block; 12 (3 per SIMD) for 8 tokens of the 4-bit formats, whose 8 tokens' x, 4 chains'
-// integer accumulators per token quad and the chains take more than 128 VGPRs
-constexpr int tiles_mma8_waves(int kqt, int mt) { return mt == 8 && kq_symbits(kqt) == 4 ? 12 : TILES_MMA_WAVES; }
 template <int KQ, int NTAB, int MT>
-__global__ void __launch_bounds__(64 * tiles_mma8_waves(KQ, MT), 1)
+__global__ void __launch_bounds__(64 * tiles_mma_waves(KQ, MT), 1)
 k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
   static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
   constexpr int SYMB = kq_symbits(KQ);
@@ -3300,11 +3308,11 @@ size_t tiles_mma_xs_bytes(const FlatPlan& p, int per) {
   return (size_t)std::max(per, 0) * std::max(p.mt, 0) * (kq_symbits(p.e[0].M.kqt) == 4 ? 2 * TK : TK) / 32 * 4;
 }
 
-int tiles_mma8_max_waves(int kqt, int mt) { return tiles_mma8_waves(kqt, mt <= 4 ? 4 : 8); }
+int tiles_mma_max_waves(int kqt, int mt) { return tiles_mma_waves(kqt, mt <= 4 ? 4 : 8); }
 
 hipError_t launch_fused_tiles_mma8(const FlatPlan& p, int per, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || per < p.W || p.ntiles < 1 || p.mt < 1 || p.mt > 8 || !p.i8 ||
-      p.W > tiles_mma8_max_waves(p.e[0].M.kqt, p.mt))
+      p.W > tiles_mma_max_waves(p.e[0].M.kqt, p.mt))
     return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
   for (int i = 0; i < p.n; ++i) {
@@ -3328,8 +3336,8 @@ hipError_t launch_fused_tiles_mma8(const FlatPlan& p, int per, hipStream_t s) {
 }
 
 hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > TILES_MMA_WAVES || per < p.W || p.ntiles < 1 || p.mt < 1 ||
-      p.mt > 8 || p.i8)
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || per < p.W || p.ntiles < 1 || p.mt < 1 || p.mt > 8 || p.i8 ||
+      p.W > tiles_mma_max_waves(p.e[0].M.kqt, p.mt))
     return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
   if (kqt != KQ_Q4_K && kqt != KQ_Q5_K) return hipErrorInvalidValue;

@@ -626,7 +626,7 @@ int tiles_mma_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   per = (fp.ntiles + cus - 1) / cus;
   if (fp.n > 1) per = std::min(per, mintiles);
   const long room = 160L * 1024 - tables - 16 - (long)lw::tiles_mma_xs_bytes(fp, per);
-  const int wmax = (int)std::min<long>(16, room / (rows * 128L));
+  const int wmax = (int)std::min<long>(lw::tiles_mma_max_waves(fp.e[0].M.kqt, fp.mt), room / (rows * 128L));
   if (wmax < 1) return 0;
   return std::min(wmax, per);
 }
@@ -847,7 +847,6 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     }
     int tpb = 0;
     fp.W = tiles_mma_width(fp, mintiles, tpb);  // (plan.i8: no x sums in LDS)
-    fp.W = std::min(fp.W, lw::tiles_mma8_max_waves(fp.e[0].M.kqt, mt));
     if (fp.W < 1) continue;
     for (int j : sel) done[j] = reduced[j] = exc_in[j] = whole[j] = 1;
     HIPCHECK(lw::launch_fused_tiles_mma8(fp, tpb, s));
