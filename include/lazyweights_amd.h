@@ -102,9 +102,9 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * per wave copied to LDS, 8 chains per lane, every tile including exception tiles), or the half-tile kernel (two
  * buffered half-tile units per wave, the next one's copy in flight while one decodes) where the whole-tile kernel's
  * blocks would have fewer than 10 waves (few tiles per CU); m = 1 with int8 activations, the whole-tile kernel;
- * 2 <= m <= 8 with fp16 activations and Q4_K / Q5_K, the whole-tile kernel with its products on the matrix cores;
- * otherwise the ring-staged kernels wherever a matrix has a ring schedule (the flat kernel for int8 activations, the
- * block-per-column kernel otherwise). 1 = the whole-tile fallback kernel everywhere; 2 = the block-per-column ring
+ * 2 <= m <= 8 with fp16 activations and Q4_K / Q5_K, or with int8 activations and every format, the whole-tile
+ * kernel with its products on the matrix cores; otherwise the ring-staged kernels wherever a matrix has a ring
+ * schedule (the block-per-column kernel). 1 = the whole-tile fallback kernel everywhere; 2 = the block-per-column ring
  * kernel for every m; 7 = the ring-staged kernels for every m (for m = 1 the flat, load-balanced ring kernel);
  * 3 = as 7, but exception tiles are never decoded inside the flat launch (always by the separate exception pass);
  * 4 = as 7, with the low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 7, never the low-latency
@@ -127,9 +127,10 @@ int lw_set_prefill_gemm(int which);
  * and lw_group_matmul_dev quantize x per block of 32 (d = max|x| / 127, q = x / d rounded to nearest even, plus
  * d sum q) and the fused kernels take integer dot products per sub-block, y += s d acc - o d sum q. Replaces the
  * reference's act8 switch (kernels/llmrt.cu:2221, LLMRT_FP_ACT; kernels k_quant_x8 / k_gemvm_kq8 at
- * kernels/llmrt.cu:1035-1169), which is on by default there. m > 1 runs one pass over the weights for all tokens
- * (the same bits per token as an m = 1 call); with kernel mode 6 or a packed matrix, one m = 1 pass per token. Needs
- * kernel mode 0, 3, 4, 5 or 6 (the flat kernels). Returns 0 or -1. */
+ * kernels/llmrt.cu:1035-1169), which is on by default there. m > 1 runs one pass over the weights for all tokens:
+ * with kernel mode 0 on the matrix cores (each token within fp32 rounding of its m = 1 result), with modes 3, 4, 5
+ * and 7 by the ring kernels (the same bits per token as an m = 1 call); with kernel mode 6 or a packed matrix, one
+ * m = 1 pass per token. Needs kernel mode 0, 3, 4, 5, 6 or 7. Returns 0 or -1. */
 int lw_set_act8(int on);
 
 /* The int8 quantization of lw_set_act8 on host buffers (test entry, runs the device kernel): X [m, K] fp32 or fp16
