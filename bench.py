@@ -225,6 +225,8 @@ def main():
     ap.add_argument("--only-configs", action="store_true",
                     help="time configs 1, 3 and 4 (Q5_K) only (for a kernel trace of their kernels)")
     ap.add_argument("--kernel-mode", type=int, default=0, help="lw_set_kernel_mode for the whole run (0 = auto)")
+    ap.add_argument("--act8", action="store_true",
+                    help="with --profile: int8 activations (lw_set_act8) for the passes, e.g. with --m 5")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
@@ -302,8 +304,11 @@ def main():
                     raise RuntimeError(lib.lw_last_error().decode())
 
         if a.profile:
+            if a.act8 and lib.lw_set_act8(1) != 0:
+                raise SystemExit("bench.py: int8 activations refused: " + lib.lw_last_error().decode())
             for _ in range(max(1, a.steps)):
                 step()
+            lib.lw_set_act8(0)
             src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
             dst = torch.empty_like(src)
             dst.copy_(src)  # calibration: 256 MiB read + 256 MiB written
