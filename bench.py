@@ -557,8 +557,10 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": traffic["bytes_per_layer_launch"] if traffic else None,
-                         "traffic_detail": traffic, "kernel": "k_fused_tiles" if a.kernel_mode in (0, 6) else
-                         "k_fused_flat", "launch": "one grouped launch per layer",
+                         "traffic_detail": traffic,
+                         "kernel": {0: "k_fused_tiles", 6: "k_fused_tiles", 8: "k_fused_halves",
+                                    9: "k_fused_tiles (comparator lookup)"}.get(a.kernel_mode, "k_fused_flat"),
+                         "launch": "one grouped launch per layer",
                          "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
             "serial_per_matrix": {"ms_per_step": round(serial_ms, 4),
                                   "GBps": round(bytes_per_step / (serial_ms * 1e-3) / 1e9, 1)},

@@ -109,7 +109,11 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * 3 = as 7, but exception tiles are never decoded inside the flat launch (always by the separate exception pass);
  * 4 = as 7, with the low-latency kernel (8 chains per lane) for every m = 1 launch; 5 = as 7, never the low-latency
  * kernel; 6 = as 0, but m = 1 always through the whole-tile kernel and int8 activations one m = 1 pass per token;
- * 8 = as 0, but m = 1 with fp16 activations always through the half-tile kernel. Returns 0 or -1. */
+ * 8 = as 0, but m = 1 with fp16 activations always through the half-tile kernel; 9 = as 6, with the whole-tile
+ * kernel (m = 1, fp16 activations) looking each code up by the comparator over the canonical code's per-length
+ * limits (the reference's hw/huff/huff_engine.h:54-77 lookup) and a 256-entry table in canonical order instead of
+ * the 2048-entry table: the same bits, about 3x slower (returns -1 for a matrix whose codes are not the canonical
+ * code of their lengths). Returns 0 or -1. */
 int lw_set_kernel_mode(int mode);
 
 /* Prefill GEMM (path 2, and fp32 X with m > 8) for every handle. The reference dequantizes to fp32 and runs its own
@@ -130,7 +134,7 @@ int lw_set_prefill_gemm(int which);
  * kernels/llmrt.cu:1035-1169), which is on by default there. m > 1 runs one pass over the weights for all tokens:
  * with kernel mode 0 on the matrix cores (each token within fp32 rounding of its m = 1 result), with modes 3, 4, 5
  * and 7 by the ring kernels (the same bits per token as an m = 1 call); with kernel mode 6 or a packed matrix, one
- * m = 1 pass per token. Needs kernel mode 0, 3, 4, 5, 6 or 7. Returns 0 or -1. */
+ * m = 1 pass per token. Needs kernel mode 0, 3, 4, 5, 6, 7 or 9 (as 6). Returns 0 or -1. */
 int lw_set_act8(int on);
 
 /* The int8 quantization of lw_set_act8 on host buffers (test entry, runs the device kernel): X [m, K] fp32 or fp16
@@ -174,6 +178,15 @@ int lw_write_bundle(const char* dir, int count, const char* const* names, const 
 /* Huffman code lengths of a histogram (n <= 256 symbols): lmax > 0 gives the length-limited lengths of
  * lazyweights/lanecodecs.py:28-38, lmax <= 0 the plain heap lengths of lazyweights/huffman.py:8-26. */
 int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L);
+
+/* The comparator table kernel mode 9 looks codes up in (built at load time for every K-quant matrix; host-side, for
+ * tests): from a bundle decode table lut [2048] (sym | len << 8) and K-quant type kqt (1..4), out [288] = the limits
+ * of code lengths 1..10 (a window value v of 11 bits, first code bit most significant, holds a code longer than k
+ * when v >= out[k - 1]), for l = 1..11 out[9 + l] = (4 (base_l - first_l)) << 16 | (11 - l), and out[32 ..] the
+ * kernels' table entries of the symbols in canonical order; the reference builds the same limits / first / base in
+ * hw/huff/huff_engine.h:39-52 (build_canon). Returns 0, or -1 when the table's codes are not the canonical code of
+ * their lengths (or bad arguments). */
+int lw_canon_table(int kqt, const uint16_t* lut, uint32_t* out);
 
 /* The device layout this library builds from a blob at load time (host-side, for inspection and tests): fills tbase
  * [T], mid [T * 32], split [T * 16 * 32] (bit offsets of symbols 32 k per lane: the chain starts of the

@@ -46,6 +46,7 @@ SIGNATURES = {
     "lw_bundle_finish": (_i, [_vp]),
     "lw_huffman_lengths": (_i, [_vp, _i, _i, _vp]),
     "lw_build_layout": (_ll, [_vp, _ll, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _ll]),
+    "lw_canon_table": (_i, [_i, _vp, _vp]),
     "lw_set_kernel_mode": (_i, [_i]),
     "lw_set_prefill_gemm": (_i, [_i]),
     "lw_set_act8": (_i, [_i]),

@@ -179,6 +179,13 @@ int lw_huffman_lengths(const int64_t* hist, int n, int lmax, uint8_t* L) {
   return 0;
 }
 
+int lw_canon_table(int kqt, const uint16_t* lut, uint32_t* out) {
+  if (!lut || !out || kqt < 1 || kqt > 4) return -1;
+  std::vector<uint32_t> entries(lw::LUTN);
+  lw::decode_table4(kqt, lut, entries.data());
+  return lw::canon_table(lut, entries.data(), out) ? 0 : -1;
+}
+
 long long lw_build_layout(const uint8_t* blob, long long len, int N, int KS, int pre_il, int compact, uint32_t* tbase,
                           uint16_t* mid, uint16_t* split, uint16_t* rows, uint64_t* sched, int* ring_rows,
                           uint32_t* words, long long words_cap) {

@@ -19,6 +19,7 @@ struct DevMat {
   const uint16_t* lut;
   const uint32_t* lut4;  // the ring kernels' 4-byte table entries (decode_table4 in lw_layout.h); null if kqt == 0
   const uint32_t* luti8; // the same with int8 grid values (decode_table_i8), for int8 activations
+  const uint32_t* canon; // the comparator form of lut4 (canon_table in lw_layout.h); null if the codes are not canonical
   const uint32_t* tbase;
   const uint16_t* mid;
   const uint16_t* split;  // [T][SPLITS][32] chain starts of the low-latency and whole-tile kernels (Layout::split)
@@ -97,6 +98,7 @@ struct FlatPlan {
   int nspare;
   int i8;  // 1: int8 activations (the entries' XQ / DX / SX)
   int mt;  // tokens: 0 or 1, or 2..8 with int8 activations (the flat ring and low-latency kernels, one pass)
+  int canon;  // 1: the whole-tile kernel (fp16 activations) looks codes up by the comparator form (DevMat::canon)
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
 // waves of the flat kernel one CU holds at once (its register use) for int8 activations, mt tokens (1, or 2..8)
@@ -124,6 +126,8 @@ int split_stage_rows(const FlatPlan& plan);
 // wave in LDS at a time (tiles_buf_rows rows), 8 chains per lane; every tile of the entries (exceptions included)
 // and the in-launch reduction for entries with Y
 hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
+// the most waves of a whole-tile block with the comparator lookup (FlatPlan::canon)
+constexpr int TILES_CANON_WAVES = 12;
 // The half-tile kernel (m = 1, fp16 activations, no int8): as launch_fused_tiles, but a wave decodes half-tile units
 // (a tile's rows 32 f .. 32 f + 31) with two LDS buffers, the next unit's copy in flight while one decodes; the
 // in-launch reduction per tile row and half (each entry's cnt holds 2 NT counters). W waves per block, each with two

@@ -385,6 +385,39 @@ __device__ __forceinline__ uint32_t table_addr(uint32_t w, uint32_t base, uint32
   return a;
 }
 
+// LDS address of the entry of the code at window bits 2..12 of w by the comparator lookup (reference
+// hw/huff/huff_engine.h:54-77) over a matrix's comparator table (canon_table): v = the 11 window bits with the
+// code's first bit most significant; its length l is 1 + the number of limits lim[0..9] that v reaches, and
+// pk[l - 1] = (table base + 4 (base_l - first_l)) << 16 | (11 - l) turns v into the entry's address. lim and pk
+// are wave-uniform (SGPRs): 10 subtract / shift / insert steps per code.
+// compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1 (indices that must be constants: MFMA
+// broadcast fields, register-array indices; bodies past the loop unroller's size limit)
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for_from(F& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_from<I + 1, N>(f);
+  }
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_from<0, N>(f);
+}
+
+__device__ __forceinline__ uint32_t canon_addr(uint32_t w, const uint32_t* lim, const uint32_t* pk) {
+  const uint32_t v = __builtin_amdgcn_ubfe(__builtin_bitreverse32(w), 19, 11);
+  uint32_t p = pk[0];
+#pragma unroll
+  for (int k = 0; k < 10; ++k) {  // p = v < lim[k] ? p : pk[k + 1] by the sign of v - lim[k] (11-bit values) and a
+                                   // bitfield insert: no VCC, and no per-lane indexed load of pk
+    uint32_t t;
+    asm("v_subrev_u32 %1, %3, %2\n\tv_ashrrev_i32 %1, 31, %1\n\tv_bfi_b32 %0, %1, %0, %4"
+        : "+v"(p), "=&v"(t)
+        : "v"(v), "s"(lim[k]), "s"(pk[k + 1]));
+  }
+  return ((v >> (p & 31u)) << 2) + (uint32_t)((int)p >> 16);
+}
+
 // x sub-block sums held in LDS per block ([NG][MT], the block-per-column kernel)
 struct XgLds {
   const float* xg;
@@ -1625,8 +1658,11 @@ constexpr int TILES_COPIES = LW_TILES_COPIES;
 // (tile_gemv_i8's for int8 activations), the bits of the other kernels.
 // (at most 16 waves per CU by the LDS of the tile buffers: 4 per SIMD, so the scheduler may spend up to 128 VGPRs on
 // keeping the 8 chains' reads in flight)
-template <int KQ, int NTAB, bool I8>
-__global__ void __launch_bounds__(1024, 1)
+// CANON (kernel mode 9, fp16 activations): codes are looked up by the comparator (canon_addr) in a 256-entry table
+// of entries in canonical order instead of the 2048-entry table; the same entries, so the same bits. Its blocks have
+// at most TILES_CANON_WAVES waves (3 per SIMD): the comparator's registers spill at 4.
+template <int KQ, int NTAB, bool I8, bool CANON = false>
+__global__ void __launch_bounds__(CANON ? 64 * TILES_CANON_WAVES : 1024, 1)
 k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -1661,7 +1697,14 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
-  {  // the tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W
+  if (CANON) {  // the comparator tables' 256 entries: one 1 KB direct-to-LDS load per table, at the tables' places
+    const uint4* ta = reinterpret_cast<const uint4*>(ea->M.canon + 32);
+    const uint4* tb = reinterpret_cast<const uint4*>(eb->M.canon + 32);
+    const int nchunk = (NTAB > 1 && mb != ma) ? 2 : 1;
+    for (int c = wave; c < nchunk; c += W)
+      __builtin_amdgcn_global_load_lds((c ? tb : ta) + lane, (__attribute__((address_space(3))) void*)(lut4 + LUTN * c),
+                                       16, 0, 0);
+  } else {  // the tables: 1 KB direct-to-LDS loads, chunk c (8 per table) by wave c mod W
     const uint4* ta = reinterpret_cast<const uint4*>(I8 ? ea->M.luti8 : ea->M.lut4);
     const uint4* tb = reinterpret_cast<const uint4*>(I8 ? eb->M.luti8 : eb->M.lut4);
     const int nchunk = (NTAB > 1 && mb != ma) ? 16 : 8;
@@ -1767,6 +1810,19 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     uint32_t P[NC];
     tile_chain_starts(M, t, f, s, P);
     const uint32_t tsel = second ? 4u * LUTN : 0u;
+    uint32_t clim[10], cpk[11];  // the comparator's limits and length words (CANON), the table's place added
+    if (CANON) {
+      KU32* cz = (KU32*)M.canon;
+#pragma unroll
+      for (int k = 0; k < 10; ++k) clim[k] = cz[k];
+#pragma unroll
+      for (int k = 0; k < 11; ++k) cpk[k] = cz[10 + k] + (tsel << 16);
+      // values in SGPRs (not a per-lane indexed load of the table words)
+#pragma unroll
+      for (int k = 0; k < 10; ++k) asm volatile("" : "+s"(clim[k]));
+#pragma unroll
+      for (int k = 0; k < 11; ++k) asm volatile("" : "+s"(cpk[k]));
+    }
     // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
     // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
     // used through DPP broadcasts), int8 x as dwords l, l + 64, .. read back with v_readlane
@@ -1806,10 +1862,8 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       iacc[j] = 0;
       wprev[j] = 0;
     }
-#pragma unroll
-    for (int gi = 0; gi < NG; ++gi) {
-#pragma unroll
-      for (int p = 0; p < 8; ++p) {
+    // one pair of symbols of every chain (group gi, pair p), then the end of a 16-symbol group
+    auto pair_step = [&](const int gi, const int p) __attribute__((always_inline)) {
         // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
         // (the reads return in order: a chain waits only for its own)
         // (scheduling barriers keep the stages apart, so every chain's read is issued before the first result is
@@ -1818,11 +1872,14 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
           w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
-          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+          e1[j] = *(LdsU32*)(CANON ? canon_addr(w1[j], clim, cpk) : table_addr(w1[j], tsel, tmask));
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+        for (int j = 0; j < NC; ++j) {
+          const uint32_t w2 = w1[j] >> (e1[j] & 31u);
+          e2[j] = *(LdsU32*)(CANON ? canon_addr(w2, clim, cpk) : table_addr(w2, tsel, tmask));
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -1858,7 +1915,8 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
             dot2_row(acc[j], xr[c >> 4], c & 15, v);
           }
         }
-      }
+    };
+    auto group_end = [&](const int gi) __attribute__((always_inline)) {
       if (GPSUB == 1 || (gi & 1)) {
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
@@ -1866,6 +1924,19 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
           acc[j] = 0.f;
           iacc[j] = 0;
         }
+      }
+    };
+    if constexpr (CANON) {  // (the comparator's steps are past the unroller's size limit)
+      static_for<NG>([&](auto gi) {
+        static_for<8>([&](auto p) { pair_step(gi, p); });
+        group_end(gi);
+      });
+    } else {
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+#pragma unroll
+        for (int p = 0; p < 8; ++p) pair_step(gi, p);
+        group_end(gi);
       }
     }
 
@@ -2412,20 +2483,6 @@ k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
 // 8 tokens' x, the 4 chains' accumulators per token quad and the chains take more than 128 VGPRs
 constexpr int TILES_MMA_WAVES = 16;
 constexpr int tiles_mma_waves(int kqt, int mt) { return mt == 8 && kq_symbits(kqt) == 4 ? 12 : TILES_MMA_WAVES; }
-
-// compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N - 1 (indices that must be constants: MFMA
-// broadcast fields, register-array indices)
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for_from(F& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for_from<I + 1, N>(f);
-  }
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_from<0, N>(f);
-}
 
 // v_mfma_f32_4x4x4f16 over 16 blocks with A broadcast from block ABID
 template <int ABID>
@@ -3204,14 +3261,14 @@ static hipError_t tiles_mma8_launch(const FlatPlan& p, int per, int buf_rows, hi
   return one ? tiles_mma8_launch_t<KQ, 1, 8>(p, per, buf_rows, s) : tiles_mma8_launch_t<KQ, 2, 8>(p, per, buf_rows, s);
 }
 
-template <int KQ, int NTAB, bool I8>
+template <int KQ, int NTAB, bool I8, bool CANON = false>
 static hipError_t tiles_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8, CANON>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + per - 1) / per;
-  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
+  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8, CANON>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
   return hipGetLastError();
 }
 
@@ -3219,6 +3276,8 @@ template <int KQ>
 static hipError_t tiles_launch(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const bool one = p.n == 1;  // one matrix: one table
   if (p.i8) return one ? tiles_launch_t<KQ, 1, true>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, true>(p, per, buf_rows, s);
+  if (p.canon)
+    return one ? tiles_launch_t<KQ, 1, false, true>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, false, true>(p, per, buf_rows, s);
   return one ? tiles_launch_t<KQ, 1, false>(p, per, buf_rows, s) : tiles_launch_t<KQ, 2, false>(p, per, buf_rows, s);
 }
 
@@ -3231,7 +3290,8 @@ int tiles_buf_rows(const FlatPlan& p) {
 }
 
 hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > 16 || per < p.W || p.ntiles < 1 || p.mt > 1)
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > (p.canon ? TILES_CANON_WAVES : 16) || per < p.W ||
+      p.ntiles < 1 || p.mt > 1)
     return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
   for (int i = 0; i < p.n; ++i) {
@@ -3240,7 +3300,8 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
     // a block (`per` consecutive tiles) spans at most two matrices
     if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
-        (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)))
+        (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)) ||
+        (p.canon && (p.i8 || !e.M.canon)))
       return hipErrorInvalidValue;
   }
   const int rows = tiles_buf_rows(p);

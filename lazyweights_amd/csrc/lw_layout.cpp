@@ -510,4 +510,40 @@ void decode_table_i8(int kqt, const uint16_t* lut, uint32_t* out) {
   }
 }
 
+bool canon_table(const uint16_t* lut, const uint32_t* entries, uint32_t* out) {
+  int len[256] = {}, cnt[LMAX + 1] = {};
+  int idx_of[256];  // a window index of each symbol's code (any)
+  for (int i = 0; i < LUTN; ++i) {
+    const int sym = lut[i] & 255, l = lut[i] >> 8;
+    if (l < 1 || l > LMAX) continue;
+    if (len[sym] && len[sym] != l) return false;
+    len[sym] = l;
+    idx_of[sym] = i;
+  }
+  for (int sym = 0; sym < 256; ++sym) cnt[len[sym]] += len[sym] ? 1 : 0;
+  memset(out, 0, CANON_WORDS * 4);
+  int code = 0, b = 0;
+  for (int l = 1; l <= LMAX; ++l) {
+    out[10 + l - 1] = (uint32_t)(4 * (b - code)) << 16 | (uint32_t)(LMAX - l);
+    for (int sym = 0; sym < 256; ++sym)
+      if (len[sym] == l) out[32 + b++] = entries[idx_of[sym]];
+    code += cnt[l];
+    if (code > (1 << l)) return false;  // not a prefix code
+    if (l < LMAX) out[l - 1] = (uint32_t)code << (LMAX - l);
+    code <<= 1;
+  }
+  // every window that the table decodes must give the same entry by comparison
+  for (int i = 0; i < LUTN; ++i) {
+    const int l = lut[i] >> 8;
+    if (l < 1 || l > LMAX) continue;
+    uint32_t v = 0;
+    for (int k = 0; k < LMAX; ++k) v |= ((uint32_t)i >> k & 1u) << (LMAX - 1 - k);
+    uint32_t p = out[10];
+    for (int k = 0; k < LMAX - 1; ++k) p = v >= out[k] ? out[11 + k] : p;
+    const int e = (int)(v >> (p & 31u)) + ((int32_t)p >> 16) / 4;
+    if ((int)(p & 31u) != LMAX - l || e < 0 || e >= b || out[32 + e] != entries[i]) return false;
+  }
+  return true;
+}
+
 }  // namespace lw

@@ -75,5 +75,13 @@ void decode_table4(int kqt, const uint16_t* lut, uint32_t* out);
 // The int8-activation kernels' table: as decode_table4, with the grid values as int8 bytes (4-bit symbols: bytes 2
 // and 3 = f(q) of the low and high code, Q4_K q, IQ4_XS kv[q]; 8-bit symbols: byte 2 = f(q), Q5_K q, Q6_K q - 32).
 void decode_table_i8(int kqt, const uint16_t* lut, uint32_t* out);
+// The comparator form of the table (reference hw/huff/huff_engine.h:39-77, build_canon + lookup): out[0..9] = the
+// limits of code lengths 1..10 (an 11-bit window value v, first code bit most significant, holds a code longer
+// than k when v >= limit k), out[10..20] = for lengths l = 1..11: (4 (base_l - first_l)) << 16 | (11 - l), out[21..31]
+// = 0, out[32..287] = entries[] (decode_table4 entries) of the symbols in canonical order (by length, then
+// symbol), so that entry index base_l + (v >> (11 - l)) - first_l is the code's. False when the table's codes are
+// not the canonical code of their lengths (no window may then be looked up this way).
+constexpr int CANON_WORDS = 288;
+bool canon_table(const uint16_t* lut, const uint32_t* entries, uint32_t* out);
 
 }  // namespace lw

@@ -265,10 +265,11 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   if (!ok) return fail(t.name + ": " + err);
   std::vector<uint8_t>().swap(blob);
   const int T = t.T();
-  // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][tbase 4T][mid 64T][split 1024T][rows 2T]
+  // [lut 4096 B][4-byte table 8192 B][int8 table 8192 B][comparator table 1152 B][tbase 4T][mid 64T][split 1024T][rows 2T]
   // [sched 16T (16-aligned)][hrow 4T][hsplit 1024T][dsplit 512T][exception tiles 4E] padded to 256 B, then the words
   const size_t nexc = L.exc.size();
-  const size_t o_lut4 = 2 * lw::LUTN, o_luti8 = o_lut4 + 4 * lw::LUTN, o_tb = o_luti8 + 4 * lw::LUTN;
+  const size_t o_lut4 = 2 * lw::LUTN, o_luti8 = o_lut4 + 4 * lw::LUTN, o_canon = o_luti8 + 4 * lw::LUTN;
+  const size_t o_tb = o_canon + 4 * lw::CANON_WORDS;
   const size_t o_mid = o_tb + 4ull * T;
   const size_t o_split = o_mid + 64ull * T, o_rows = o_split + 64ull * lw::SPLITS * T;
   const size_t o_sched = (o_rows + 2ull * T + 15) & ~(size_t)15, o_hrow = o_sched + 16ull * T;
@@ -278,9 +279,12 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   const size_t bytes = o_words + 4 * L.words.size();
   std::vector<uint8_t> host(o_words, 0);
   memcpy(host.data(), L.lut, 2 * lw::LUTN);
+  bool canon = false;
   if (t.kqt) {
     lw::decode_table4(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_lut4));
     lw::decode_table_i8(t.kqt, L.lut, reinterpret_cast<uint32_t*>(host.data() + o_luti8));
+    canon = lw::canon_table(L.lut, reinterpret_cast<const uint32_t*>(host.data() + o_lut4),
+                            reinterpret_cast<uint32_t*>(host.data() + o_canon));
   }
   memcpy(host.data() + o_tb, L.tbase.data(), 4ull * T);
   memcpy(host.data() + o_mid, L.mid.data(), 64ull * T);
@@ -333,6 +337,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.lut = reinterpret_cast<const uint16_t*>(b);
   dm.lut4 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_lut4) : nullptr;
   dm.luti8 = t.kqt ? reinterpret_cast<const uint32_t*>(b + o_luti8) : nullptr;
+  dm.canon = canon ? reinterpret_cast<const uint32_t*>(b + o_canon) : nullptr;
   dm.tbase = reinterpret_cast<const uint32_t*>(b + o_tb);
   dm.mid = reinterpret_cast<const uint16_t*>(b + o_mid);
   dm.split = reinterpret_cast<const uint16_t*>(b + o_split);
@@ -604,7 +609,7 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   const int cus = cu_count();
   const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
   if (rows > 256) return 0;
-  const int wmax = std::min(16, (160 * 1024 - tables) / (rows * 128));
+  const int wmax = std::min(fp.canon ? lw::TILES_CANON_WAVES : 16, (160 * 1024 - tables) / (rows * 128));
   if (wmax < 1) return 0;
   per = (fp.ntiles + cus - 1) / cus;
   if (fp.n > 1) per = std::min(per, mintiles);
@@ -733,9 +738,10 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     return 0;
   };
   const bool ring_ok = g_kernel_mode != 1;
-  const bool flat = ring_ok && g_kernel_mode != 2 && (mt == 1 || (x8 && mt <= 8 && g_kernel_mode != 6));
+  const bool one_pass = g_kernel_mode == 6 || g_kernel_mode == 9;  // modes taking int8 tokens one pass each
+  const bool flat = ring_ok && g_kernel_mode != 2 && (mt == 1 || (x8 && mt <= 8 && !one_pass));
   if (x8 && !flat) {
-    g_err = "int8 activations: a flat kernel mode (0, 3, 4, 5, 7, or 6 for m = 1) and at most 8 tokens only";
+    g_err = "int8 activations: a flat kernel mode (0, 3, 4, 5, 7, or 6 and 9 for m = 1) and at most 8 tokens only";
     return -1;
   }
   for (int i = 0; x8 && mt > 1 && i < count; ++i)
@@ -900,11 +906,18 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
         continue;
       }
     }
-    if (mt == 1 && (g_kernel_mode == 0 || g_kernel_mode == 6)) {
+    if (mt == 1 && (g_kernel_mode == 0 || one_pass)) {
       // the whole-tile kernel (the m = 1 default: faster than the ring kernel on every configuration measured):
       // every tile, the reduction in the launch; the ring kernel where the tiles do not fit its LDS
+      // kernel mode 9: codes looked up by the comparator form instead of the 2048-entry table (fp16 activations)
+      fp.canon = g_kernel_mode == 9 && !x8;
       int rounds = 0;  // tiles per block
       fp.W = tiles_width(fp, mintiles, rounds);
+      for (int k = 0; fp.W > 0 && fp.canon && k < fp.n; ++k)
+        if (!fp.e[k].M.canon) {
+          g_err = "kernel mode 9: a matrix's codes are not the canonical code of their lengths";
+          return -1;
+        }
       if (fp.W > 0) {
         for (int k = 0; k < fp.n; ++k) {
           fp.e[k].Y = Y[sel[k]];
@@ -1088,11 +1101,11 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
 // Int8-activation matmuls of `count` matrices for m <= 8 tokens (x [m][K_i], fp16 or fp32, rows K_i apart; y rows
 // ldy apart): one quantization launch, then one fused pass over the weights for all tokens (the reference's MT-token
 // int8 kernel, kernels/llmrt.cu:1057-1169), which gives every token the bits of an m = 1 call. Packed matrices and
-// kernel mode 6 take one m = 1 pass per token.
+// kernel modes 6 and 9 take one m = 1 pass per token.
 int act8_tokens(Model& M, Tensor* const* ts, const void* const* X, int x_f16, int count, int m, float* const* Y,
                 const int* ldy, hipStream_t s, int* launches) {
   std::vector<X8> x8;
-  bool one = m > 1 && g_kernel_mode != 6;
+  bool one = m > 1 && g_kernel_mode != 6 && g_kernel_mode != 9;
   for (int i = 0; i < count; ++i) one = one && !ts[i]->dm.packed;
   if (one || m == 1) {
     if (quant_x8_dev(M, ts, X, x_f16, count, x8, s, m)) return -1;
@@ -1721,7 +1734,7 @@ int lw_set_act8(int on) {
 }
 
 int lw_set_kernel_mode(int mode) {
-  if (mode < 0 || mode > 8) return -1;
+  if (mode < 0 || mode > 9) return -1;
   g_kernel_mode = mode;
   return 0;
 }

@@ -566,6 +566,57 @@ def test_gpu_tiles_kernel_same_bits(fmt_rt, orc, tmp_path):
             check_err(a[0].numpy(), orc.gemv_f64(orc.dequant(2, codes, side), x.double().numpy()), nm)
 
 
+def test_gpu_comparator_lookup_same_bits(fmt_rt, orc, tmp_path):
+    """Kernel mode 9: the whole-tile kernel looking each code up by the comparator (the canonical code's per-length
+    limits, reference hw/huff/huff_engine.h:54-77, in a 256-entry table of entries in canonical order) instead of
+    the 2048-entry table gives the table's bits (mode 6, the same kernel with the table) for every format, for single
+    matrices and groups whose blocks span two tables, and for matrices with exception tiles."""
+    import ctypes
+
+    import torch
+    from lazyweights_amd import Runtime
+    from lazyweights_amd.bundle import Writer
+    from test_layout import mild_skew_codes, skewed_tile_codes
+
+    def run(rt, names, xs, mode):
+        assert rt.lib.lw_set_kernel_mode(mode) == 0
+        try:
+            ys = [torch.zeros(1, rt.info(nm)["N"], device="cuda") for nm in names]
+            n = len(names)
+            rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
+                                            (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs]), 1,
+                                            (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys]), None)
+            assert rc == 0, rt.lib.lw_last_error()
+            torch.cuda.synchronize()
+            return [y.cpu() for y in ys]
+        finally:
+            rt.lib.lw_set_kernel_mode(0)
+
+    rt, mats = fmt_rt
+    for kqt, fmt, H in FORMATS:
+        for names in ([fmt], [fmt + "_small"], [fmt + "_small", fmt, fmt + "_small"]):
+            X = [torch.randn(1, mats[nm][3]).half() for nm in names]
+            xs = [x.cuda() for x in X]
+            say("comparator lookup", fmt, len(names))
+            a, b = run(rt, names, xs, 9), run(rt, names, xs, 6)
+            for nm, x, ya, yb in zip(names, X, a, b):
+                assert torch.equal(ya, yb), nm
+                _, y64 = reference_y(orc, mats[nm], x.double().numpy())
+                check_err(ya.numpy(), y64, "%s comparator lookup" % nm)
+    w = Writer(str(tmp_path))
+    cases = {"mskew": mild_skew_codes(), "skew": skewed_tile_codes()}
+    for nm, (codes, side) in cases.items():
+        w.add_kquant(nm, 2, codes, side)
+    w.close()
+    with Runtime(tmp_path) as rt2:
+        x = torch.randn(1, 8192).half()
+        for nm, (codes, side) in cases.items():
+            say("comparator lookup, exception tiles", nm)
+            a, b = run(rt2, [nm], [x.cuda()], 9), run(rt2, [nm], [x.cuda()], 6)
+            assert torch.equal(a[0], b[0]), nm
+            check_err(a[0].numpy(), orc.gemv_f64(orc.dequant(2, codes, side), x.double().numpy()), nm)
+
+
 def test_gpu_half_tile_kernel_same_bits(gpu, tmp_path, orc):
     """The half-tile kernel (kernel mode 8; the m = 1 default where whole tiles would give a block's waves fewer than
     two each) gives the whole-tile (mode 6) and ring (mode 7) kernels' bits for every format, on matrices with 7 tiles

@@ -406,3 +406,61 @@ def test_ring_exception_tiles(lib):
     assert (int(sched[2 * 5 + 1]) >> 33) & 1 == 0  # no 32-row schedule either
     lut = np.frombuffer(blob, np.uint16, 2048, 0)
     assert np.array_equal(emulate_ring(lut, tbase, mid, words, sched, RS, 128, 8192, sym), sym)
+
+
+def _bitrev11(w):
+    return int("{:011b}".format(w)[::-1], 2)
+
+
+@pytest.mark.parametrize("case", golden_cases())
+def test_canon_table_matches_oracle(lib, orc, case):
+    """The comparator table of kernel mode 9 (lw_canon_table, built for every K-quant matrix at load time) on the
+    reference encoder's decode tables: the oracle's limits, first / base per length and symbol order
+    (orc_canon_build, itself pinned to the table over every window), and its own lookup of every window a code
+    reaches gives the table's symbol and length."""
+    lut = np.ascontiguousarray(load_golden(case)["lut"], np.uint16)
+    out = np.zeros(288, np.uint32)
+    assert lib.lw_canon_table(1, lut.ctypes.data, out.ctypes.data) == 0
+    limit, first, base, srt = orc.canon_tables(lut)
+    assert np.array_equal(out[:10], limit[1:11].astype(np.uint32))
+    for l in range(1, 12):
+        w = int(out[9 + l])
+        assert w & 31 == 11 - l
+        assert (w >> 16) - (1 << 16 if w >> 31 else 0) == 4 * (int(base[l]) - int(first[l])), l
+    nsym = len({int(e) & 255 for e in lut if e >> 8})
+    ent = out[32:32 + nsym]
+    assert np.array_equal((ent >> 16 & 15) | (ent >> 24 & 15) << 4, srt[:nsym].astype(np.uint32))
+    for win in range(2048):
+        if not lut[win] >> 8:
+            continue
+        v = _bitrev11(win)
+        p = int(out[10])
+        for k in range(10):
+            if v >= out[k]:
+                p = int(out[11 + k])
+        idx = (v >> (p & 31)) + ((p >> 16) - (1 << 16 if p >> 31 else 0)) // 4
+        e = int(out[32 + idx])
+        assert (e & 255, (e >> 16 & 15) | (e >> 24 & 15) << 4) == (int(lut[win]) >> 8, int(lut[win]) & 255), win
+
+
+def test_canon_table_rejects_non_canonical(lib):
+    """A prefix code whose codes of one length are not in symbol order is not the canonical code: lw_canon_table
+    refuses it (kernel mode 9 then refuses the matrix instead of decoding wrong symbols)."""
+    def two_of_one_length(lut):
+        lens = {}
+        for e in lut:
+            if e >> 8:
+                lens.setdefault(int(e) >> 8, set()).add(int(e) & 255)
+        return next((sorted(s)[:2] for l, s in sorted(lens.items()) if len(s) >= 2), None)
+
+    luts = [np.ascontiguousarray(load_golden(c)["lut"], np.uint16) for c in golden_cases()]
+    lut = next(t for t in luts if two_of_one_length(t))
+    out = np.zeros(288, np.uint32)
+    assert lib.lw_canon_table(1, lut.ctypes.data, out.ctypes.data) == 0
+    a, b = two_of_one_length(lut)
+    bad = lut.copy()
+    for i, e in enumerate(lut):
+        if e >> 8 and int(e) & 255 in (a, b):
+            bad[i] = (int(e) & 0xFF00) | (b if int(e) & 255 == a else a)
+    assert lib.lw_canon_table(1, bad.ctypes.data, out.ctypes.data) == -1
+    assert lib.lw_canon_table(0, lut.ctypes.data, out.ctypes.data) == -1
