@@ -174,25 +174,25 @@ def test_gpu_act8_kernels_same_bits(a8_rt, orc, lib, act8):
         shared = torch.randn(1, mats[fmt][3]).half().cuda()
         xs = [shared, torch.randn(1, 512).half().cuda(), shared, torch.randn(1, 512).half().cuda()]
         runs = {}
-        for mode in (0, 4, 5, 6, 7):
+        for mode in (0, 4, 5, 6, 7, 9):
             assert lib.lw_set_kernel_mode(mode) == 0
             runs[mode] = group(rc, names, xs)
         lib.lw_set_kernel_mode(0)
         runs["packed"] = group(rp, names, xs)
         say("act8 kernels same bits", fmt)
-        for k in (0, 4, 5, 6, 7, "packed"):
+        for k in (0, 4, 5, 6, 7, 9, "packed"):
             for nm, x, y in zip(names, xs, runs[k]):
                 y8, _ = y_act8(orc, mats[nm], x.float().cpu().numpy())
                 check(y, y8, TOL_ACT8, "%s act8 grouped (%s)" % (nm, k))
-        for k in (4, 5, 6, 7, "packed"):
+        for k in (4, 5, 6, 7, 9, "packed"):
             for a, b in zip(runs[0], runs[k]):
                 assert np.array_equal(a, b), (fmt, k)
-        # m = 5 in one pass (modes 0, 4, 5, 7) or one pass per token (mode 6, packed): every token the bits of its own
-        # m = 1 call (mode 0, the matrix-core kernel: within 5e-6 of max |y|), and within tolerance of the oracle
+        # m = 5 in one pass (modes 0, 4, 5, 7) or one pass per token (modes 6 and 9, packed): every token the bits of
+        # its own m = 1 call (mode 0, the matrix-core kernel: within 5e-6 of max |y|), and within tolerance of the oracle
         x5 = [torch.randn(5, mats[nm][3]).half().cuda() for nm in names]
         ones = [group(rc, names, [x[j:j + 1].contiguous() for x in x5]) for j in range(5)]
         say("act8 m=5 grouped", fmt)
-        for mode in (0, 4, 5, 6, 7):
+        for mode in (0, 4, 5, 6, 7, 9):
             assert lib.lw_set_kernel_mode(mode) == 0
             y5 = group(rc, names, x5, 5)
             for i in range(len(names)):
