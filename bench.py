@@ -12,8 +12,8 @@ accounting; device-layout padding is not credited).
 
 roofline: the dominant kernel (k_fused_tiles: a tile per wave copied to LDS, 8 chains per lane; one grouped launch
 per layer that also sums the tile-column partials)
-timed with HIP events around each layer's launches on their stream; achieved = the layer's algorithmic bytes / mean
-duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view). traffic = HBM
+timed with HIP events around each pass of the layers' launches on their stream (the launches run back to back),
+divided by the launches per pass; achieved = the layer's algorithmic bytes / that mean duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view). traffic = HBM
 bytes per layer launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --profile`,
 each scaled by what the counter reads for the 256 MiB device copy that --profile also runs (null when rocprofv3 is
 unavailable or a pass fails). cpu_baseline: the oracle's restatement of the reference CPU path (cpu_decode,
@@ -126,8 +126,12 @@ def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps):
                   (ctypes.c_void_p * per)(*yp[sl])) for sl in groups]
 
         def timed(fn):
-            fn()
-            torch.cuda.synchronize()
+            # untimed runs for about 20 ms first: the clocks settle again after a change of workload
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 0.02:
+                for _ in range(10):
+                    fn()
+                torch.cuda.synchronize()
             t0 = time.perf_counter()
             for _ in range(steps):
                 fn()
@@ -148,7 +152,7 @@ def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps):
             kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
             sizes = (ctypes.c_int * layers)(*([per] * layers))
             out = (ctypes.c_double * 3)()
-            if lib.lw_bench_groups(rt.h, layers, sizes, names, xp, m, yp, 1, max(3, steps // 2), out) != 0:
+            if lib.lw_bench_groups(rt.h, layers, sizes, names, xp, m, yp, 10, max(3, steps // 2), out) != 0:
                 raise RuntimeError(lib.lw_last_error().decode())
             rec = {"ms_per_step": round(sms, 4), "GBps_coded": round(sbytes / (sms * 1e-3) / 1e9, 1),
                    "kernel_ms_per_pass": round(out[1], 4), "launches_per_pass": int(out[2]),
@@ -317,6 +321,23 @@ def main():
             log("bench --profile: %d passes over %d layers + 256 MiB copy done" % (max(1, a.steps), a.layers))
             rt.close()
             return
+        # dominant kernel: HIP events around each pass of the fused launches, on the library's stream (an event
+        # between two launches costs the stream about 2 us). It runs first, after 60
+        # untimed passes (about 20 ms): under sustained load the GPU's clocks ramp up over the first 10-15 ms (the
+        # kernel trace shows the layer launch going from 43-44 us to 39.7-40 us over its first ~300 launches), which
+        # would otherwise land in whichever measurement came first; the headline's W warmup and K timed steps follow
+        sizes = (ctypes.c_int * a.layers)(*([7] * a.layers))
+        out = (ctypes.c_double * 3)()
+        rc = lib.lw_bench_groups(rt.h, a.layers, sizes, names, xp, m, yp, 60, max(3, a.steps // 2), out)
+        if rc != 0:
+            raise RuntimeError(lib.lw_last_error().decode())
+        kernel_ms_per_pass = out[1]
+        launches = int(out[2])
+        kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
+        achieved = kbytes / (kernel_ms_per_pass * 1e-3) / 1e9
+        layer_us = kernel_ms_per_pass * 1e3 / a.layers
+        log("bench: fused kernels %.3f ms per pass (%d launches for %d layers, %.1f us per layer), %.1f GB/s"
+            % (kernel_ms_per_pass, launches, a.layers, layer_us, achieved))
         for _ in range(a.warmup):
             step()
         torch.cuda.synchronize()
@@ -327,6 +348,48 @@ def main():
         ms_per_step = (time.perf_counter() - t0) * 1e3 / a.steps
         value = bytes_per_step / (ms_per_step * 1e-3) / 1e9
         log("bench: %.3f ms per step (%d GEMVs), %.1f GB/s coded" % (ms_per_step, n, value))
+        # speculative verify (config 4: m = 5 tokens on the same layers, one grouped call per layer), timed right
+        # after the m = 1 step it is compared with, before the other measurements' allocations: fp16 x and
+        # int8 x (one pass over the weights for all tokens); bytes as m = 1 plus 5x the x and y traffic
+        verify = None
+        if m == 1:
+            vm = 5
+            XV = [torch.randn(vm, inf["K"], generator=g).half().cuda() for inf in infos]
+            YV = [torch.zeros(vm, inf["N"], device="cuda") for inf in infos]
+            vcalls = []
+            for l in range(a.layers):
+                sl = slice(7 * l, 7 * l + 7)
+                vcalls.append(((ctypes.c_char_p * 7)(*names[sl]),
+                               (ctypes.c_void_p * 7)(*[x.data_ptr() for x in XV[sl]]),
+                               (ctypes.c_void_p * 7)(*[y.data_ptr() for y in YV[sl]])))
+            vbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * vm + 4 * vm * inf["N"]
+                               for inf in infos))
+            verify = {"m": vm}
+            for a8, key in ((0, "fp16_x"), (1, "int8_x")):
+                lib.lw_set_act8(a8)
+                try:
+                    def vstep():
+                        for nm, xx, yy in vcalls:
+                            if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, vm, yy, stream) != 0:
+                                raise RuntimeError(lib.lw_last_error().decode())
+                    for _ in range(max(40, a.warmup)):  # about 17 ms: the clocks settle again after the switch
+                        vstep()
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    for _ in range(a.steps):
+                        vstep()
+                    torch.cuda.synchronize()
+                    vms = (time.perf_counter() - t0) * 1e3 / a.steps
+                finally:
+                    lib.lw_set_act8(0)
+                verify[key] = {"ms_per_step": round(vms, 4), "GBps_coded": round(vbytes / (vms * 1e-3) / 1e9, 1),
+                               "over_one_m1_step": round(vms / ms_per_step, 3)}
+                log("bench: verify m=%d (%s): %.3f ms per step, %.1f GB/s coded" % (vm, key, vms, verify[key]["GBps_coded"]))
+            # config 4's comparison: the 5 tokens as 5 m = 1 steps over the same layers (the headline step, timed above)
+            verify["five_m1_steps_ms"] = round(vm * ms_per_step, 4)
+            verify["fp16_x"]["over_five_m1_steps"] = round(verify["fp16_x"]["ms_per_step"] / (vm * ms_per_step), 3)
+            del XV, YV
+
         serial_step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -337,19 +400,6 @@ def main():
         log("bench: serial per-matrix launches %.3f ms per step, %.1f GB/s coded"
             % (serial_ms, bytes_per_step / (serial_ms * 1e-3) / 1e9))
 
-        # dominant kernel: HIP events around each fused launch, on the library's stream
-        sizes = (ctypes.c_int * a.layers)(*([7] * a.layers))
-        out = (ctypes.c_double * 3)()
-        rc = lib.lw_bench_groups(rt.h, a.layers, sizes, names, xp, m, yp, 1, max(3, a.steps // 2), out)
-        if rc != 0:
-            raise RuntimeError(lib.lw_last_error().decode())
-        kernel_ms_per_pass = out[1]
-        launches = int(out[2])
-        kbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * m for inf in infos))
-        achieved = kbytes / (kernel_ms_per_pass * 1e-3) / 1e9
-        layer_us = kernel_ms_per_pass * 1e3 / a.layers
-        log("bench: fused kernels %.3f ms per pass (%d launches for %d layers, %.1f us per layer), %.1f GB/s"
-            % (kernel_ms_per_pass, launches, a.layers, layer_us, achieved))
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
         # decode only (the reference's decode bench, rt_gpu_decode_all): every matrix of the workload to code bytes,
@@ -385,46 +435,6 @@ def main():
                     "speed_vs_fp16_x": round(ms_per_step / ams, 3)}
             log("bench: int8 activations %.3f ms per step (%.1f GB/s coded; kernels %.3f ms per pass, %d launches)"
                 % (ams, act8["GBps_coded"], out8[1], int(out8[2])))
-
-        # speculative verify (config 4: m = 5 tokens on the same layers, one grouped call per layer): fp16 x and
-        # int8 x (one pass over the weights for all tokens); bytes as m = 1 plus 5x the x and y traffic
-        verify = None
-        if m == 1:
-            vm = 5
-            XV = [torch.randn(vm, inf["K"], generator=g).half().cuda() for inf in infos]
-            YV = [torch.zeros(vm, inf["N"], device="cuda") for inf in infos]
-            vcalls = []
-            for l in range(a.layers):
-                sl = slice(7 * l, 7 * l + 7)
-                vcalls.append(((ctypes.c_char_p * 7)(*names[sl]),
-                               (ctypes.c_void_p * 7)(*[x.data_ptr() for x in XV[sl]]),
-                               (ctypes.c_void_p * 7)(*[y.data_ptr() for y in YV[sl]])))
-            vbytes = float(sum(inf["blob_bytes"] + inf["side_bytes"] + 2 * inf["K"] * vm + 4 * vm * inf["N"]
-                               for inf in infos))
-            verify = {"m": vm}
-            for a8, key in ((0, "fp16_x"), (1, "int8_x")):
-                lib.lw_set_act8(a8)
-                try:
-                    def vstep():
-                        for nm, xx, yy in vcalls:
-                            if lib.lw_group_matmul_dev(rt.h, 7, nm, xx, vm, yy, stream) != 0:
-                                raise RuntimeError(lib.lw_last_error().decode())
-                    vstep()
-                    torch.cuda.synchronize()
-                    t0 = time.perf_counter()
-                    for _ in range(a.steps):
-                        vstep()
-                    torch.cuda.synchronize()
-                    vms = (time.perf_counter() - t0) * 1e3 / a.steps
-                finally:
-                    lib.lw_set_act8(0)
-                verify[key] = {"ms_per_step": round(vms, 4), "GBps_coded": round(vbytes / (vms * 1e-3) / 1e9, 1),
-                               "over_one_m1_step": round(vms / ms_per_step, 3)}
-                log("bench: verify m=%d (%s): %.3f ms per step, %.1f GB/s coded" % (vm, key, vms, verify[key]["GBps_coded"]))
-            # config 4's comparison: the 5 tokens as 5 m = 1 steps over the same layers (the headline step, timed above)
-            verify["five_m1_steps_ms"] = round(vm * ms_per_step, 4)
-            verify["fp16_x"]["over_five_m1_steps"] = round(verify["fp16_x"]["ms_per_step"] / (vm * ms_per_step), 3)
-            del XV, YV
 
         # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
         # matrices, with the default GEMM (the hand-written matrix-core GEMM over the codes, k_gemm_prefill) and with

@@ -145,7 +145,8 @@ int lw_test_quant_x8(const void* X, int x_f16, int m, int K, int8_t* xq, float* 
 /* Times `iters` repetitions (after `warmup`) of lw_group_matmul_dev over `ngroups` groups laid out back to back in
  * names/X/Y (group g has sizes[g] matrices), cycling through the groups, with HIP events on the launch stream.
  * out[0] = mean ms per pass over all groups, out[1] = mean ms per pass of the groups' kernels alone (events around
- * each group's launches: decode + GEMV and reduction), out[2] = number of kernel launches per pass. */
+ * each pass of the groups' launches, host work excluded: min(iters, 20) passes enqueued back to back after one that
+ * is not counted), out[2] = number of kernel launches per pass. */
 int lw_bench_groups(void* h, int ngroups, const int* sizes, const char* const* names, const void* const* X, int m,
                     float* const* Y, int warmup, int iters, double* out);
 
