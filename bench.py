@@ -13,7 +13,9 @@ accounting; device-layout padding is not credited).
 roofline: the dominant kernel (k_fused_tiles: a tile per wave copied to LDS, 8 chains per lane; one grouped launch
 per layer that also sums the tile-column partials)
 timed with HIP events around each pass of the layers' launches on their stream (the launches run back to back),
-divided by the launches per pass; achieved = the layer's algorithmic bytes / that mean duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view). traffic = HBM
+divided by the launches per pass; achieved = the layer's algorithmic bytes / that mean duration, peak = 8 TB/s. serial_per_matrix: the same step with every GEMV launched on its own (latency view);
+decode_step_forward_order: the same GEMVs as a forward pass orders them (per layer q, k, v grouped, then o, then gate
+and up grouped, then down: 4 dependent launches, kernels/llmrt.cu:2366-2411). traffic = HBM
 bytes per layer launch from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --profile`,
 each scaled by what the counter reads for the 256 MiB device copy that --profile also runs (null when rocprofv3 is
 unavailable or a pass fails). cpu_baseline: the oracle's restatement of the reference CPU path (cpu_decode,
@@ -53,11 +55,19 @@ def counter_pass(counter, layers, tmp, timeout=240):
            os.path.abspath(__file__), "--profile", "--steps", "2", "--layers", str(layers)]
     log("bench: counter pass %s" % counter)
     p = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, start_new_session=True)
+    timed_out = False
     try:
         p.wait(timeout=timeout)
     except subprocess.TimeoutExpired:
+        timed_out = True
+    # the pass's own process group (its session, started above) is reaped whether or not rocprofv3 ended by itself:
+    # a child of the profiler that outlives it would otherwise outlive bench.py
+    try:
         os.killpg(p.pid, signal.SIGKILL)
-        p.wait()
+    except (ProcessLookupError, PermissionError):
+        pass
+    p.wait()
+    if timed_out:
         log("bench: counter pass %s timed out" % counter)
         return None
     rows = {}
@@ -307,6 +317,22 @@ def main():
                 if lib.lw_group_matmul_dev(rt.h, 1, nm, xx, m, yy, stream) != 0:
                     raise RuntimeError(lib.lw_last_error().decode())
 
+        # a decode step in the order the reference's forward pass issues a layer's matmuls (rt_forward,
+        # kernels/llmrt.cu:2366-2411): q, k, v together, then o, then gate and up together, then down, each launch
+        # on the same stream after the one before (4 dependent launches per layer)
+        dep = []
+        for l in range(a.layers):
+            for part in ((0, 1, 2), (3,), (4, 5), (6,)):
+                ii = [7 * l + i for i in part]
+                k_ = len(ii)
+                dep.append((k_, (ctypes.c_char_p * k_)(*[names[i] for i in ii]),
+                            (ctypes.c_void_p * k_)(*[xp[i] for i in ii]), (ctypes.c_void_p * k_)(*[yp[i] for i in ii])))
+
+        def dependent_step():
+            for k_, nm, xx, yy in dep:
+                if lib.lw_group_matmul_dev(rt.h, k_, nm, xx, m, yy, stream) != 0:
+                    raise RuntimeError(lib.lw_last_error().decode())
+
         if a.profile:
             if a.act8 and lib.lw_set_act8(1) != 0:
                 raise SystemExit("bench.py: int8 activations refused: " + lib.lw_last_error().decode())
@@ -399,6 +425,16 @@ def main():
         serial_ms = (time.perf_counter() - t0) * 1e3 / a.steps
         log("bench: serial per-matrix launches %.3f ms per step, %.1f GB/s coded"
             % (serial_ms, bytes_per_step / (serial_ms * 1e-3) / 1e9))
+        for _ in range(max(20, a.warmup)):
+            dependent_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            dependent_step()
+        torch.cuda.synchronize()
+        dep_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+        log("bench: decode step in forward order (4 launches per layer) %.3f ms per step, %.1f GB/s coded"
+            % (dep_ms, bytes_per_step / (dep_ms * 1e-3) / 1e9))
 
         ctrl = lib.lw_stream_read_gbps(1 << 31, 10)
         log("bench: streaming-read control %.1f GB/s" % ctrl)
@@ -575,6 +611,9 @@ def main():
                          "mean_launch_us": round(layer_us, 2), "launches_per_pass": launches},
             "serial_per_matrix": {"ms_per_step": round(serial_ms, 4),
                                   "GBps": round(bytes_per_step / (serial_ms * 1e-3) / 1e9, 1)},
+            "decode_step_forward_order": {"launches_per_layer": 4, "ms_per_step": round(dep_ms, 4),
+                                          "us_per_layer": round(dep_ms * 1e3 / a.layers, 2),
+                                          "GBps": round(bytes_per_step / (dep_ms * 1e-3) / 1e9, 1)},
             "cpu_baseline": cpu,
             "control_stream_read_GBps": round(ctrl, 1),
             "control_packed_twin": packed,

@@ -69,11 +69,19 @@ def _vregs(op):
     return {int(m.group(1))} if m else set()
 
 
+# wait states after a matrix-core write of a VGPR before a DPP read of it (at least the longest MFMA form's
+# MFMA-to-VALU read wait: 16 passes and a few more)
+MFMA_WAITS = 19
+
+
 def dpp_violations(disasm):
     """DPP operations in an llvm-objdump disassembly of gfx950 code without their wait states: 2 after a VALU write
-    of the DPP source (src0), 5 after a write of EXEC. The walk goes back over the operation's basic block (branch
-    targets and function starts end it); at a block start the predecessor is unknown, so 5 wait states (s_nop) must
-    lie inside the block. Returns "function at 0xaddr" strings."""
+    of the DPP source (src0), 5 after a write of EXEC (an SALU write naming exec, or any v_cmpx, which writes EXEC
+    implicitly), and MFMA_WAITS after a matrix-core (v_mfma) write of the DPP source (a bound above the MFMA-to-VALU
+    read wait of the longest form, 16 passes). The walk goes back over the operation's basic block (branch targets
+    and function starts end it); at a block start the predecessor is unknown, so 5 wait states (s_nop) must lie
+    inside the block (an MFMA write before the block start is not seen: none of this build's DPP sources comes from
+    the matrix cores). Returns "function at 0xaddr" strings."""
     import re
     fn, base = "?", 0
     ins, targets = [], set()
@@ -105,11 +113,13 @@ def dpp_violations(disasm):
             if mn.startswith("s_nop"):
                 waits += (int(ops[0], 0) if ops else 0) + 1
             else:
-                if ops and ((mn.startswith("v_") and (_vregs(ops[0]) & src) and waits < 2) or
-                            (ops[0].startswith("exec") and waits < 5)):
+                writes_src = bool(ops) and mn.startswith("v_") and bool(_vregs(ops[0]) & src)
+                if ((writes_src and mn.startswith("v_mfma") and waits < MFMA_WAITS) or
+                        (writes_src and waits < 2) or
+                        (((ops and ops[0].startswith("exec")) or mn.startswith("v_cmpx")) and waits < 5)):
                     break
                 waits += 1
-            if waits >= 5:
+            if waits >= MFMA_WAITS:
                 ok = True
                 break
             j -= 1

@@ -57,10 +57,17 @@ namespace {
 // manifest text (cfg lines first, then one t line per tensor in write order) is kept in memory and written by
 // finish(). A refused name or key writes nothing and is reported by the call; an I/O error sticks, and finish() then
 // reports failure.
+// The directory and any missing parents (the reference Writer's os.makedirs(path, exist_ok=True),
+// lazyweights/bundle.py:114-120); a failure shows as weights.bin failing to open.
+void make_dirs(const std::string& dir) {
+  for (size_t i = 1; i <= dir.size(); ++i)
+    if (i == dir.size() || dir[i] == '/') mkdir(dir.substr(0, i).c_str(), 0755);
+}
+
 class BundleWriter {
  public:
   explicit BundleWriter(const std::string& dir) : dir_(dir) {
-    mkdir(dir.c_str(), 0755);
+    make_dirs(dir);
     bin_ = fopen((dir + "/weights.bin").c_str(), "wb");
     ok_ = bin_ != nullptr;
   }

@@ -47,3 +47,20 @@ def test_a_dpp_operation_at_a_block_start_needs_its_waits_inside_the_block():
     text = HEAD + "".join(line(0x1000 + 4 * i, r) for i, r in enumerate(rows))
     text += line(0x1000 + 4 * len(rows), "s_branch 0", target=4 * 4)  # jumps to the s_nop
     assert not dpp_violations(text)
+
+
+def test_vcmpx_writes_exec_and_needs_five_wait_states():
+    """v_cmpx writes EXEC implicitly (its first operand names vcc or an SGPR pair, not exec)."""
+    pad = ["s_mov_b32 s0, 0"] * 6
+    assert dpp_violations(body(*pad, "v_cmpx_gt_u32_e32 vcc, s4, v1", DPP))
+    assert dpp_violations(body(*pad, "v_cmpx_gt_u32_e64 s[4:5], s4, v1", "v_nop", "v_nop", DPP))
+    assert not dpp_violations(body(*pad, "v_cmpx_gt_u32_e32 vcc, s4, v1", "s_nop 4", DPP))
+
+
+def test_mfma_write_of_the_dpp_source_needs_the_matrix_core_wait():
+    pad = ["s_mov_b32 s0, 0"] * 6
+    mfma = "v_mfma_f32_4x4x4_16b_f16 v[4:7], v[0:1], v[2:3], v[4:7]"
+    assert dpp_violations(body(*pad, mfma, "s_nop 2", DPP))       # v5 written by the MFMA, 3 wait states
+    assert dpp_violations(body(*pad, mfma, "s_nop 7", "s_nop 7", DPP))  # 16
+    assert not dpp_violations(body(*pad, mfma, "s_nop 7", "s_nop 7", "s_nop 2", DPP))  # 19
+    assert not dpp_violations(body(*pad, "v_mfma_f32_4x4x4_16b_f16 v[8:11], v[0:1], v[2:3], v[8:11]", DPP))

@@ -316,7 +316,9 @@ def test_full_config1_layer(gpu, tmp_path):
 def test_full_config4_q4k_verify(gpu, tmp_path):
     """Config 4's Q4_K half: the Mistral-shaped layer (H = 2.3) verified with m = 5 tokens as one grouped call, each
     matrix against fp64 (the contract) and against five m = 1 calls token by token (fp32 rounding: the m = 5 kernel
-    forms its products on the matrix cores in another order; 5e-6 of max |y|)."""
+    forms its products on the matrix cores in another order; 5e-6 of max |y|). The m = 1 grouped calls are the
+    bench's headline launch (the 7 config-2-shaped matrices of a layer in one launch of the whole-tile kernel): each
+    token's results are checked against fp64 directly too (the reference's check, kernels/llmrt.cu:2866-2883)."""
     import torch
     from lazyweights_amd import Runtime, bundle
     from lazyweights_amd.configs import CONFIG4
@@ -341,6 +343,8 @@ def test_full_config4_q4k_verify(gpu, tmp_path):
             codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
             y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X[name].double().numpy())
             check_err(a, y64, "config 4 %s m=5" % name)
+            for j in range(5):  # the grouped m = 1 launch, token by token
+                check_err(b[j:j + 1], y64[j:j + 1], "config 4 %s grouped m=1 token %d" % (name, j))
             del codes, side
 
 
@@ -387,6 +391,28 @@ def test_gpu_grouped_launch_matches_single(fmt_rt):
         assert torch.equal(a, b)
 
 
+def verify_on_exception_tiles(rt, name, W64, K, N, orc):
+    """fp16 device x at m = 2, 5 and 8 on a matrix with exception tiles: the default (the matrix-core verify kernel,
+    every tile in place) against the ring kernels (mode 7, exception tiles through their separate pass) within
+    5e-6 of max |y|, both within tolerance of fp64."""
+    import torch
+    for m in (2, 5, 8):
+        X = torch.randn(m, K).half()
+        y64 = orc.gemv_f64(W64, X.double().numpy())
+        ys = {}
+        for mode in (0, 7):
+            assert rt.lib.lw_set_kernel_mode(mode) == 0
+            try:
+                Y = torch.zeros(m, N, device="cuda")
+                rt.matmul_dev(name, X.cuda(), Y)
+                torch.cuda.synchronize()
+                ys[mode] = Y.cpu().numpy()
+            finally:
+                rt.lib.lw_set_kernel_mode(0)
+            check_err(ys[mode], y64, "%s m=%d mode %d" % (name, m, mode))
+        assert np.abs(ys[0] - ys[7]).max() <= 5e-6 * np.abs(ys[7]).max(), (name, m)
+
+
 def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
     """A matrix whose tile 5 has no ring schedule: the ring kernel skips it and an exception pass decodes it (the
     low-latency kernel for m = 1, the whole-tile kernel for m > 1); GEMV (m = 1, fp16 x) and fp32-x m = 3 against
@@ -410,6 +436,7 @@ def test_gpu_ring_exception_tile(gpu, tmp_path, orc):
         torch.cuda.synchronize()
         check_err(Y.cpu().numpy(), y64[:1], "exception tile m=1")
         check_err(rt.test_matmul("skew", X.float().numpy(), path=0), y64, "exception tile fp32 m=3")
+        verify_on_exception_tiles(rt, "skew", W64, 8192, 128, orc)
 
 
 def test_gpu_exception_tiles_in_place(gpu, tmp_path, orc):
@@ -464,6 +491,7 @@ def test_gpu_exception_tiles_in_place(gpu, tmp_path, orc):
         check_err(runs[0][1], ys64, "in-place exceptions grouped: small")
         check_err(runs[0][2], y64[:1], "in-place exceptions grouped")
         check_err(rt.test_matmul("mskew", X.float().numpy(), path=0), y64, "exception pass fp32 m=3")
+        verify_on_exception_tiles(rt, "mskew", W64, 8192, 128, orc)
 
 
 def test_gpu_low_latency_kernel_same_bits(fmt_rt, orc, tmp_path):

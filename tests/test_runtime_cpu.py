@@ -260,6 +260,12 @@ def test_writer_and_manifest_round_trip(lib, tmp_path):
     w2.close()
     cfg, ts = bundle.read_manifest(str(tmp_path / "two"))
     assert cfg == {} and [t["name"] for t in ts] == ["x"] and ts[0]["offset"] == 0 and ts[0]["nbytes"] == 3
+    # missing parent directories are created (the reference Writer's os.makedirs, lazyweights/bundle.py:114-120)
+    w3 = bundle.Writer(str(tmp_path / "a" / "b" / "c"))
+    w3.add("y", "raw8", 1, 2, 1.0, 0, b"yz")
+    w3.close()
+    cfg, ts = bundle.read_manifest(str(tmp_path / "a" / "b" / "c"))
+    assert [t["name"] for t in ts] == ["y"] and ts[0]["nbytes"] == 2
     w.close()
     cfg, ts = bundle.read_manifest(str(tmp_path))
     assert cfg == {"hidden": "512", "eps": "1e-05"}
