@@ -259,7 +259,7 @@ def main():
     def further_configs(work):
         steps = max(3, a.steps // 2)
         return {"config1": time_config(lib, Runtime, bundle, torch, work, "config1", CONFIG1, 8, (1,), steps),
-                "config3": time_config(lib, Runtime, bundle, torch, work, "config3", CONFIG3, 4, (1,), steps),
+                "config3": time_config(lib, Runtime, bundle, torch, work, "config3", CONFIG3, 4, (1, 5), steps),
                 "config4_q5k": time_config(lib, Runtime, bundle, torch, work, "config4_q5k",
                                            [mt for mt in CONFIG4 if mt[1] == Q5_K], 3, (1, 5), steps)}
 

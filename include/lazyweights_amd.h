@@ -102,7 +102,7 @@ int lw_group_matmul_dev(void* h, int count, const char* const* names, const void
  * per wave copied to LDS, 8 chains per lane, every tile including exception tiles), or the half-tile kernel (two
  * buffered half-tile units per wave, the next one's copy in flight while one decodes) where the whole-tile kernel's
  * blocks would have fewer than 10 waves (few tiles per CU); m = 1 with int8 activations, the whole-tile kernel;
- * 2 <= m <= 8 with fp16 activations and Q4_K / Q5_K, or with int8 activations and every format, the whole-tile
+ * 2 <= m <= 8 with fp16 or int8 activations and every format, the whole-tile
  * kernel with its products on the matrix cores; otherwise the ring-staged kernels wherever a matrix has a ring
  * schedule (the block-per-column kernel). 1 = the whole-tile fallback kernel everywhere; 2 = the block-per-column ring
  * kernel for every m; 7 = the ring-staged kernels for every m (for m = 1 the flat, load-balanced ring kernel);

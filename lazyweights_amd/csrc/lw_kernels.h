@@ -135,7 +135,7 @@ constexpr int TILES_CANON_WAVES = 12;
 hipError_t launch_fused_halves(const FlatPlan& plan, int per, hipStream_t s);
 int halves_buf_rows(const FlatPlan& plan);
 int tiles_buf_rows(const FlatPlan& plan);
-// The whole-tile kernel for 2..8 tokens of fp16 activations (Q4_K / Q5_K, plan.mt tokens, every tile of each entry):
+// The whole-tile kernel for 2..8 tokens of fp16 activations (every format, plan.mt tokens, every tile of each entry):
 // the products on the matrix cores (4x4x4 blocks, x broadcast from one block), every token in one pass over the
 // tiles; each block forms the x sums of its tile columns in LDS (tiles_mma_xs_bytes beside W tile buffers of
 // tiles_buf_rows word rows)

@@ -2466,17 +2466,20 @@ k_fused_halves(FlatPlan plan, int per, int ubuf_rows) {
   reduce_pending();
 }
 
-// ── whole-tile kernel on the matrix cores (2..8 tokens, fp16 activations, Q4_K / Q5_K) ─────────────────────
+// ── whole-tile kernel on the matrix cores (2..8 tokens, fp16 activations, every format) ───────────────────
 // The decode of k_fused_tiles (a tile per wave in LDS; 4 chains per lane), with the products of MT tokens on
 // v_mfma_f32_4x4x4f16 (16 blocks of 4 lanes): block b computes D[i][j] = sum_k A[4 b' + i][k] B[4 b + j][k] into lane
 // 4 b + j, register i, where b' is the block named by the instruction's broadcast field (cbsz 4, abid b'). B = the
 // lane's own 4 weights of the pair (its row), A = the 4 x values of token i at those positions, broadcast from block
 // b' of a register that holds 16 position blocks: x of a tile column fits 8 (4-bit formats) or 4 register pairs per
-// 4 tokens, with no LDS traffic. The weights enter as sc q (Q5_K: fp16(q) sc; Q4_K: sc q / 16 from the 0x54 byte
-// permute and one fma, every step exact), so one accumulator per super-block and 4 tokens suffices; d (x 16 for
-// Q4_K) applies once per super-block. The mins term dmin sum_j m_j (sum x)_j runs on the same instruction with
-// A = the sub-block sums of x as fp16 hi and lo (XS) and B = the row's mins. Each token's values agree with its own
-// m = 1 launch to fp32 rounding (another order of the same products). Partials [KT][mt][N], the in-launch reduction.
+// 4 tokens, with no LDS traffic. The weights enter unscaled and exact in fp16: the 4-bit formats' grid bytes (Q4_K q,
+// IQ4_XS kv[q] + 128) as denormals g 2^-24 from one byte permute per table entry, the 8-bit formats' fp16(f(q))
+// (Q5_K q, Q6_K q - 32) from the entries; each chain keeps its current sub-block's sums of 4 tokens in one
+// accumulator and folds them into fp32 with d s_j (2^24 d s_j for the denormal form; s_j signed for Q6_K and
+// IQ4_XS) when the sub-block ends. The offset terms run on the same instruction with A = the sub-block sums of x as
+// fp16 hi and lo (XS): Q4_K / Q5_K dmin sum_j m_j (sum x)_j with B = the row's mins, IQ4_XS 128 d sum_j s_j (sum x)_j
+// (the grid's +128) with B = the row's signed scales; Q6_K has none. Each token's values agree with its own m = 1
+// launch to fp32 rounding (another order of the same products). Partials [KT][mt][N], the in-launch reduction.
 // The tile pipeline is k_fused_tiles': tables by direct-to-LDS loads, paced first copies, row-major tiles, the next
 // tile's copy issued as soon as a decode ends.
 // at most 16 waves per block (4 per SIMD: 128 VGPRs); 12 (3 per SIMD) for 8 tokens of the 4-bit formats, whose
@@ -2493,7 +2496,6 @@ __device__ __forceinline__ f4v mfma4_from(h4v a, h4v b, f4v c) {
 template <int KQ, int NTAB, int MT>
 __global__ void __launch_bounds__(64 * tiles_mma_waves(KQ, MT), 1)
 k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
-  static_assert(KQ == KQ_Q4_K || KQ == KQ_Q5_K, "scaled codes are exact in fp16 for Q4_K / Q5_K only");
   static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
   constexpr int SYMB = kq_symbits(KQ);
   constexpr int TW = SYMB == 4 ? 2 * TK : TK;
@@ -2503,7 +2505,9 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
   constexpr int NC = 4, NG = 16 / NC;  // chains per lane (64 symbols each: 8 tokens' x and accumulators leave no
                                        // registers for 8 chains at 4 waves per SIMD), 16-symbol groups per chain
-  constexpr int GPSUB = SYMB == 4 ? 1 : 2;  // 16-symbol groups per sub-block of 32 weights
+  constexpr int GW = kq_gw(KQ), NSUB = 256 / GW;          // weights per sub-block, sub-blocks per super-block
+  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block
+  constexpr bool XSUMS = KQ != KQ_Q6_K;                   // an offset term over the sub-blocks' x sums
   // the weights enter unscaled: 4-bit codes as fp16 denormals q 2^-24 (one byte permute per entry), 8-bit formats as
   // fp16(q) from the table; each chain's sums per sub-block are scaled by dA s_j (2^24 s_j) when the sub-block ends
   constexpr float WSCALE = SYMB == 4 ? 16777216.f : 1.f;
@@ -2605,7 +2609,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   const int ncb = (NTAB > 1 && mb != ma) ? cols(eb, 0, Tl - eb->tile0, cb0) : 0;
   uint64_t* xsb = reinterpret_cast<uint64_t*>(tbuf + (size_t)W * buf_rows * 32);
   const int xw0 = W > C ? C : 0, xnw = W - xw0;
-  if (wave >= xw0) {
+  if (XSUMS && wave >= xw0) {
     const int na = nca * mt * GPC, ntot = na + ncb * mt * GPC;
     for (int i = (wave - xw0) * 64 + lane; i < ntot; i += xnw * 64) {
       const bool second = i >= na;
@@ -2654,7 +2658,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
   // every share of the x sums stored: checked at each tile start until it holds; a tile that starts earlier (a
   // first tile) reads its sums after its decode instead
-  bool xs_ready = false;
+  bool xs_ready = !XSUMS;
 #pragma unroll 1
   while (have) {
     if (!xs_ready)
@@ -2701,7 +2705,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       for (int q = 0; q < NQ; ++q) {
         const int tok = 4 * q + qi, cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
         uint64_t sv = 0;
-        if (tok < mt && qb < 4 * NSB) {
+        if (XSUMS && tok < mt && qb < 4 * NSB) {
           const int lc = second ? nca + (tc - cb0 + KT) % KT : (tc - ca0 + KT) % KT;  // the column's slot
           sv = xsb[((size_t)lc * mt + tok) * (GPC * 2) + 2 * sh + lo];
         }
@@ -2722,13 +2726,20 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
     }
     // the lane's sub-block scales (bytes, low first) per super-block
-    uint64_t scq[NSB];
+    uint64_t scq[NSB], scq2[NSB];  // scales of sub-blocks 0..7 and (Q6_K) 8..15
     float dA[NSB], dB[NSB];
 #pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) {
-      uint64_t q2;
-      side_packed<KQ>(sw[sb], scq[sb], q2, dA[sb], dB[sb]);
-    }
+    for (int sb = 0; sb < NSB; ++sb) side_packed<KQ>(sw[sb], scq[sb], scq2[sb], dA[sb], dB[sb]);
+    // s_j of sub-block js of the tile row (a constant after unrolling), extracted where it is used: the scale words
+    // are opaque here, so the compiler does not hold every converted scale through the decode (8 tokens of IQ4_XS
+    // spilled)
+    auto scale_of = [&](int js) -> float {
+      const int jsb = js / NSUB, jj = js % NSUB;
+      uint32_t w = (uint32_t)((jj >= 8 ? scq2[jsb] : scq[jsb]) >> (32 * ((jj % 8) / 4)));
+      asm("" : "+v"(w));
+      const uint32_t b = (w >> (8 * (jj % 4))) & 255u;
+      return (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)b : (float)b;
+    };
     f4v acc[NC][NQ];  // per chain: its current sub-block's sums, 4 tokens per register quad
     float fa[NQ][4];  // scaled sums of the finished sub-blocks
 #pragma unroll
@@ -2793,7 +2804,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         static_for<NC>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
           constexpr int js = (NG * j + gi) / GPSUB;  // sub-block within the tile row
-          const float sa = dA[js / 8] * WSCALE * (float)(uint32_t)((scq[js / 8] >> (8 * (js % 8))) & 255u);
+          const float sa = dA[js / NSUB] * WSCALE * scale_of(js);
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
 #pragma unroll
@@ -2831,12 +2842,19 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
       ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
       copy_tile(sec ? eb : ea, t);
     }
-    // mins: per super-block and token, sum_j m_j (sum x)_j from the hi and lo halves of the sums
+    // offset terms: per super-block and token, sum_j c_j (sum x)_j from the hi and lo halves of the sums, c_j = the
+    // mins m_j (Q4_K / Q5_K) or the signed scales s_j (IQ4_XS)
     f4v mac[NSB][NQ];
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
+      if constexpr (!XSUMS) break;
       float mf[8];
-      side_mins(sw[sb], mf);
+      if constexpr (KQ == KQ_IQ4_XS) {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) mf[jj] = scale_of(8 * sb + jj);
+      } else {
+        side_mins(sw[sb], mf);
+      }
       const h4v m0 = h4v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3]};
       const h4v m1 = h4v{(_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
 #pragma unroll
@@ -2862,8 +2880,11 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float tot = fa[q][i];
+        if constexpr (XSUMS) {
 #pragma unroll
-        for (int sb = 0; sb < NSB; ++sb) tot = fmaf(-dB[sb], mac[sb][q][i], tot);
+          for (int sb = 0; sb < NSB; ++sb)
+            tot = fmaf(KQ == KQ_IQ4_XS ? -128.f * dA[sb] : -dB[sb], mac[sb][q][i], tot);
+        }
         if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
@@ -3401,7 +3422,6 @@ hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
       p.W > tiles_mma_max_waves(p.e[0].M.kqt, p.mt))
     return hipErrorInvalidValue;
   const int kqt = p.e[0].M.kqt;
-  if (kqt != KQ_Q4_K && kqt != KQ_Q5_K) return hipErrorInvalidValue;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
@@ -3414,7 +3434,13 @@ hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
   if (rows > 256 ||
       (size_t)p.W * rows * 128 + tiles_mma_xs_bytes(p, per) + (p.n > 1 ? 2 : 1) * 4 * LUTN + 16 > 160 * 1024)
     return hipErrorInvalidValue;
-  return kqt == KQ_Q4_K ? tiles_mma_launch<KQ_Q4_K>(p, per, rows, s) : tiles_mma_launch<KQ_Q5_K>(p, per, rows, s);
+  switch (kqt) {
+    case KQ_Q4_K: return tiles_mma_launch<KQ_Q4_K>(p, per, rows, s);
+    case KQ_Q5_K: return tiles_mma_launch<KQ_Q5_K>(p, per, rows, s);
+    case KQ_Q6_K: return tiles_mma_launch<KQ_Q6_K>(p, per, rows, s);
+    case KQ_IQ4_XS: return tiles_mma_launch<KQ_IQ4_XS>(p, per, rows, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int KQ, int RS, int NTAB, bool I8, int MT = 1>

@@ -667,9 +667,9 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + 2 * (size_t)ts[i]->dm.NT;  // per tile row and half
   // partials and counters: the model's (grown on demand) or a caller's fixed scratch (nothing allocated; its counters
   // are cleared by a fill kernel on the stream, since the last call on that scratch may have left anything there)
-  // 2..8 tokens of fp16 activations, Q4_K / Q5_K: the whole-tile kernel with its products on the matrix cores
+  // 2..8 tokens of fp16 activations, every format: the whole-tile kernel with its products on the matrix cores
   auto mma_ok = [&](const lw::DevMat& dm) {
-    return (dm.kqt == lw::KQ_Q4_K || dm.kqt == lw::KQ_Q5_K) && !dm.packed && dm.dsplit && dm.lut4 && dm.rows &&
+    return dm.kqt >= lw::KQ_Q4_K && dm.kqt <= lw::KQ_IQ4_XS && !dm.packed && dm.dsplit && dm.lut4 && dm.rows &&
            dm.max_rows + 2 <= 256;
   };
   const bool mma = !x8 && per == 1 && mt >= 2 && mt <= 8 && g_kernel_mode == 0;

@@ -348,6 +348,37 @@ def test_full_config4_q4k_verify(gpu, tmp_path):
             del codes, side
 
 
+def test_full_config3_verify(gpu, tmp_path):
+    """Config 3's layer (Q6_K down, IQ4_XS gate / up) verified with m = 5 tokens as one grouped call (the
+    matrix-core verify kernel for every format): each matrix against fp64 and against five m = 1 grouped calls
+    (5e-6 of max |y|), which are checked against fp64 token by token too."""
+    import torch
+    from lazyweights_amd import Runtime, bundle
+    from lazyweights_amd.configs import CONFIG3
+    from oracle import oracle as orc
+    bundle.write_synthetic_bundle(str(tmp_path), CONFIG3, threads=16)
+    with Runtime(tmp_path) as rt:
+        names = [m[0] for m in CONFIG3]
+        X = {m[0]: torch.randn(5, m[3], generator=torch.Generator().manual_seed(m[5])).half() for m in CONFIG3}
+        y5 = {m[0]: torch.zeros(5, m[2], device="cuda") for m in CONFIG3}
+        say("config 3 m=5 grouped")
+        grouped_matmul(rt, names, [X[n].cuda() for n in names], 5, [y5[n] for n in names])
+        y1 = {m[0]: torch.zeros(5, m[2], device="cuda") for m in CONFIG3}
+        for j in range(5):
+            grouped_matmul(rt, names, [X[n][j:j + 1].cuda() for n in names], 1, [y1[n][j:j + 1] for n in names])
+        torch.cuda.synchronize()
+        for mat in CONFIG3:
+            name, kqt, N, K, H, seed = mat
+            a, b = y5[name].cpu().numpy(), y1[name].cpu().numpy()
+            say("config 3", name, "m=5 vs 5 x m=1: %.3g" % (np.abs(a - b).max() / np.abs(b).max()))
+            assert np.abs(a - b).max() <= 5e-6 * np.abs(b).max(), name
+            codes, side = bundle.synth_matrix(kqt, N, K, H, seed, threads=16)
+            y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X[name].double().numpy())
+            check_err(a, y64, "config 3 %s m=5" % name)
+            check_err(b, y64, "config 3 %s 5 x m=1" % name)
+            del codes, side
+
+
 def test_gpu_whole_tile_kernel_mode(fmt_rt, orc):
     """The whole-tile kernel (the fallback for matrices without a ring schedule) stays exact too."""
     import torch
@@ -726,8 +757,8 @@ def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
             assert torch.equal(a, b), name
             codes, side = bundle.synth_matrix(kqt, N, K, H, seed)
             assert np.array_equal(rp.test_decode(name), codes)
-            # m = 5: the ring kernel (mode 7) gives the packed twin's bits; the default for Q4_K / Q5_K (the
-            # matrix-core whole-tile kernel) the same values up to the fp32 order of its sums
+            # m = 5: the ring kernel (mode 7) gives the packed twin's bits; the default (the matrix-core whole-tile
+            # kernel) the same values up to the fp32 order of its sums
             X5 = torch.randn(5, K).half().cuda()
             y5c, y5p, y5d = (torch.zeros(5, N, device="cuda") for _ in range(3))
             assert rc.lib.lw_set_kernel_mode(7) == 0
