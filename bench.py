@@ -109,11 +109,50 @@ def measure_traffic(layers):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
-def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps):
+def time_prefill(lib, rt, torch, names, infos, ms=(128, 512), reps=5):
+    """Prefill shapes (fp32 x resident) over the named matrices through path 2 (decode to scratch + GEMM), per m
+    with the default GEMM (hand-written on the matrix cores over tiled codes) and with rocBLAS over fp16 hi + lo
+    weights (lw_set_prefill_gemm 4): ms per pass over the matrices and useful TFLOP/s (2 m N K per matrix)."""
+    import ctypes
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(5)
+    runs = []
+    for pm in ms:
+        XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos]
+        YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos]
+
+        def one_pass():
+            for nm, inf, x, y in zip(names, infos, XP, YP):
+                if lib.lw_matmul_dev(rt.h, nm, ctypes.c_void_p(x.data_ptr()), 0, pm, ctypes.c_void_p(y.data_ptr()),
+                                     inf["N"], stream) != 0:
+                    raise RuntimeError(lib.lw_last_error().decode())
+        flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos)
+        run = {"m": pm}
+        try:
+            for which, key in ((0, "own_mfma"), (4, "rocblas")):
+                lib.lw_set_prefill_gemm(which)
+                one_pass()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    one_pass()
+                torch.cuda.synchronize()
+                fms = (time.perf_counter() - t0) * 1e3 / reps
+                run[key] = {"ms_per_pass": round(fms, 3), "TFLOPs": round(flops / (fms * 1e-3) / 1e12, 1)}
+        finally:
+            lib.lw_set_prefill_gemm(0)
+        run["own_over_rocblas"] = round(run["rocblas"]["ms_per_pass"] / run["own_mfma"]["ms_per_pass"], 2)
+        runs.append(run)
+        del XP, YP
+    return runs
+
+
+def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps, prefill=False):
     """A further configuration of the benchmark contract: `layers` copies of its matrices (own seeds, together beyond
     the 256 MB Infinity Cache), one grouped call per layer and step, fp16 x resident. Per m: ms per step, GB/s of
     algorithmic coded bytes (as the headline), and the kernels alone timed with HIP events (lw_bench_groups) against
-    the HBM peak; for m > 1 also the same tokens as m consecutive m = 1 steps."""
+    the HBM peak; for m > 1 also the same tokens as m consecutive m = 1 steps. prefill: also the prefill shapes over
+    layer 0's matrices, one figure per format (time_prefill)."""
     import ctypes
     d = os.path.join(work, key)
     lm = [("l%d.%s" % (l, nm), kqt, N, K, H, seed + 97 * l) for l in range(layers)
@@ -193,6 +232,17 @@ def time_config(lib, rt_cls, bundle, torch, work, key, mats, layers, ms, steps):
                 if m > 1:
                     res["m%d" % m]["repeated_m1"]["gemm_over_one_m1_step"] = round(
                         res["m%d" % m]["ms_per_step"] / res["m1"]["ms_per_step"], 3)
+        if prefill:
+            res["prefill_path2"] = {}
+            for kqt in sorted({mt[1] for mt in mats}):
+                sel = [i for i in range(per) if lm[i][1] == kqt]
+                fmt = {1: "Q4_K", 2: "Q5_K", 3: "Q6_K", 4: "IQ4_XS"}[kqt]
+                runs = time_prefill(lib, rt, torch, [lm[i][0].encode() for i in sel], [infos[i] for i in sel])
+                res["prefill_path2"][fmt] = {"matrices": [lm[i][0] for i in sel], "runs": runs}
+                for r in runs:
+                    log("bench: %s prefill %s m=%d: own %.3f ms (%.1f TFLOP/s), rocblas %.3f ms (%.1f TFLOP/s)"
+                        % (key, fmt, r["m"], r["own_mfma"]["ms_per_pass"], r["own_mfma"]["TFLOPs"],
+                           r["rocblas"]["ms_per_pass"], r["rocblas"]["TFLOPs"]))
         return res
     finally:
         rt.close()
@@ -234,7 +284,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--no-packed", action="store_true", help="skip the packed-twin control")
-    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-shape (m = 128) figure")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-shape figures (m = 128 and 512)")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 1, 3 and 4 (Q5_K)")
     ap.add_argument("--only-configs", action="store_true",
                     help="time configs 1, 3 and 4 (Q5_K) only (for a kernel trace of their kernels)")
@@ -259,7 +309,8 @@ def main():
     def further_configs(work):
         steps = max(3, a.steps // 2)
         return {"config1": time_config(lib, Runtime, bundle, torch, work, "config1", CONFIG1, 8, (1,), steps),
-                "config3": time_config(lib, Runtime, bundle, torch, work, "config3", CONFIG3, 4, (1, 5), steps),
+                "config3": time_config(lib, Runtime, bundle, torch, work, "config3", CONFIG3, 4, (1, 5), steps,
+                                       prefill=not a.no_prefill),
                 "config4_q5k": time_config(lib, Runtime, bundle, torch, work, "config4_q5k",
                                            [mt for mt in CONFIG4 if mt[1] == Q5_K], 3, (1, 5), steps)}
 
@@ -475,38 +526,20 @@ def main():
 
         # prefill shapes (m = 128 and 512, fp32 x resident): the decode-to-scratch path (path 2) over layer 0's seven
         # matrices, with the default GEMM (the hand-written matrix-core GEMM over the codes, k_gemm_prefill) and with
-        # rocBLAS over fp16 hi + lo weights (a reported figure, not the metric)
+        # rocBLAS over fp16 hi + lo weights (a reported figure, not the metric); config 3 adds Q6_K and IQ4_XS
         prefill = None
         if not a.no_prefill:
-            prefill = {"path": "own_mfma (default): codes decoded to scratch, scaled to exact fp16 weights, "
-                               "v_mfma_f32_32x32x16_f16 with fp16 hi + lo x and fp32 accumulation; rocblas: codes "
-                               "dequantized to fp16 hi + lo weights, rocBLAS fp16 GEMM (one GEMM over 2m columns up "
-                               "to m = 512)", "runs": []}
-            for pm in (128, 512):
-                XP = [torch.randn(pm, inf["K"], generator=g).float().cuda() for inf in infos[:7]]
-                YP = [torch.zeros(pm, inf["N"], device="cuda") for inf in infos[:7]]
-
-                def prefill_layer():
-                    for i in range(7):
-                        if lib.lw_matmul_dev(rt.h, names[i], ctypes.c_void_p(XP[i].data_ptr()), 0, pm,
-                                             ctypes.c_void_p(YP[i].data_ptr()), infos[i]["N"], stream) != 0:
-                            raise RuntimeError(lib.lw_last_error().decode())
-                flops = sum(2.0 * pm * inf["N"] * inf["K"] for inf in infos[:7])
-                run = {"m": pm}
-                for which, key in ((0, "own_mfma"), (4, "rocblas")):
-                    lib.lw_set_prefill_gemm(which)
-                    prefill_layer()
-                    torch.cuda.synchronize()
-                    t0 = time.perf_counter()
-                    for _ in range(5):
-                        prefill_layer()
-                    torch.cuda.synchronize()
-                    fms = (time.perf_counter() - t0) * 1e3 / 5
-                    run[key] = {"ms_per_layer": round(fms, 3), "TFLOPs": round(flops / (fms * 1e-3) / 1e12, 1)}
-                    log("bench: prefill m=%d (%s): %.3f ms per layer, %.1f TFLOP/s" % (pm, key, fms, run[key]["TFLOPs"]))
-                lib.lw_set_prefill_gemm(0)
-                prefill["runs"].append(run)
-                del XP, YP
+            prefill = {"path": "own_mfma (default): codes decoded to scratch in a tiled layout, v_mfma_f32_32x32x16_f16 "
+                               "with fp16 hi + lo x and fp32 accumulation (Q4_K / Q5_K: weights scaled by their 6-bit "
+                               "sub-scales, exact in fp16; Q6_K / IQ4_XS: grid values, folded per sub-block in fp32); "
+                               "rocblas: codes dequantized to fp16 hi + lo weights, rocBLAS fp16 GEMM (one GEMM over "
+                               "2m columns up to m = 512)",
+                       "matrices": "config 2 layer 0 (Q4_K)",
+                       "runs": time_prefill(lib, rt, torch, [names[i] for i in range(7)], infos[:7])}
+            for r in prefill["runs"]:
+                log("bench: prefill m=%d: own %.3f ms per layer (%.1f TFLOP/s), rocblas %.3f ms (%.1f TFLOP/s)"
+                    % (r["m"], r["own_mfma"]["ms_per_pass"], r["own_mfma"]["TFLOPs"], r["rocblas"]["ms_per_pass"],
+                       r["rocblas"]["TFLOPs"]))
 
         configs = None if a.no_configs else further_configs(work)
 

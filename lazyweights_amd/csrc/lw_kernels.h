@@ -190,14 +190,15 @@ hipError_t launch_dequant_hilo(const DevMat& M, const uint8_t* codes, int row0, 
 // The same from the coded matrix directly (decode + dequant in one kernel; coded K-quant matrices with split
 // offsets): tile rows [tr0, tr1) -> WW rows relative to tr0 * 64
 hipError_t launch_decode_hilo(const DevMat& M, int tr0, int tr1, void* WW, hipStream_t s);
-// Prefill GEMM on the matrix cores for Q4_K / Q5_K (k_gemm_prefill): Y[t][row0 + r] for the chunk's rows r < nrows
-// (a multiple of 64) from its codes in the tiled layout (launch_decode_tiled) and x in the tiled layouts of
-// launch_prefill_x; K a multiple of 256
+// Prefill GEMM on the matrix cores, every K-quant format (k_gemm_prefill: Q4_K / Q5_K; k_gemm_prefill_sub: Q6_K /
+// IQ4_XS): Y[t][row0 + r] for the chunk's rows r < nrows (a multiple of 64) from its codes in the tiled layout
+// (launch_decode_tiled) and x in the tiled layouts of launch_prefill_x (SXT read for Q4_K / Q5_K only); K a multiple
+// of 256
 hipError_t launch_gemm_prefill(const DevMat& M, const uint8_t* CT, int row0, int nrows, const void* XT,
                                const void* SXT, int m, float* Y, int ldy, hipStream_t s);
 // codes of tile rows [tr0, tr1) in the prefill GEMM's tiled layout: per 32-row tile and 32-code chunk a 1 KB piece,
-// lane (h, c) = 32 h + c holding row c's codes 16 h .. 16 h + 15 of the chunk; hipErrorNotSupported unless
-// decode_tiled_ok (packed matrices, coded ones with split offsets)
+// lane (h, c) = 32 h + c holding row c's codes 16 h .. 16 h + 15 of the chunk (IQ4_XS: their grid bytes kv[q] + 128);
+// hipErrorNotSupported unless decode_tiled_ok (packed matrices, coded ones with split offsets)
 bool decode_tiled_ok(const DevMat& M);
 hipError_t launch_decode_tiled(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s);
 // fp32 X [m][K] -> XT (fp16 hi / lo pieces, prefill_x_bytes) and SXT (per-sub-block sums as fp16 hi / lo,

@@ -3756,7 +3756,7 @@ __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ 
   const int tc = (int)(tt % M.KT), trr = (int)(tt / M.KT);
   const uint4 c = reinterpret_cast<const uint4*>(M.words)[((size_t)(tr0 + trr) * M.KT + tc) * 1024 + (size_t)(g * 64 + L)];
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-  if (TILED) {  // the prefill GEMM's layout (launch_decode_tiled): 16 codes per 16-byte piece
+  if (TILED) {  // the prefill GEMM's layout (launch_decode_tiled): 16 codes (IQ4_XS: grid bytes) per 16-byte piece
     const int row = trr * TN + L, KC = M.K / 32;
     uint8_t* o = out + ((size_t)(row >> 5) * KC * 64 + (row & 31)) * 16;
     if (SYMB == 4) {  // 32 codes = one chunk: symbols 0..7 -> piece h = 0, 8..15 -> h = 1
@@ -3767,7 +3767,10 @@ __global__ void __launch_bounds__(256) k_unpack(DevMat M, uint8_t* __restrict__ 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t sy = (w[2 * hh + (q >> 1)] >> (16 * (q & 1))) & 0xFFFFu;
-          v[q] = (sy & 15u) | ((sy >> 4) & 15u) << 8 | ((sy >> 8) & 15u) << 16 | (sy >> 12) << 24;
+          if (M.kqt == KQ_IQ4_XS)  // grid bytes kv[q] + 128 from the symbol table (lut4 bytes 2, 3)
+            v[q] = (M.lut4[sy & 255u] >> 16) | (M.lut4[sy >> 8] >> 16) << 16;
+          else
+            v[q] = (sy & 15u) | ((sy >> 4) & 15u) << 8 | ((sy >> 8) & 15u) << 16 | (sy >> 12) << 24;
         }
         *reinterpret_cast<uint4*>(o + (kc * 64 + 32 * hh) * 16) = make_uint4(v[0], v[1], v[2], v[3]);
       }
@@ -3885,7 +3888,7 @@ __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restr
 // but each lane runs the two 32-symbol chains of its 64-symbol segment (split starts 2k and 2k + 1) interleaved, and
 // stores its codes straight from registers: 16 codes make one lane's piece of the tiled layout, and the 32 lanes of a
 // row half write 32 consecutive pieces (512 B) per store. No code rows in LDS: the block holds the table and the tile.
-template <int SYMB>
+template <int SYMB, bool GRID>
 __global__ void __launch_bounds__(256) k_decode_tiled(DevMat M, uint8_t* __restrict__ out, int tr0, int tr1,
                                                       int stage_rows) {
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
@@ -3896,9 +3899,14 @@ __global__ void __launch_bounds__(256) k_decode_tiled(DevMat M, uint8_t* __restr
   if (t >= tr1 * KT) return;
   const int tc = t % KT, tr = t / KT;
   const int R = min((int)M.rows[t] + 2, stage_rows);
-  for (int i = threadIdx.x; i < LUTN; i += 256) {
-    const uint32_t e = M.lut[i];
-    lut4[i] = (e >> 8) | (e & 255u) << 16;
+  if (GRID) {  // entries len | grid byte of the pair's first code << 16 | second << 24 (decode_table4)
+    for (int i = threadIdx.x; i < LUTN / 4; i += 256)
+      reinterpret_cast<uint4*>(lut4)[i] = reinterpret_cast<const uint4*>(M.lut4)[i];
+  } else {
+    for (int i = threadIdx.x; i < LUTN; i += 256) {
+      const uint32_t e = M.lut[i];
+      lut4[i] = (e >> 8) | (e & 255u) << 16;
+    }
   }
   const uint4* src = reinterpret_cast<const uint4*>(M.words + M.tbase[t]);
   for (int i = threadIdx.x; i < 8 * R; i += 256) reinterpret_cast<uint4*>(tw)[i] = src[i];
@@ -3940,8 +3948,8 @@ __global__ void __launch_bounds__(256) k_decode_tiled(DevMat M, uint8_t* __restr
       slot[ch] = nslot;
       C[ch] = *(LdsU32*)(rlb + (nslot << 7));
       const uint32_t s1 = e1 >> 16, s2 = e2 >> 16;
-      if (SYMB == 4) {  // 4 codes per pair, low nibble first; a piece every 4 pairs
-        acc[ch][p & 3] = (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
+      if (SYMB == 4) {  // 4 codes per pair, low nibble first (GRID: their grid bytes); a piece every 4 pairs
+        acc[ch][p & 3] = GRID ? s1 | s2 << 16 : (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
         if ((p & 3) == 3) {
           const int q = p >> 2;  // piece q of the chain's 64 codes: chunk kc0 + 2 ch + q / 2, half q % 2
           *reinterpret_cast<uint4*>(obase + ((size_t)(kc0 + 2 * ch + (q >> 1)) * 64 + 32 * (q & 1)) * 16) =
@@ -3982,7 +3990,8 @@ static hipError_t decode_fast(const DevMat& M, uint8_t* out, int tr0, int tr1, h
 }
 
 bool decode_tiled_ok(const DevMat& M) {
-  return M.K % 32 == 0 && (M.packed || (M.split && M.rows && M.lut && M.max_rows + 2 <= 256));
+  return M.K % 32 == 0 && (M.kqt != KQ_IQ4_XS || M.lut4) &&
+         (M.packed || (M.split && M.rows && M.lut && M.max_rows + 2 <= 256));
 }
 
 hipError_t launch_decode_tiled(const DevMat& M, uint8_t* out, int tr0, int tr1, hipStream_t s) {
@@ -3990,13 +3999,16 @@ hipError_t launch_decode_tiled(const DevMat& M, uint8_t* out, int tr0, int tr1, 
   if (M.packed || tr0 >= tr1) return decode_fast<true>(M, out, tr0, tr1, s);
   const int rows = M.max_rows + 2;
   const size_t sm = (size_t)rows * 128;
-  const void* f = M.symbits == 4 ? reinterpret_cast<const void*>(&k_decode_tiled<4>)
-                                 : reinterpret_cast<const void*>(&k_decode_tiled<8>);
+  const bool grid_bytes = M.kqt == KQ_IQ4_XS;
+  const void* f = M.symbits != 4 ? reinterpret_cast<const void*>(&k_decode_tiled<8, false>)
+                  : grid_bytes   ? reinterpret_cast<const void*>(&k_decode_tiled<4, true>)
+                                 : reinterpret_cast<const void*>(&k_decode_tiled<4, false>);
   hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)sm);
   if (e != hipSuccess) return e;
   const dim3 grid((unsigned)((tr1 - tr0) * M.KT));
-  if (M.symbits == 4) hipLaunchKernelGGL(k_decode_tiled<4>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
-  else hipLaunchKernelGGL(k_decode_tiled<8>, grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  if (M.symbits != 4) hipLaunchKernelGGL((k_decode_tiled<8, false>), grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  else if (grid_bytes) hipLaunchKernelGGL((k_decode_tiled<4, true>), grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
+  else hipLaunchKernelGGL((k_decode_tiled<4, false>), grid, dim3(256), sm, s, M, out, tr0, tr1, rows);
   return hipGetLastError();
 }
 
@@ -4331,6 +4343,156 @@ __global__ void __launch_bounds__(64 * GEMM_WAVES) k_gemm_prefill(DevMat M, cons
   }
 }
 
+// ── prefill GEMM on the matrix cores, Q6_K / IQ4_XS: unscaled grid weights, folded per sub-block ─────────────
+// Y[t][n] = sum over sub-blocks j of d_n s_n,j (x_t . f(q_n)) with f(q) = q - 32 (Q6_K) or kv[q] (IQ4_XS): integers of
+// at most 8 bits, exact in fp16, where the scaled s f(q) (up to 128 x 32 or 32 x 127) is not. Each sub-block's
+// products go to a fresh accumulator tile (x split into fp16 hi + lo, as k_gemm_prefill), folded into the fp32 total
+// with d s_j (exact in fp32) once the sub-block is in. No offsets: neither format has mins.
+// The block, the waves' split of K, the rings and the wave-order LDS sum are those of k_gemm_prefill. A step's K = 16
+// must lie in one sub-block:
+//   IQ4_XS (32-weight sub-blocks) takes k_gemm_prefill's steps (a chunk = a sub-block) over the grid bytes kv[q] + 128
+//   of the tiled codes; weights fp16(1024 + g) from a byte permute against 0x64, minus 1152.
+//   Q6_K (16-weight sub-blocks) takes weights 16 s + 8 h + 0..7 of the chunk in step s for lane (h, c), so that step s
+//   is sub-block 2 kc + s: 8 bytes of the codes piece at lane slot 32 s + c, byte 8 h, and the x piece of step h at
+//   lane slot 32 s + c (the products of a chunk are still each taken once); weights fp16(1024 + q) minus 1056.
+template <int KQ>
+__global__ void __launch_bounds__(64 * GEMM_WAVES) k_gemm_prefill_sub(DevMat M, const uint8_t* __restrict__ CT, int row0,
+                                                                   const uint16_t* __restrict__ XT, int m,
+                                                                   float* __restrict__ Y, int ldy) {
+  static_assert(KQ == KQ_Q6_K || KQ == KQ_IQ4_XS, "per-sub-block folding: Q6_K and IQ4_XS");
+  constexpr bool Q6 = KQ == KQ_Q6_K;
+  constexpr int SB = kq_sbytes(KQ), NSB = kq_symbits(KQ) == 4 ? 2 : 1;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+  const int rp = blockIdx.x, tt = blockIdx.y;
+  const int K = M.K, KC = K / 32, NB = K / 256;
+  const int nA = rp * 64 + c, nB = nA + 32;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(CT + (size_t)rp * 2 * KC * 1024), (short)0, 2 * KC * 1024, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(XT + (size_t)tt * KC * 2048), (short)0, KC * 4096, kBufferRsrcWord3);
+  // the lane's byte offsets of step s's operands in a chunk's codes piece and in its x pieces (hi, then lo 2 KB on)
+  uint32_t vq[2], vx[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    vq[st] = Q6 ? (uint32_t)(32 * st + c) * 16 + 8 * h : (uint32_t)lane * 16;
+    vx[st] = Q6 ? (uint32_t)h * 1024 + (uint32_t)(32 * st + c) * 16 : (uint32_t)st * 1024 + (uint32_t)lane * 16;
+  }
+  // a chunk's codes as 4 words per row tile, words 2 s and 2 s + 1 = the 8 weights of step s
+  auto load_q = [&](int kc, u32x4& qa, u32x4& qb) {
+    if (Q6) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const auto a = __builtin_amdgcn_raw_buffer_load_b64(rc, vq[st], kc * 1024, 0);
+        const auto b = __builtin_amdgcn_raw_buffer_load_b64(rc, vq[st], (KC + kc) * 1024, 0);
+        qa[2 * st] = a[0];
+        qa[2 * st + 1] = a[1];
+        qb[2 * st] = b[0];
+        qb[2 * st + 1] = b[1];
+      }
+    } else {
+      qa = __builtin_amdgcn_raw_buffer_load_b128(rc, vq[0], kc * 1024, 0);
+      qb = __builtin_amdgcn_raw_buffer_load_b128(rc, vq[0], (KC + kc) * 1024, 0);
+    }
+  };
+  auto load_x = [&](int kc, u32x4* x) {  // x[2 half + s]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, vx[i & 1] + (i >> 1) * 2048, kc * 4096, 0);
+  };
+  // 4 weights (bytes of qw) -> fp16 f(q) in two words
+  const h2v bias = Q6 ? h2v{(_Float16)-1056.f, (_Float16)-1056.f} : h2v{(_Float16)-1152.f, (_Float16)-1152.f};
+  auto grid16 = [&](uint32_t qw) -> uint2 {
+    const h2v a = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04010400u));
+    const h2v b = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, qw, 0x04030402u));
+    return make_uint2(__builtin_bit_cast(uint32_t, a + bias), __builtin_bit_cast(uint32_t, b + bias));
+  };
+  // d s_j of sub-block j of a super-block record (words as side_load)
+  auto sub_scale = [&](const uint32_t* w, int j) -> float {
+    if (Q6) return h2f(w[4]) * (float)(int)(int8_t)(uint8_t)(w[j >> 2] >> (8 * (j & 3)));
+    const uint32_t ls = ((w[1] >> (4 * j)) & 15u) | ((w[0] >> (16 + 2 * j)) & 3u) << 4;
+    return h2f(w[0]) * (float)((int)ls - 32);
+  };
+  f16x16 totA = {}, totB = {};
+  uint32_t swa[5] = {}, swb[5] = {};
+  u32x4 qa[4] = {}, qb[4] = {}, xr[4][4] = {};
+  if (wave < NB) {
+    side_load<KQ>(M.side + side_record(row0 + nA, wave, M.KT, NSB) * SB, swa);
+    side_load<KQ>(M.side + side_record(row0 + nB, wave, M.KT, NSB) * SB, swb);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      load_q(wave * 8 + i, qa[i], qb[i]);
+      load_x(wave * 8 + i, xr[i]);
+    }
+  }
+  for (int sb = wave; sb < NB; sb += GEMM_WAVES) {
+    uint32_t wa[5], wb[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      wa[i] = swa[i];
+      wb[i] = swb[i];
+    }
+    const int nsb = sb + GEMM_WAVES;
+    if (nsb < NB) {
+      side_load<KQ>(M.side + side_record(row0 + nA, nsb, M.KT, NSB) * SB, swa);
+      side_load<KQ>(M.side + side_record(row0 + nB, nsb, M.KT, NSB) * SB, swb);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // the super-block's 8 chunks
+      if (j < 5 || nsb < NB) {
+        const int kn = j < 5 ? sb * 8 + j + 3 : nsb * 8 + j - 5;
+        load_q(kn, qa[(j + 3) & 3], qb[(j + 3) & 3]);
+        load_x(kn, xr[(j + 3) & 3]);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads issued here, ahead of this chunk's products
+      const u32x4 ca = qa[j & 3], cb = qb[j & 3];
+      const u32x4* xc = xr[j & 3];
+      f16x16 dA = {}, dB = {};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        if (Q6 && st == 1) {
+          dA = f16x16{};
+          dB = f16x16{};
+        }
+        const uint2 a0 = grid16(ca[2 * st]), a1 = grid16(ca[2 * st + 1]);
+        const uint2 b0 = grid16(cb[2 * st]), b1 = grid16(cb[2 * st + 1]);
+        const h8v wva = __builtin_bit_cast(h8v, make_uint4(a0.x, a0.y, a1.x, a1.y));
+        const h8v wvb = __builtin_bit_cast(h8v, make_uint4(b0.x, b0.y, b1.x, b1.y));
+        const h8v xh = __builtin_bit_cast(h8v, xc[st]), xl = __builtin_bit_cast(h8v, xc[2 + st]);
+        dA = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wva, dA, 0, 0, 0);
+        dB = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, wvb, dB, 0, 0, 0);
+        dA = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, wva, dA, 0, 0, 0);
+        dB = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, wvb, dB, 0, 0, 0);
+        if (Q6 || st == 1) {  // the sub-block is in: fold it
+          const int js = Q6 ? 2 * j + st : j;
+          const float sa = sub_scale(wa, js), sbb = sub_scale(wb, js);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            totA[r] = fmaf(sa, dA[r], totA[r]);
+            totB[r] = fmaf(sbb, dB[r], totB[r]);
+          }
+          // keep the fold here: sunk below the chunk loop's branches it would hold every chunk's tiles live (spills)
+          asm volatile("" : "+v"(totA), "+v"(totB));
+        }
+      }
+    }
+  }
+  __shared__ float part[GEMM_WAVES][2][16][64];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    part[wave][0][r][lane] = totA[r];
+    part[wave][1][r][lane] = totB[r];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 2 * 16 * 64; e += 64 * GEMM_WAVES) {
+    const int half = e >> 10, r = (e >> 6) & 15, l = e & 63;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < GEMM_WAVES; ++w) acc += part[w][half][r][l];
+    const int t = tt * 32 + 8 * (r / 4) + 4 * (l >> 5) + (r % 4);
+    if (t < m) Y[(size_t)t * ldy + row0 + rp * 64 + 32 * half + (l & 31)] = acc;
+  }
+}
+
 // x of the prefill GEMM: fp32 X [m][K] -> XT (fp16 hi = fp16(x), lo = fp16(x - hi)) and SXT (per sub-block of 32
 // weights s = ((a0 + a1) + (a2 + a3)), a_q the in-order fp32 sum of its q-th 8 values, as fp16 hi / lo), tokens
 // padded with zeros to a multiple of 64. Thread = (chunk, q, token c of the tile): the 32 threads of one q write one
@@ -4398,6 +4560,8 @@ hipError_t launch_gemm_prefill(const DevMat& M, const uint8_t* CT, int row0, int
   switch (M.kqt) {
     case KQ_Q4_K: hipLaunchKernelGGL(k_gemm_prefill<KQ_Q4_K>, grid, block, 0, s, M, CT, row0, x, sx, m, Y, ldy); break;
     case KQ_Q5_K: hipLaunchKernelGGL(k_gemm_prefill<KQ_Q5_K>, grid, block, 0, s, M, CT, row0, x, sx, m, Y, ldy); break;
+    case KQ_Q6_K: hipLaunchKernelGGL(k_gemm_prefill_sub<KQ_Q6_K>, grid, block, 0, s, M, CT, row0, x, m, Y, ldy); break;
+    case KQ_IQ4_XS: hipLaunchKernelGGL(k_gemm_prefill_sub<KQ_IQ4_XS>, grid, block, 0, s, M, CT, row0, x, m, Y, ldy); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

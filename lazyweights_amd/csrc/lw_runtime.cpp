@@ -1137,10 +1137,11 @@ int fused_dev(Model& M, Tensor& t, const void* X16, int m, int per, float* Y, in
   return fused_group_dev(M, &tp, &X16, 1, m, per, &Y, &ldy, s);
 }
 
-// Prefill GEMM of path 2: 0 (default) = the hand-written MFMA GEMM with scaled fp16 weights for Q4_K / Q5_K
-// (k_gemm_prefill), rocBLAS for the other formats; 1 = hand-written for every format (Q6_K / IQ4_XS through
-// k_gemm_codes_mfma); 2 / 3 = rocBLAS, always the two-GEMM / the one-GEMM form over fp16 hi + lo weights; 4 = rocBLAS
-// with the one-GEMM form up to g_prefill_one_max tokens, else two GEMMs. Kernel mode 1 keeps the SIMT GEMM.
+// Prefill GEMM of path 2: 0 (default) = the hand-written MFMA GEMM over tiled codes for every K-quant format
+// (k_gemm_prefill: scaled fp16 weights, Q4_K / Q5_K; k_gemm_prefill_sub: grid weights folded per sub-block, Q6_K /
+// IQ4_XS); 1 = the older hand-written GEMM over row-major codes (k_gemm_codes_mfma, every format); 2 / 3 = rocBLAS,
+// always the two-GEMM / the one-GEMM form over fp16 hi + lo weights; 4 = rocBLAS with the one-GEMM form up to
+// g_prefill_one_max tokens, else two GEMMs. Kernel mode 1 keeps the SIMT GEMM.
 int g_prefill = 0;
 
 // Y[:, r0 : r0 + nr] = x . w^T for a chunk of rows through rocBLAS. WW is the column-major nr x 2K matrix [w hi |
@@ -1191,10 +1192,9 @@ int g_prefill_one_max = 512;
 
 // decode into scratch (tile-row chunks) + GEMM with the side bytes (path 2 / m > 8; llmrt.cu:1826-1841)
 int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ldy, hipStream_t s) {
-  const bool scaled_ok = t.kqt == lw::KQ_Q4_K || t.kqt == lw::KQ_Q5_K;
-  const bool own = g_kernel_mode != 1 && (g_prefill == 1 || (g_prefill == 0 && scaled_ok));
-  if (own && scaled_ok && t.K % 256 == 0 && lw::decode_tiled_ok(t.dm)) {
-    // the hand-written GEMM with scaled fp16 weights over tiled codes, x hi + lo and Sx hi + lo
+  const bool kq = t.kqt >= lw::KQ_Q4_K && t.kqt <= lw::KQ_IQ4_XS;
+  if (g_kernel_mode != 1 && g_prefill == 0 && kq && t.K % 256 == 0 && lw::decode_tiled_ok(t.dm)) {
+    // the hand-written GEMM over tiled codes, x hi + lo (and, for the formats with mins, Sx hi + lo)
     const size_t row_bytes = (size_t)lw::TN * t.K;
     const size_t cap = std::max(row_bytes, std::min<size_t>((size_t)t.N * t.K, (size_t)64 << 20));
     if (grow(M.codes, M.codes_cap, cap) || grow(M.X16, M.X16_cap, lw::prefill_x_bytes(m, (int)t.K)) ||
@@ -1209,8 +1209,8 @@ int decode_gemm_dev(Model& M, Tensor& t, const float* X, int m, float* Y, int ld
     }
     return 0;
   }
-  const bool blas = g_kernel_mode != 1 && !own;
-  const bool mfma = g_kernel_mode != 1 && !blas;
+  const bool mfma = g_kernel_mode != 1 && g_prefill == 1;
+  const bool blas = g_kernel_mode != 1 && !mfma;
   if (blas) {
     if (!M.blas && rocblas_create_handle(&M.blas) != rocblas_status_success) {
       M.blas = nullptr;

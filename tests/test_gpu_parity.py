@@ -123,7 +123,8 @@ def test_gpu_decode_gemm_path(fmt_rt, orc, kqt, fmt, H):
 @pytest.mark.parametrize("kqt,fmt,H", FORMATS)
 def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
     """Prefill-shaped path 2 (m = 80: two full 32-token tiles and a partial one) through every prefill GEMM (the
-    hand-written matrix-core GEMMs over the codes, the default for Q4_K / Q5_K; rocBLAS over fp16 hi + lo weights in
+    hand-written matrix-core GEMMs over the codes: the default over tiled codes, k_gemm_prefill for Q4_K / Q5_K and
+    k_gemm_prefill_sub for Q6_K / IQ4_XS, and the older one over row-major codes; rocBLAS over fp16 hi + lo weights in
     its forms) against fp64, and against the SIMT GEMM (kernel mode 1) to fp32 rounding."""
     rt, mats = fmt_rt
     mat = mats[fmt]
@@ -135,8 +136,8 @@ def test_gpu_prefill_gemm_matrix_cores(fmt_rt, orc, kqt, fmt, H):
         Ys = rt.test_matmul(fmt, X, path=2)
     finally:
         rt.lib.lw_set_kernel_mode(0)
-    for which, what in ((0, "default (hand-written for Q4_K / Q5_K)"), (2, "rocBLAS two GEMMs"),
-                        (3, "rocBLAS one GEMM"), (4, "rocBLAS auto"), (1, "hand-written matrix-core GEMM")):
+    for which, what in ((0, "default (hand-written, tiled codes)"), (2, "rocBLAS two GEMMs"),
+                        (3, "rocBLAS one GEMM"), (4, "rocBLAS auto"), (1, "hand-written, row-major codes")):
         say("prefill m=80", fmt, what)
         assert rt.lib.lw_set_prefill_gemm(which) == 0
         try:
@@ -777,8 +778,8 @@ def test_gpu_packed_twin_same_bits(gpu, tmp_path, orc):
             assert np.array_equal(yc, yp), name
             y64 = orc.gemv_f64(orc.dequant(kqt, codes, side), X3.astype(np.float64))
             check_err(yp, y64, name + " packed fp32 m=3")
-            # prefill path: the coded matrix's fused decode + dequant and the packed one's unpack + dequant give the
-            # same fp16 hi + lo weights, so the same GEMM bits
+            # prefill path: the coded matrix's decode and the packed one's unpack give the same tiled codes (IQ4_XS:
+            # grid bytes), so the same GEMM bits
             X12 = np.random.default_rng(kqt + 7).standard_normal((12, K)).astype(np.float32)
             yc, yp = rc.test_matmul(name, X12, path=2), rp.test_matmul(name, X12, path=2)
             assert np.array_equal(yc, yp), name
