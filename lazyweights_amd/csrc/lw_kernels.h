@@ -53,6 +53,11 @@ struct DevMat {
 // [block0, block0 + KT * ceil(NT / WPB)); X2 = its fp16 activations [mt][K] as pairs, P its partials [KT][mt][N]
 // (the exception tiles' partials are written by the whole-tile kernel's pass).
 constexpr int MAX_GROUP = 8;
+// A partials slot between a reduction's read and the next partial's store (a signalling NaN: no arithmetic result
+// is one). Every reduction puts its slots back to this value; a partials buffer starts filled with it.
+constexpr uint32_t kNoPartial = 0x7F80A5A5u;
+// re-reads of a counted partial that is not yet visible before the in-launch reduction gives up (NaN, not a hang)
+constexpr int kPartialSpins = 1 << 16;
 struct GroupEntry {
   DevMat M;
   const uint32_t* X2;
@@ -156,9 +161,11 @@ hipError_t launch_fused_packed(const GroupPlan& plan, hipStream_t s);
 // The packed twin for m = 1 over a flat plan (one tile per wave, W waves per block, every matrix whole; no lists).
 hipError_t launch_fused_packed_flat(const FlatPlan& plan, hipStream_t s);
 
-// Ordered reduction of several matrices in one launch: Y_i[j][n] = sum_tc P_i[tc][jj][n] (as launch_reduce).
+// Ordered reduction of several matrices in one launch: Y_i[j][n] (row stride ldy) = the sum over tile columns tc (in
+// order) of P_i[tc][jj][n], jj over the `per` pseudo-tokens of token j (per = 1: fp16 activations; per = 2: fp32
+// activations split into fp16 hi + lo).
 struct ReduceEntry {
-  const float* P;
+  float* P;  // read, then every slot set back to kNoPartial
   float* Y;
   int N, KT, ldy, out0;  // out0 = first output index of this matrix in the flattened launch (m * N each)
 };
@@ -172,9 +179,6 @@ hipError_t launch_reduce_group(const ReducePlan& plan, hipStream_t s);
 hipError_t launch_fused(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
 // the whole-tile kernel over M.exc[nexc32 .. nexc) (exception tiles without any ring schedule); no-op if none
 hipError_t launch_fused_exceptions(const DevMat& M, const void* X16, int mt, float* P, hipStream_t s);
-// Y[j][n] (row stride ldy) = sum over tile columns tc (in order) of P[tc][jj][n], jj over `per` pseudo-tokens of
-// token j (per = 1: fp16 activations; per = 2: fp32 activations split into fp16 hi + lo).
-hipError_t launch_reduce(const float* P, float* Y, int m, int per, int N, int ldy, int KT, hipStream_t s);
 // fp32 X [m][K] -> fp16 X16 [2m][K] (row 2j = hi, 2j + 1 = lo = x - hi)
 hipError_t launch_split_x(const float* X, void* X16, int m, int K, hipStream_t s);
 // codes [N][K] (one byte per weight) for tile rows [tr0, tr1)

@@ -802,35 +802,61 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 }
 
 // ── flat launches (m = 1): shared pieces ─────────────────────────────────────────────────────────────────
-// Reduction in the launch, after a wave stored its tile's 64 partials (agent-scope atomic stores): it waits for
-// the stores to complete (vmcnt(0)) before lane 0 counts the tile in its tile row with a relaxed agent-scope atomic;
-// the wave that counts the row's last tile resets the counter and sums the row's partials in tile-column order (the
-// order of k_reduce_group, so the bits are the same) with agent-scope atomic loads. This relies on the hardware's
-// completion order (the store acknowledgements precede the increment), not on release / acquire semantics: on
-// gfx950 an agent-scope release is a buffer_wbl2 and an acquire a buffer_inv per wave, which measured 106-143 us per
-// config-2 layer against 45 us. Used only by kernels outside the m = 1 headline path (whose blocks reduce whole tile
-// rows in LDS behind a workgroup barrier). No-op when the entry has no Y (reduced by a separate launch).
-// The sum of tile row tr's partials by the wave that counted the row's last tile (resets the counter).
+// Reduction in the launch. A wave stores its tile's 64 partials (relaxed agent-scope atomic stores), waits for the
+// stores to complete (vmcnt(0)), and lane 0 counts the tile in its tile row with a relaxed agent-scope atomic; the
+// wave that counts the row's last tile resets the counter and sums the row's partials in tile-column order (the order
+// of k_reduce_group, so the bits are the same). No ordering between the partials and the counter is assumed (an
+// agent-scope release / acquire on gfx950 is a buffer_wbl2 / buffer_inv per wave, which measured 106-143 us per
+// config-2 layer against 45 us): a partial slot holds kNoPartial from the end of one reduction to the store of the
+// next partial, so the summing wave takes each slot by an atomic exchange with kNoPartial until what it takes is not
+// kNoPartial (coherence of that one location: it sees the last reduction's kNoPartial, which a launch boundary
+// orders before, or the new partial). The counter only elects the summing wave. No-op when the entry has no Y
+// (reduced by a separate launch, which resets the slots likewise). Slots start as kNoPartial (filled when the
+// partials buffer is allocated).
+
+// The sum over columns c < KT, in order, of the partial slots q + c cs. Each slot is taken by an exchange with
+// kNoPartial, 32 in flight. A slot still holding kNoPartial (its partial counted but not yet visible here) makes the
+// running sum NaN, so one test per batch finds it; the batch is then summed again once every such slot has its
+// partial (at most kPartialSpins re-reads each, a few hundred cycles apiece; past that the sum is NaN rather than a
+// hang). A NaN of the data itself only costs the re-summation: no arithmetic result has kNoPartial's bits.
+__device__ __forceinline__ float sum_partials(uint32_t* q, size_t cs, int KT) {
+  constexpr int B = 32;
+  auto take = [&](int c) {
+    return __hip_atomic_exchange(q + (size_t)c * cs, kNoPartial, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  float a = 0.f;
+  for (int c0 = 0; c0 < KT; c0 += B) {
+    uint32_t v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) v[u] = c0 + u < KT ? take(c0 + u) : 0u;
+    const float a0 = a;
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (c0 + u < KT) a += __builtin_bit_cast(float, v[u]);
+    if (__builtin_expect(a != a, 0)) {
+      a = a0;
+      for (int u = 0; u < B && c0 + u < KT; ++u) {
+        uint32_t w = v[u];
+        for (int i = 0; w == kNoPartial && i < kPartialSpins; ++i) {
+          __builtin_amdgcn_s_sleep(2);
+          w = take(c0 + u);
+        }
+        a += w == kNoPartial ? __builtin_nanf("") : __builtin_bit_cast(float, w);
+      }
+    }
+  }
+  return a;
+}
+// The sums of tile row tr's partials, per token j < mt, by the wave that counted the row's last tile (it also resets
+// the counter). P is [KT][mt][N]: token j's partial of tile column c at P + (c mt + j) N.
 template <class KEntryRef>
 __device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
   if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // P is [KT][mt][N]: token j's partial of tile column c at P + (c mt + j) N
-  for (int j = 0; j < mt; ++j) {
-    const float* pr = E.P + (size_t)j * N + (size_t)tr * TN + (uint32_t)lane;
-    const size_t cs = (size_t)mt * N;
-    float a = 0.f;
-    for (int c0 = 0; c0 < KT; c0 += 16) {
-      float v[16];
-#pragma unroll
-      for (int c = 0; c < 16; ++c)
-        v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * cs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : 0.f;
-#pragma unroll
-      for (int c = 0; c < 16; ++c)
-        if (c0 + c < KT) a += v[c];
-    }
-    E.Y[(size_t)j * (mt > 1 ? E.ldy : 0) + (size_t)tr * TN + (uint32_t)lane] = a;
-  }
+  uint32_t* const q = reinterpret_cast<uint32_t*>(E.P + (size_t)tr * TN + (uint32_t)lane);
+#pragma unroll 1
+  for (int j = 0; j < mt; ++j)
+    E.Y[(size_t)j * (mt > 1 ? E.ldy : 0) + (size_t)tr * TN + (uint32_t)lane] =
+        sum_partials(q + (size_t)j * N, (size_t)mt * N, KT);
 }
 
 template <class KEntryRef>
@@ -1767,6 +1793,12 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     if (old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
     pend = -1;
   };
+  // Wave priority 3 - (tiles taken after the first), at least 0. Among waves of equal priority a SIMD favours the
+  // oldest (lowest index), so the block's last waves, whose first copies are paced behind the others', would run
+  // slowest and end the launch alone; waves that have decoded fewer tiles go first instead, and the waves end closer
+  // together (config 2: 39.6 against 40.3 us per layer).
+  int tdone = 0;
+  __builtin_amdgcn_s_setprio(3);
   int n = wave;
   bool have = n < per && T0 + n < plan.ntiles;
   int sec = 0, t = 0, ncopy = 0;
@@ -1960,6 +1992,10 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
       copy_tile(sec ? eb : ea, t);
+      ++tdone;  // the wave's priority falls with the tiles it has taken
+      if (tdone == 1) __builtin_amdgcn_s_setprio(2);
+      else if (tdone == 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
     }
     // the row partial in tile_gemv's order (tile_gemv_i8's for int8 activations)
     float tot = 0.f;
@@ -2052,19 +2088,8 @@ template <class KEntryRef>
 __device__ __forceinline__ void row_sum_half(const KEntryRef& E, int tr, int f, int KT, int N, int lane) {
   if (lane == 0) __hip_atomic_store(E.cnt + 2 * tr + f, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (lane >= 32) return;
-  const float* pr = E.P + (size_t)tr * TN + (uint32_t)(32 * f + lane);
-  float a = 0.f;
-  for (int c0 = 0; c0 < KT; c0 += 16) {
-    float v[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      v[c] = c0 + c < KT ? __hip_atomic_load(pr + (size_t)(c0 + c) * N, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                         : 0.f;
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c0 + c < KT) a += v[c];
-  }
-  E.Y[(size_t)tr * TN + (uint32_t)(32 * f + lane)] = a;
+  E.Y[(size_t)tr * TN + (uint32_t)(32 * f + lane)] =
+      sum_partials(reinterpret_cast<uint32_t*>(E.P + (size_t)tr * TN + (uint32_t)(32 * f + lane)), (size_t)N, KT);
 }
 
 template <int KQ>
@@ -3646,6 +3671,7 @@ __global__ void k_reduce_group(ReducePlan plan) {
   const uint32_t o0 = (uint32_t)(j * PER * E.N + n), step = (uint32_t)(plan.m * PER * E.N);
   // partials summed in tile-column order (a column's pseudo-tokens in order), the loads of up to 32 / PER columns
   // in flight
+  // (the partials are a previous launch's, complete; their slots go back to kNoPartial for the in-launch reductions)
   constexpr int B = 32 / PER;
   float a = 0.f;
   for (int tc = 0; tc < E.KT; tc += B) {
@@ -3659,7 +3685,10 @@ __global__ void k_reduce_group(ReducePlan plan) {
     for (int u = 0; u < B; ++u)
       if (tc + u < E.KT)
 #pragma unroll
-        for (int q = 0; q < PER; ++q) a += v[u][q];
+        for (int q = 0; q < PER; ++q) {
+          a += v[u][q];
+          reinterpret_cast<uint32_t*>(E.P)[o0 + (uint32_t)(tc + u) * step + (uint32_t)(q * E.N)] = kNoPartial;
+        }
   }
   E.Y[(size_t)j * E.ldy + n] = a;
 }
@@ -3668,22 +3697,6 @@ hipError_t launch_reduce_group(const ReducePlan& p, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.total < 1 || p.per < 1 || p.per > 2) return hipErrorInvalidValue;
   if (p.per == 1) hipLaunchKernelGGL(k_reduce_group<1>, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
   else hipLaunchKernelGGL(k_reduce_group<2>, dim3((p.total + 255) / 256), dim3(256), 0, s, p);
-  return hipGetLastError();
-}
-
-// ── ordered reduction over tile columns ──────────────────────────────────────────────────────────────────
-__global__ void k_reduce(const float* __restrict__ P, float* __restrict__ Y, int m, int per, int N, int ldy, int KT) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= m * N) return;
-  const int j = i / N, n = i - j * N, mt = m * per;
-  float a = 0.f;
-  for (int tc = 0; tc < KT; ++tc)
-    for (int q = 0; q < per; ++q) a += P[((size_t)tc * mt + j * per + q) * N + n];
-  Y[(size_t)j * ldy + n] = a;
-}
-
-hipError_t launch_reduce(const float* P, float* Y, int m, int per, int N, int ldy, int KT, hipStream_t s) {
-  hipLaunchKernelGGL(k_reduce, dim3((m * N + 255) / 256), dim3(256), 0, s, P, Y, m, per, N, ldy, KT);
   return hipGetLastError();
 }
 

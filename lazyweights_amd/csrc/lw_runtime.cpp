@@ -666,7 +666,8 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   std::vector<size_t> coff(count + 1, 0);  // tile-row counters per entry (in-launch reduction)
   for (int i = 0; i < count; ++i) coff[i + 1] = coff[i] + 2 * (size_t)ts[i]->dm.NT;  // per tile row and half
   // partials and counters: the model's (grown on demand) or a caller's fixed scratch (nothing allocated; its counters
-  // are cleared by a fill kernel on the stream, since the last call on that scratch may have left anything there)
+  // and partial slots are set by fill kernels on the stream, since the last call on that scratch may have left
+  // anything there). Partial slots hold kNoPartial outside a reduction (lw_kernels.h).
   // 2..8 tokens of fp16 activations, every format: the whole-tile kernel with its products on the matrix cores
   auto mma_ok = [&](const lw::DevMat& dm) {
     return dm.kqt >= lw::KQ_Q4_K && dm.kqt <= lw::KQ_IQ4_XS && !dm.packed && dm.dsplit && dm.lut4 && dm.rows &&
@@ -721,8 +722,12 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     Cb = reinterpret_cast<uint32_t*>(fixed->base);
     Pb = reinterpret_cast<float*>(fixed->base + cnt_bytes);
     HIPCHECK(lw::launch_fill_u32(Cb, coff[count], 0u, s));
+    HIPCHECK(lw::launch_fill_u32(reinterpret_cast<uint32_t*>(Pb), off[count], lw::kNoPartial, s));
   } else {
+    const size_t cap0 = M.P_cap;
     if (grow(M.P, M.P_cap, off[count] * sizeof(float))) return -1;
+    if (M.P_cap != cap0)  // a new buffer: every slot empty (the reductions keep them so)
+      HIPCHECK(lw::launch_fill_u32(reinterpret_cast<uint32_t*>(M.P), M.P_cap / sizeof(uint32_t), lw::kNoPartial, s));
     if (grow_zeroed(M.cnt, M.cnt_cap, coff[count] * sizeof(uint32_t))) return -1;
     Pb = M.P;
     Cb = M.cnt;

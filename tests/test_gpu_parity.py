@@ -187,6 +187,45 @@ def test_gpu_fused_fp16_x_device(fmt_rt, orc, kqt, fmt, H):
         check_err(Y.cpu().numpy(), y64[:m], "%s fp16 m=%d" % (fmt, m))
 
 
+@pytest.mark.parametrize("kqt,fmt,H", FORMATS)
+def test_gpu_reduction_with_nan_activations(fmt_rt, orc, kqt, fmt, H):
+    """The in-launch reduction takes each partial slot by an exchange with an empty marker (a signalling NaN) and
+    re-sums a batch whose sum is NaN. A NaN in the activations makes every partial of its token NaN: that token's
+    outputs are NaN, the other tokens' outputs stay exact (m = 5, the matrix-core kernel), nothing waits, and the
+    slots are left empty, so the next calls (m = 1 and m = 5) are again within tolerance of fp64."""
+    import torch
+    rt, mats = fmt_rt
+    mat = mats[fmt]
+    N, K = mat[2], mat[3]
+    g = torch.Generator().manual_seed(70 + kqt)
+    X = torch.randn(5, K, generator=g).half()
+    _, y64 = reference_y(orc, mat, X.double().numpy())
+    st = torch.cuda.current_stream().cuda_stream
+    Xn = X.clone()
+    Xn[2, K // 3] = float("nan")
+    Xn_d = Xn.cuda()
+    for m, bad in ((1, None), (5, 2)):
+        say("nan activations", fmt, "m", m)
+        xin = Xn_d[:m].clone()
+        if m == 1:
+            xin[0, 7] = float("nan")
+        Y = torch.zeros((m, N), dtype=torch.float32, device="cuda")
+        rt.matmul_dev(fmt, xin, Y, x_f16=True, stream=st)
+        torch.cuda.synchronize()
+        y = Y.cpu().numpy()
+        if m == 1:
+            assert np.isnan(y).all(), fmt
+        else:
+            assert np.isnan(y[bad]).all(), fmt
+            ok = [j for j in range(m) if j != bad]
+            check_err(y[ok], y64[ok], "%s m=5 beside a NaN token" % fmt)
+    for m in (1, 5):
+        Y = torch.zeros((m, N), dtype=torch.float32, device="cuda")
+        rt.matmul_dev(fmt, X[:m].cuda(), Y, x_f16=True, stream=st)
+        torch.cuda.synchronize()
+        check_err(Y.cpu().numpy(), y64[:m], "%s m=%d after the NaN calls" % (fmt, m))
+
+
 def test_gpu_verify_gemm_equals_repeated_gemv(fmt_rt, orc):
     """One m = 5 launch (products on the matrix cores, sub-block scales folded into the weights: the same products
     summed in another order) against five m = 1 launches (v_dot2): the same values up to the fp32 rounding of a
