@@ -104,6 +104,9 @@ struct FlatPlan {
   int i8;  // 1: int8 activations (the entries' XQ / DX / SX)
   int mt;  // tokens: 0 or 1, or 2..8 with int8 activations (the flat ring and low-latency kernels, one pass)
   int canon;  // 1: the whole-tile kernel (fp16 activations) looks codes up by the comparator form (DevMat::canon)
+  // the whole-tile kernel (fp16 activations) over two K-quant types: entries [0, nfa) of one, [nfa, n) of the other;
+  // nfa = n (or 0) when every entry has the first entry's type
+  int nfa;
 };
 hipError_t launch_fused_flat(const FlatPlan& plan, hipStream_t s);
 // waves of the flat kernel one CU holds at once (its register use) for int8 activations, mt tokens (1, or 2..8)
@@ -129,7 +132,8 @@ hipError_t launch_quant_x8_group(const QuantJobs& q, hipStream_t s);
 int split_stage_rows(const FlatPlan& plan);
 // whole-tile kernel for flat launches (m = 1): block = plan.W waves over `per` consecutive tiles (>= W), a tile per
 // wave in LDS at a time (tiles_buf_rows rows), 8 chains per lane; every tile of the entries (exceptions included)
-// and the in-launch reduction for entries with Y
+// and the in-launch reduction for entries with Y. With fp16 activations the entries may hold two K-quant types
+// (FlatPlan::nfa: the first nfa entries of the smaller type code, the rest of the larger), one launch for both.
 hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
 // the most waves of a whole-tile block with the comparator lookup (FlatPlan::canon)
 constexpr int TILES_CANON_WAVES = 12;

@@ -1687,17 +1687,13 @@ constexpr int TILES_COPIES = LW_TILES_COPIES;
 // CANON (kernel mode 9, fp16 activations): codes are looked up by the comparator (canon_addr) in a 256-entry table
 // of entries in canonical order instead of the 2048-entry table; the same entries, so the same bits. Its blocks have
 // at most TILES_CANON_WAVES waves (3 per SIMD): the comparator's registers spill at 4.
-template <int KQ, int NTAB, bool I8, bool CANON = false>
+template <int V>
+struct KqTag {
+  static constexpr int value = V;
+};
+template <int KQA, int NTAB, bool I8, bool CANON = false, int KQB = KQA>
 __global__ void __launch_bounds__(CANON ? 64 * TILES_CANON_WAVES : 1024, 1)
 k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
-  constexpr int SYMB = kq_symbits(KQ);
-  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
-  constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
-  constexpr int NSUBT = TW / GW;                          // sub-blocks per tile row
-  constexpr int NSB = TW / 256;                           // super-blocks per tile row
-  constexpr int NSUB = 256 / GW;                          // sub-blocks per super-block
-  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
-  constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
   constexpr int NC = 8;                                   // chains per lane (32 symbols each)
   constexpr int NG = 16 / NC;                             // 16-symbol groups per chain
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
@@ -1825,240 +1821,258 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   }
 #pragma unroll 1
   while (have) {
-    const int cur = sec;
-    const bool second = sec != 0;
-    KEntry* ep = second ? eb : ea;
-    const auto& E = *ep;
-    const auto& M = E.M;
-    const int KT = M.KT, N = M.N;
-    const int tc = t % KT, tr = t / KT;
-    // side records, x sums and chain starts while the copy is in flight
-    const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
-    uint32_t sw[NSB][5];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
-    XgRegs xgr;
-    if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
-    uint32_t P[NC];
-    tile_chain_starts(M, t, f, s, P);
-    const uint32_t tsel = second ? 4u * LUTN : 0u;
-    uint32_t clim[10], cpk[11];  // the comparator's limits and length words (CANON), the table's place added
-    if (CANON) {
-      KU32* cz = (KU32*)M.canon;
-#pragma unroll
-      for (int k = 0; k < 10; ++k) clim[k] = cz[k];
-#pragma unroll
-      for (int k = 0; k < 11; ++k) cpk[k] = cz[10 + k] + (tsel << 16);
-      // values in SGPRs (not a per-lane indexed load of the table words)
-#pragma unroll
-      for (int k = 0; k < 10; ++k) asm volatile("" : "+s"(clim[k]));
-#pragma unroll
-      for (int k = 0; k < 11; ++k) asm volatile("" : "+s"(cpk[k]));
-    }
-    // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
-    // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
-    // used through DPP broadcasts), int8 x as dwords l, l + 64, .. read back with v_readlane
-    constexpr int XV = I8 ? TW / 4 / 64 : 1, XR = I8 ? 1 : TW / 2 / 16;
-    uint32_t xv[XV], xr[XR];
-    if (I8) {
-      const uint32_t* xs = reinterpret_cast<const uint32_t*>(E.XQ) + (size_t)tc * (TW / 4);
-#pragma unroll
-      for (int k = 0; k < XV; ++k) xv[k] = xs[64 * k + lane];
-    } else {
-      const uint32_t* xs = E.X2 + (size_t)tc * (TW / 2) + (lane & 15);
-#pragma unroll
-      for (int m = 0; m < XR; ++m) xr[m] = xs[16 * m];
-    }
-    auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
-    if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (pend >= 0 && lane == 0)
-      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // register windows: rows r, r + 1 (A, B) of each chain, row r + 2 (C) read after every pair (P = bit
-    // position + 64: bits 5+ give the row C holds)
-    uint32_t slot[NC], A[NC], B[NC], C[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
-      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
-      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
-      C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
-    }
-    float sub[NSUBT];
-    float acc[NC];
-    int iacc[NC];
-    uint32_t wprev[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      acc[j] = 0.f;
-      iacc[j] = 0;
-      wprev[j] = 0;
-    }
-    // one pair of symbols of every chain (group gi, pair p), then the end of a 16-symbol group
-    auto pair_step = [&](const int gi, const int p) __attribute__((always_inline)) {
-        // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
-        // (the reads return in order: a chain waits only for its own)
-        // (scheduling barriers keep the stages apart, so every chain's read is issued before the first result is
-        // waited for; bits >= 16 of P carry table-entry payload and are ignored)
-        uint32_t w1[NC], e1[NC], e2[NC];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
-          e1[j] = *(LdsU32*)(CANON ? canon_addr(w1[j], clim, cpk) : table_addr(w1[j], tsel, tmask));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const uint32_t w2 = w1[j] >> (e1[j] & 31u);
-          e2[j] = *(LdsU32*)(CANON ? canon_addr(w2, clim, cpk) : table_addr(w2, tsel, tmask));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          P[j] = P[j] + e1[j] + e2[j];
-          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
-          const bool slide = nslot != slot[j];  // a pair advances at most 22 bits: at most one row
-          A[j] = slide ? B[j] : A[j];
-          B[j] = slide ? C[j] : B[j];
-          slot[j] = nslot;
-          C[j] = *(LdsU32*)(rlb + (nslot << 7));
-        }
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          const int g = NG * j + gi;  // 16-symbol group within the row
-          if (I8) {  // as tile_gemv_i8
-            if (SYMB == 4) {
-              iacc[j] = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u),
-                                               (int)xw(8 * g + p), iacc[j], false);
+    // one tile of format KQ (KQB: a tile of the plan's entries from nfa on)
+    auto tile = [&](auto kq) __attribute__((always_inline)) {
+      constexpr int KQ = decltype(kq)::value;
+      constexpr int SYMB = kq_symbits(KQ);
+      constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+      constexpr int GW = kq_gw(KQ), SB = kq_sbytes(KQ);
+      constexpr int NSUBT = TW / GW;                          // sub-blocks per tile row
+      constexpr int NSB = TW / 256;                           // super-blocks per tile row
+      constexpr int NSUB = 256 / GW;                          // sub-blocks per super-block
+      constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block (2 for Q5_K, else 1)
+      constexpr float VSCALE = SYMB == 4 ? 16777216.f : 1.f;
+      const int cur = sec;
+      const bool second = sec != 0;
+      KEntry* ep = second ? eb : ea;
+      const auto& E = *ep;
+      const auto& M = E.M;
+      const int KT = M.KT, N = M.N;
+      const int tc = t % KT, tr = t / KT;
+      // side records, x sums and chain starts while the copy is in flight
+      const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+      uint32_t sw[NSB][5];
+  #pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+      XgRegs xgr;
+      if (!I8) xgr = column_xsums<KQ>(E.X2, tc, lane);
+      uint32_t P[NC];
+      tile_chain_starts(M, t, f, s, P);
+      const uint32_t tsel = second ? 4u * LUTN : 0u;
+      uint32_t clim[10], cpk[11];  // the comparator's limits and length words (CANON), the table's place added
+      if (CANON) {
+        KU32* cz = (KU32*)M.canon;
+  #pragma unroll
+        for (int k = 0; k < 10; ++k) clim[k] = cz[k];
+  #pragma unroll
+        for (int k = 0; k < 11; ++k) cpk[k] = cz[10 + k] + (tsel << 16);
+        // values in SGPRs (not a per-lane indexed load of the table words)
+  #pragma unroll
+        for (int k = 0; k < 10; ++k) asm volatile("" : "+s"(clim[k]));
+  #pragma unroll
+        for (int k = 0; k < 11; ++k) asm volatile("" : "+s"(cpk[k]));
+      }
+      // the tile column's activations in VGPRs, no scalar loads inside the decode loop (whose waits would drain every
+      // chain's LDS reads): fp16 x as 16-dword rows repeated in each 16-lane row (xr[m] lane l = dword 16 m + l % 16,
+      // used through DPP broadcasts), int8 x as dwords l, l + 64, .. read back with v_readlane
+      constexpr int XV = I8 ? TW / 4 / 64 : 1, XR = I8 ? 1 : TW / 2 / 16;
+      uint32_t xv[XV], xr[XR];
+      if (I8) {
+        const uint32_t* xs = reinterpret_cast<const uint32_t*>(E.XQ) + (size_t)tc * (TW / 4);
+  #pragma unroll
+        for (int k = 0; k < XV; ++k) xv[k] = xs[64 * k + lane];
+      } else {
+        const uint32_t* xs = E.X2 + (size_t)tc * (TW / 2) + (lane & 15);
+  #pragma unroll
+        for (int m = 0; m < XR; ++m) xr[m] = xs[16 * m];
+      }
+      auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
+      if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (pend >= 0 && lane == 0)
+        pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // register windows: rows r, r + 1 (A, B) of each chain, row r + 2 (C) read after every pair (P = bit
+      // position + 64: bits 5+ give the row C holds)
+      uint32_t slot[NC], A[NC], B[NC], C[NC];
+  #pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+        A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+        B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+        C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+      }
+      float sub[NSUBT];
+      float acc[NC];
+      int iacc[NC];
+      uint32_t wprev[NC];
+  #pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        acc[j] = 0.f;
+        iacc[j] = 0;
+        wprev[j] = 0;
+      }
+      // one pair of symbols of every chain (group gi, pair p), then the end of a 16-symbol group
+      auto pair_step = [&](const int gi, const int p) __attribute__((always_inline)) {
+          // each step of the pair decode for all chains before the next step, so the chains' LDS round trips overlap
+          // (the reads return in order: a chain waits only for its own)
+          // (scheduling barriers keep the stages apart, so every chain's read is issued before the first result is
+          // waited for; bits >= 16 of P carry table-entry payload and are ignored)
+          uint32_t w1[NC], e1[NC], e2[NC];
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
+            e1[j] = *(LdsU32*)(CANON ? canon_addr(w1[j], clim, cpk) : table_addr(w1[j], tsel, tmask));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            const uint32_t w2 = w1[j] >> (e1[j] & 31u);
+            e2[j] = *(LdsU32*)(CANON ? canon_addr(w2, clim, cpk) : table_addr(w2, tsel, tmask));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            P[j] = P[j] + e1[j] + e2[j];
+            const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+            const bool slide = nslot != slot[j];  // a pair advances at most 22 bits: at most one row
+            A[j] = slide ? B[j] : A[j];
+            B[j] = slide ? C[j] : B[j];
+            slot[j] = nslot;
+            C[j] = *(LdsU32*)(rlb + (nslot << 7));
+          }
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            const int g = NG * j + gi;  // 16-symbol group within the row
+            if (I8) {  // as tile_gemv_i8
+              if (SYMB == 4) {
+                iacc[j] = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u),
+                                                 (int)xw(8 * g + p), iacc[j], false);
+              } else {
+                const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e1[j], 0x0C0C0602u);
+                if (p & 1) iacc[j] = __builtin_amdgcn_sdot4((int)(wprev[j] | (v2 << 16)), (int)xw(4 * g + p / 2), iacc[j], false);
+                else wprev[j] = v2;
+              }
+            } else if (SYMB == 4) {
+              const uint32_t v1 = __builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u);
+              const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u);
+              const int c = 16 * g + 2 * p;
+              dot2_row(acc[j], xr[c >> 4], c & 15, v1);
+              dot2_row(acc[j], xr[(c + 1) >> 4], (c + 1) & 15, v2);
             } else {
-              const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e1[j], 0x0C0C0602u);
-              if (p & 1) iacc[j] = __builtin_amdgcn_sdot4((int)(wprev[j] | (v2 << 16)), (int)xw(4 * g + p / 2), iacc[j], false);
-              else wprev[j] = v2;
+              const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
+              const int c = 8 * g + p;
+              dot2_row(acc[j], xr[c >> 4], c & 15, v);
             }
-          } else if (SYMB == 4) {
-            const uint32_t v1 = __builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u);
-            const uint32_t v2 = __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u);
-            const int c = 16 * g + 2 * p;
-            dot2_row(acc[j], xr[c >> 4], c & 15, v1);
-            dot2_row(acc[j], xr[(c + 1) >> 4], (c + 1) & 15, v2);
-          } else {
-            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
-            const int c = 8 * g + p;
-            dot2_row(acc[j], xr[c >> 4], c & 15, v);
+          }
+      };
+      auto group_end = [&](const int gi) __attribute__((always_inline)) {
+        if (GPSUB == 1 || (gi & 1)) {
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            sub[(NG * j + gi) / GPSUB] = I8 ? (float)iacc[j] : acc[j];  // |iacc| < 2^24: exact
+            acc[j] = 0.f;
+            iacc[j] = 0;
           }
         }
-    };
-    auto group_end = [&](const int gi) __attribute__((always_inline)) {
-      if (GPSUB == 1 || (gi & 1)) {
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          sub[(NG * j + gi) / GPSUB] = I8 ? (float)iacc[j] : acc[j];  // |iacc| < 2^24: exact
-          acc[j] = 0.f;
-          iacc[j] = 0;
+      };
+      if constexpr (CANON) {  // (the comparator's steps are past the unroller's size limit)
+        static_for<NG>([&](auto gi) {
+          static_for<8>([&](auto p) { pair_step(gi, p); });
+          group_end(gi);
+        });
+      } else {
+  #pragma unroll
+        for (int gi = 0; gi < NG; ++gi) {
+  #pragma unroll
+          for (int p = 0; p < 8; ++p) pair_step(gi, p);
+          group_end(gi);
         }
       }
-    };
-    if constexpr (CANON) {  // (the comparator's steps are past the unroller's size limit)
-      static_for<NG>([&](auto gi) {
-        static_for<8>([&](auto p) { pair_step(gi, p); });
-        group_end(gi);
-      });
-    } else {
-#pragma unroll
-      for (int gi = 0; gi < NG; ++gi) {
-#pragma unroll
-        for (int p = 0; p < 8; ++p) pair_step(gi, p);
-        group_end(gi);
-      }
-    }
 
-    // the sub-block sums are formed here, not sunk past the claim and the copy below (the int8 products would be,
-    // holding every table entry of the tile in scratch)
-#pragma unroll
-    for (int k = 0; k < NSUBT; ++k) asm volatile("" : "+v"(sub[k]));
-    // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
-    // so the buffer is free); the pending row first
-    {
-      uint32_t nx = 0;
-      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      n = __builtin_amdgcn_readfirstlane((int)nx);
-    }
-    // the pending row's counter value (arrived during the decode)
-    const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
-    have = n < per && T0 + n < plan.ntiles;
-    if (have) {
-      tile_of(n, sec, t);
-      uint32_t k = 0;
-      if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
-      copy_tile(sec ? eb : ea, t);
-      ++tdone;  // the wave's priority falls with the tiles it has taken
-      if (tdone == 1) __builtin_amdgcn_s_setprio(2);
-      else if (tdone == 2) __builtin_amdgcn_s_setprio(1);
-      else __builtin_amdgcn_s_setprio(0);
-    }
-    // the row partial in tile_gemv's order (tile_gemv_i8's for int8 activations)
-    float tot = 0.f;
-    if (I8) {
-      KF32* dx = (KF32*)(E.DX + (size_t)tc * (TW / 32));
-      KF32* sx = (KF32*)(E.SX + (size_t)tc * (TW / 32));
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        float dA, dB, mf[8];
-        uint64_t scq, scq2;
-        side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
-        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
-#pragma unroll
-        for (int jj = 0; jj < NSUB; ++jj) {
-          if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
-          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
-                                                               : (float)(uint32_t)(scq & 255u);
-          scq >>= 8;
-          const int xb = (sb * 256 + jj * GW) / 32;
-          tot = fmaf(dA * scv * dx[xb], sub[sb * NSUB + jj], tot);
-          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+      // the sub-block sums are formed here, not sunk past the claim and the copy below (the int8 products would be,
+      // holding every table entry of the tile in scratch)
+  #pragma unroll
+      for (int k = 0; k < NSUBT; ++k) asm volatile("" : "+v"(sub[k]));
+      // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
+      // so the buffer is free); the pending row first
+      {
+        uint32_t nx = 0;
+        if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        n = __builtin_amdgcn_readfirstlane((int)nx);
+      }
+      // the pending row's counter value (arrived during the decode)
+      const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
+      have = n < per && T0 + n < plan.ntiles;
+      if (have) {
+        tile_of(n, sec, t);
+        uint32_t k = 0;
+        if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
+        copy_tile(sec ? eb : ea, t);
+        ++tdone;  // the wave's priority falls with the tiles it has taken
+        if (tdone == 1) __builtin_amdgcn_s_setprio(2);
+        else if (tdone == 2) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
+      // the row partial in tile_gemv's order (tile_gemv_i8's for int8 activations)
+      float tot = 0.f;
+      if (I8) {
+        KF32* dx = (KF32*)(E.DX + (size_t)tc * (TW / 32));
+        KF32* sx = (KF32*)(E.SX + (size_t)tc * (TW / 32));
+  #pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          float dA, dB, mf[8];
+          uint64_t scq, scq2;
+          side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) side_mins(sw[sb], mf);
+  #pragma unroll
+          for (int jj = 0; jj < NSUB; ++jj) {
+            if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+            const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                                 : (float)(uint32_t)(scq & 255u);
+            scq >>= 8;
+            const int xb = (sb * 256 + jj * GW) / 32;
+            tot = fmaf(dA * scv * dx[xb], sub[sb * NSUB + jj], tot);
+            if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) tot = fmaf(-(dB * mf[jj]), sx[xb], tot);
+          }
+        }
+      } else {
+  #pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          float dA, dB;
+          uint64_t scq, scq2;
+          side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
+          if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
+            float mf[8], msum = 0.f;
+            side_mins(sw[sb], mf);
+  #pragma unroll
+            for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xgr(sb, jj, 0), msum);
+            tot = fmaf(-dB, msum, tot);
+          }
+          if (KQ == KQ_IQ4_XS) {
+            float csum = 0.f;
+  #pragma unroll
+            for (int jj = 0; jj < NSUB; ++jj) csum = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgr(sb, jj, 0), csum);
+            tot = fmaf(-128.f * dA, csum, tot);
+          }
+          float tsum = 0.f;
+  #pragma unroll
+          for (int jj = 0; jj < NSUB; ++jj) {
+            if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
+            const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
+                                                                 : (float)(uint32_t)(scq & 255u);
+            scq >>= 8;
+            tsum = fmaf(scv, sub[sb * NSUB + jj], tsum);
+          }
+          tot = fmaf(dA * VSCALE, tsum, tot);
         }
       }
+      float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
+      __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
+      pend = -1;
+      if (E.Y) {
+        pend = cur;
+        ptr = tr;
+        pKT = KT;
+        pN = N;
+      }
+    };
+    if constexpr (KQB != KQA) {
+      if (__builtin_amdgcn_readfirstlane((sec ? mb : ma) >= plan.nfa ? 1 : 0)) tile(KqTag<KQB>{});
+      else tile(KqTag<KQA>{});
     } else {
-#pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        float dA, dB;
-        uint64_t scq, scq2;
-        side_packed<KQ>(sw[sb], scq, scq2, dA, dB);
-        if (KQ == KQ_Q4_K || KQ == KQ_Q5_K) {
-          float mf[8], msum = 0.f;
-          side_mins(sw[sb], mf);
-#pragma unroll
-          for (int jj = 0; jj < NSUB; ++jj) msum = fmaf(mf[jj], xgr(sb, jj, 0), msum);
-          tot = fmaf(-dB, msum, tot);
-        }
-        if (KQ == KQ_IQ4_XS) {
-          float csum = 0.f;
-#pragma unroll
-          for (int jj = 0; jj < NSUB; ++jj) csum = fmaf((float)(int)(int8_t)(uint8_t)(scq >> (8 * jj)), xgr(sb, jj, 0), csum);
-          tot = fmaf(-128.f * dA, csum, tot);
-        }
-        float tsum = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < NSUB; ++jj) {
-          if (KQ == KQ_Q6_K && jj == 8) scq = scq2;
-          const float scv = (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)scq
-                                                               : (float)(uint32_t)(scq & 255u);
-          scq >>= 8;
-          tsum = fmaf(scv, sub[sb * NSUB + jj], tsum);
-        }
-        tot = fmaf(dA * VSCALE, tsum, tot);
-      }
-    }
-    float* out = E.P + (size_t)tc * N + (size_t)tr * TN + (uint32_t)lane;
-    __hip_atomic_store(out, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
-    pend = -1;
-    if (E.Y) {
-      pend = cur;
-      ptr = tr;
-      pKT = KT;
-      pN = N;
+      tile(KqTag<KQA>{});
     }
   }
   if (pend >= 0) {  // the last tile's reduction
@@ -3307,15 +3321,29 @@ static hipError_t tiles_mma8_launch(const FlatPlan& p, int per, int buf_rows, hi
   return one ? tiles_mma8_launch_t<KQ, 1, 8>(p, per, buf_rows, s) : tiles_mma8_launch_t<KQ, 2, 8>(p, per, buf_rows, s);
 }
 
-template <int KQ, int NTAB, bool I8, bool CANON = false>
+template <int KQ, int NTAB, bool I8, bool CANON = false, int KQB = KQ>
 static hipError_t tiles_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8, CANON>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles<KQ, NTAB, I8, CANON, KQB>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + per - 1) / per;
-  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8, CANON>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
+  hipLaunchKernelGGL((k_fused_tiles<KQ, NTAB, I8, CANON, KQB>), dim3(blocks), dim3(p.W * 64), smem, s, p, per,
+                     buf_rows);
   return hipGetLastError();
+}
+
+// two K-quant types in one launch (fp16 activations): entries [0, nfa) of type KQA < KQB, the rest of KQB
+static hipError_t tiles_launch_mixed(int kqa, int kqb, const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  switch (kqa * 8 + kqb) {
+    case KQ_Q4_K * 8 + KQ_Q5_K: return tiles_launch_t<KQ_Q4_K, 2, false, false, KQ_Q5_K>(p, per, buf_rows, s);
+    case KQ_Q4_K * 8 + KQ_Q6_K: return tiles_launch_t<KQ_Q4_K, 2, false, false, KQ_Q6_K>(p, per, buf_rows, s);
+    case KQ_Q4_K * 8 + KQ_IQ4_XS: return tiles_launch_t<KQ_Q4_K, 2, false, false, KQ_IQ4_XS>(p, per, buf_rows, s);
+    case KQ_Q5_K * 8 + KQ_Q6_K: return tiles_launch_t<KQ_Q5_K, 2, false, false, KQ_Q6_K>(p, per, buf_rows, s);
+    case KQ_Q5_K * 8 + KQ_IQ4_XS: return tiles_launch_t<KQ_Q5_K, 2, false, false, KQ_IQ4_XS>(p, per, buf_rows, s);
+    case KQ_Q6_K * 8 + KQ_IQ4_XS: return tiles_launch_t<KQ_Q6_K, 2, false, false, KQ_IQ4_XS>(p, per, buf_rows, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int KQ>
@@ -3339,12 +3367,15 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
   if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || p.W > (p.canon ? TILES_CANON_WAVES : 16) || per < p.W ||
       p.ntiles < 1 || p.mt > 1)
     return hipErrorInvalidValue;
-  const int kqt = p.e[0].M.kqt;
+  // two K-quant types: entries [0, nfa) of the first (the smaller type code), the rest of the second
+  const bool mixed = p.nfa > 0 && p.nfa < p.n;
+  const int kqt = p.e[0].M.kqt, kqb = mixed ? p.e[p.nfa].M.kqt : kqt;
+  if (mixed && (p.i8 || p.canon || kqb <= kqt)) return hipErrorInvalidValue;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
     // a block (`per` consecutive tiles) spans at most two matrices
-    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
+    if (e.M.kqt != (mixed && i >= p.nfa ? kqb : kqt) || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || (!e.list && e.ntile != e.M.NT * e.M.KT) ||
         (i == 0 && e.tile0 != 0) || (p.i8 && (!e.M.luti8 || !e.XQ || !e.DX || !e.SX)) ||
         (p.canon && (p.i8 || !e.M.canon)))
@@ -3352,6 +3383,7 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
   }
   const int rows = tiles_buf_rows(p);
   if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  if (mixed) return tiles_launch_mixed(kqt, kqb, p, per, rows, s);
   switch (kqt) {
     case KQ_Q4_K: return tiles_launch<KQ_Q4_K>(p, per, rows, s);
     case KQ_Q5_K: return tiles_launch<KQ_Q5_K>(p, per, rows, s);

@@ -863,6 +863,49 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
     HIPCHECK(lw::launch_fused_tiles_mma8(fp, tpb, s));
     if (launches) ++*launches;
   }
+  // m = 1, fp16 x, kernel mode 0: matrices of two K-quant types in one whole-tile launch (entries of the smaller type
+  // code first), one launch fewer than a launch per type (config 3's Q6_K down with IQ4_XS gate / up)
+  auto tiles_ok = [&](const lw::DevMat& dm) {
+    return dm.kqt >= lw::KQ_Q4_K && dm.kqt <= lw::KQ_IQ4_XS && !dm.packed && dm.dsplit && dm.mid && dm.lut4 &&
+           dm.rows && dm.max_rows + 2 <= 256;
+  };
+  while (flat && mt == 1 && !x8 && g_kernel_mode == 0) {
+    int ka = 0, kb = 0;
+    for (int i = 0; i < count; ++i) {
+      if (done[i] || !tiles_ok(ts[i]->dm)) continue;
+      const int k = ts[i]->dm.kqt;
+      if (!ka) ka = k;
+      else if (k != ka && !kb) kb = k;
+    }
+    if (!kb) break;
+    if (kb < ka) std::swap(ka, kb);
+    std::vector<int> sel;
+    for (int pass = 0; pass < 2; ++pass)
+      for (int j = 0; j < count && (int)sel.size() < lw::MAX_GROUP; ++j)
+        if (!done[j] && tiles_ok(ts[j]->dm) && ts[j]->dm.kqt == (pass ? kb : ka)) sel.push_back(j);
+    lw::FlatPlan fp{};
+    int mintiles = 1 << 30;
+    for (int j : sel) {
+      const lw::DevMat& dm = ts[j]->dm;
+      if (dm.kqt == ka) ++fp.nfa;
+      lw::FlatEntry& e = fp.e[fp.n++];
+      e.M = dm;
+      e.X2 = static_cast<const uint32_t*>(X16[j]);
+      e.P = Pb + off[j];
+      e.tile0 = fp.ntiles;
+      e.ntile = dm.NT * dm.KT;
+      e.Y = Y[j];
+      e.cnt = Cb + coff[j];
+      fp.ntiles += e.ntile;
+      mintiles = std::min(mintiles, e.ntile);
+    }
+    if (fp.nfa == fp.n) break;  // the batch of MAX_GROUP holds one type only: the per-type launches take it
+    int per = 0;
+    fp.W = tiles_width(fp, mintiles, per);
+    if (fp.W < 1) break;
+    for (int j : sel) done[j] = reduced[j] = exc_in[j] = whole[j] = 1;
+    tile_plans.emplace_back(fp, per);
+  }
   for (int i = 0; flat && i < count; ++i) {
     if (done[i]) continue;
     const lw::DevMat& di = ts[i]->dm;
