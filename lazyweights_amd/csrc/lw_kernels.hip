@@ -2532,24 +2532,15 @@ __device__ __forceinline__ f4v mfma4_from(h4v a, h4v b, f4v c) {
   return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 4, ABID, 0);
 }
 
-template <int KQ, int NTAB, int MT>
-__global__ void __launch_bounds__(64 * tiles_mma_waves(KQ, MT), 1)
+template <int KQA, int NTAB, int MT, int KQB = KQA>
+__global__ void __launch_bounds__(64 * (tiles_mma_waves(KQA, MT) < tiles_mma_waves(KQB, MT) ? tiles_mma_waves(KQA, MT)
+                                                                                         : tiles_mma_waves(KQB, MT)),
+                                  1)
 k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   static_assert(MT == 4 || MT == 8, "4 or 8 token slots");
-  constexpr int SYMB = kq_symbits(KQ);
-  constexpr int TW = SYMB == 4 ? 2 * TK : TK;
-  constexpr int SB = kq_sbytes(KQ);
-  constexpr int NSB = TW / 256;   // super-blocks per tile row
   constexpr int NQ = MT / 4;      // token quads
-  constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
   constexpr int NC = 4, NG = 16 / NC;  // chains per lane (64 symbols each: 8 tokens' x and accumulators leave no
                                        // registers for 8 chains at 4 waves per SIMD), 16-symbol groups per chain
-  constexpr int GW = kq_gw(KQ), NSUB = 256 / GW;          // weights per sub-block, sub-blocks per super-block
-  constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block
-  constexpr bool XSUMS = KQ != KQ_Q6_K;                   // an offset term over the sub-blocks' x sums
-  // the weights enter unscaled: 4-bit codes as fp16 denormals q 2^-24 (one byte permute per entry), 8-bit formats as
-  // fp16(q) from the table; each chain's sums per sub-block are scaled by dA s_j (2^24 s_j) when the sub-block ends
-  constexpr float WSCALE = SYMB == 4 ? 16777216.f : 1.f;
   typedef __attribute__((address_space(3))) const uint32_t LdsU32;
   typedef __attribute__((address_space(4))) const char KChar;
   typedef __attribute__((address_space(4))) const FlatEntry KEntry;
@@ -2637,7 +2628,8 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   // halves. Column slots: the first entry's columns from ca0 (mod KT), then the second entry's from cb0. Formed by
   // the waves that wait for their first copy's turn (all waves when none waits) before they ask for it; read once
   // the block's counter shows every share stored.
-  constexpr int GPC = TW / 128;  // groups of 4 sub-blocks per tile column
+  // (groups of 4 sub-blocks per tile column: TW / 128 of the entry's type; Q6_K has no x sums)
+  auto gpc_of = [&](KEntry* e) { return e->M.symbits == 4 ? 4 : 2; };
   auto cols = [&](KEntry* e, int u0, int u1, int& c0) {  // the columns of the entry's tiles u0 .. u1 (row-major)
     const int KT = e->M.KT;
     c0 = u1 - u0 + 1 >= KT ? 0 : u0 % KT;
@@ -2646,14 +2638,17 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   int ca0 = 0, cb0 = 0;
   const int nca = cols(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0, ca0);
   const int ncb = (NTAB > 1 && mb != ma) ? cols(eb, 0, Tl - eb->tile0, cb0) : 0;
+  const int gpa = gpc_of(ea), gpb = gpc_of(eb);
+  const bool xsa = ea->M.kqt != KQ_Q6_K, xsbe = ncb > 0 && eb->M.kqt != KQ_Q6_K;
   uint64_t* xsb = reinterpret_cast<uint64_t*>(tbuf + (size_t)W * buf_rows * 32);
+  const size_t xsb_b = (size_t)nca * mt * gpa * 2;  // the second entry's sums after the first's
   const int xw0 = W > C ? C : 0, xnw = W - xw0;
-  if (XSUMS && wave >= xw0) {
-    const int na = nca * mt * GPC, ntot = na + ncb * mt * GPC;
+  if ((xsa || xsbe) && wave >= xw0) {
+    const int na = xsa ? nca * mt * gpa : 0, ntot = na + (xsbe ? ncb * mt * gpb : 0);
     for (int i = (wave - xw0) * 64 + lane; i < ntot; i += xnw * 64) {
       const bool second = i >= na;
       KEntry* e = second ? eb : ea;
-      const int ii = second ? i - na : i;
+      const int ii = second ? i - na : i, GPC = second ? gpb : gpa, TW = 128 * GPC;
       const int gq = ii % GPC, r = ii / GPC, tok = r % mt, lc = r / mt;
       const int KT = e->M.KT, K = e->M.K;
       int c = (second ? cb0 : ca0) + lc;
@@ -2673,7 +2668,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         hi4 |= (uint64_t)__builtin_bit_cast(uint16_t, hi) << (16 * k);
         lo4 |= (uint64_t)__builtin_bit_cast(uint16_t, (_Float16)(sum - (float)hi)) << (16 * k);
       }
-      uint64_t* xs = xsb + ((size_t)((second ? nca : 0) + lc) * mt + tok) * (GPC * 2) + 2 * gq;
+      uint64_t* xs = xsb + (second ? xsb_b : 0) + ((size_t)lc * mt + tok) * (GPC * 2) + 2 * gq;
       xs[0] = hi4;
       xs[1] = lo4;
     }
@@ -2697,242 +2692,264 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
   // every share of the x sums stored: checked at each tile start until it holds; a tile that starts earlier (a
   // first tile) reads its sums after its decode instead
-  bool xs_ready = !XSUMS;
+  bool xs_ready = !(xsa || xsbe);
 #pragma unroll 1
   while (have) {
     if (!xs_ready)
       xs_ready = __builtin_amdgcn_readfirstlane((int)__hip_atomic_load(xs_done, __ATOMIC_RELAXED,
                                                                         __HIP_MEMORY_SCOPE_WORKGROUP)) >= xnw;
     asm volatile("" ::: "memory");
-    const bool xs_late = !xs_ready;
-    const int cur = sec;
-    const bool second = sec != 0;
-    KEntry* ep = second ? eb : ea;
-    const auto& E = *ep;
-    const auto& M = E.M;
-    const int KT = M.KT, N = M.N, K = M.K;
-    const int tc = t % KT, tr = t / KT;
-    const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
-    uint32_t sw[NSB][5];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
-    uint32_t P[NC];
-    {
-      uint32_t P8[8];
-      tile_chain_starts(M, t, f, s, P8);
-#pragma unroll
-      for (int j = 0; j < NC; ++j) P[j] = P8[j * (8 / NC)];
-    }
-    const uint32_t tsel = second ? 4u * LUTN : 0u;
-    // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
-    // (zero for tokens >= mt)
-    h4v xa[NQ][NPR], xs[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const int tok = 4 * q + qi;
-      const bool ok = tok < mt;
-      const uint32_t* xrow = E.X2 + (size_t)(ok ? tok : 0) * (K / 2) + (size_t)tc * (TW / 2);
-#pragma unroll
-      for (int m = 0; m < NPR; ++m) {
-        const uint2 v = ok ? *reinterpret_cast<const uint2*>(xrow + 2 * (16 * m + qb)) : make_uint2(0u, 0u);
-        xa[q][m] = __builtin_bit_cast(h4v, v);
+    // one tile of format KQ (KQB: a tile of the plan's entries from nfa on)
+    auto tile = [&](auto kq) __attribute__((always_inline)) {
+      constexpr int KQ = decltype(kq)::value;
+      constexpr int SYMB = kq_symbits(KQ);
+      constexpr int TW = SYMB == 4 ? 2 * TK : TK;
+      constexpr int SB = kq_sbytes(KQ);
+      constexpr int NSB = TW / 256;   // super-blocks per tile row
+      constexpr int NPR = TW / 64;    // x register pairs per quad (16 position blocks of 4 weights each)
+      constexpr int GW = kq_gw(KQ), NSUB = 256 / GW;          // weights per sub-block, sub-blocks per super-block
+      constexpr int GPSUB = (GW / (SYMB == 4 ? 2 : 1)) / 16;  // 16-symbol groups per sub-block
+      constexpr int GPC = TW / 128;                           // groups of 4 sub-blocks per tile column
+      constexpr bool XSUMS = KQ != KQ_Q6_K;                   // an offset term over the sub-blocks' x sums
+      // the weights enter unscaled: 4-bit codes as fp16 denormals q 2^-24 (one byte permute per entry), 8-bit formats
+      // as fp16(q) from the table; each chain's sums per sub-block are scaled by dA s_j (2^24 s_j) when it ends
+      constexpr float WSCALE = SYMB == 4 ? 16777216.f : 1.f;
+      const bool xs_late = !xs_ready;
+      const int cur = sec;
+      const bool second = sec != 0;
+      KEntry* ep = second ? eb : ea;
+      const auto& E = *ep;
+      const auto& M = E.M;
+      const int KT = M.KT, N = M.N, K = M.K;
+      const int tc = t % KT, tr = t / KT;
+      const uint8_t* srow = M.side + side_record(tr * TN, tc * NSB, KT, NSB) * SB + (uint32_t)(lane * SB);
+      uint32_t sw[NSB][5];
+  #pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) side_load<KQ>(srow + sb * (TN * SB), sw[sb]);
+      uint32_t P[NC];
+      {
+        uint32_t P8[8];
+        tile_chain_starts(M, t, f, s, P8);
+  #pragma unroll
+        for (int j = 0; j < NC; ++j) P[j] = P8[j * (8 / NC)];
       }
-    }
-    // XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks (hi or lo halves), block b = 2 (2 sb + half) + (lo)
-    auto load_xs = [&]() {
-#pragma unroll
+      const uint32_t tsel = second ? 4u * LUTN : 0u;
+      // x of the tile column: register pair m of quad q, lane 4 b + i = token 4 q + i's weights 4 (16 m + b) .. + 3
+      // (zero for tokens >= mt)
+      h4v xa[NQ][NPR], xs[NQ];
+  #pragma unroll
       for (int q = 0; q < NQ; ++q) {
-        const int tok = 4 * q + qi, cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
-        uint64_t sv = 0;
-        if (XSUMS && tok < mt && qb < 4 * NSB) {
-          const int lc = second ? nca + (tc - cb0 + KT) % KT : (tc - ca0 + KT) % KT;  // the column's slot
-          sv = xsb[((size_t)lc * mt + tok) * (GPC * 2) + 2 * sh + lo];
+        const int tok = 4 * q + qi;
+        const bool ok = tok < mt;
+        const uint32_t* xrow = E.X2 + (size_t)(ok ? tok : 0) * (K / 2) + (size_t)tc * (TW / 2);
+  #pragma unroll
+        for (int m = 0; m < NPR; ++m) {
+          const uint2 v = ok ? *reinterpret_cast<const uint2*>(xrow + 2 * (16 * m + qb)) : make_uint2(0u, 0u);
+          xa[q][m] = __builtin_bit_cast(h4v, v);
         }
-        xs[q] = __builtin_bit_cast(h4v, sv);
       }
-    };
-    if (!xs_late) load_xs();
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
-    if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (pend >= 0 && lane == 0)
-      pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t slot[NC], A[NC], B[NC], C[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
-      A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
-      B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
-      C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
-    }
-    // the lane's sub-block scales (bytes, low first) per super-block
-    uint64_t scq[NSB], scq2[NSB];  // scales of sub-blocks 0..7 and (Q6_K) 8..15
-    float dA[NSB], dB[NSB];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) side_packed<KQ>(sw[sb], scq[sb], scq2[sb], dA[sb], dB[sb]);
-    // s_j of sub-block js of the tile row (a constant after unrolling), extracted where it is used: the scale words
-    // are opaque here, so the compiler does not hold every converted scale through the decode (8 tokens of IQ4_XS
-    // spilled)
-    auto scale_of = [&](int js) -> float {
-      const int jsb = js / NSUB, jj = js % NSUB;
-      uint32_t w = (uint32_t)((jj >= 8 ? scq2[jsb] : scq[jsb]) >> (32 * ((jj % 8) / 4)));
-      asm("" : "+v"(w));
-      const uint32_t b = (w >> (8 * (jj % 4))) & 255u;
-      return (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)b : (float)b;
-    };
-    f4v acc[NC][NQ];  // per chain: its current sub-block's sums, 4 tokens per register quad
-    float fa[NQ][4];  // scaled sums of the finished sub-blocks
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa[q][i] = 0.f;
-#pragma unroll
-      for (int j = 0; j < NC; ++j) acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
-    }
-    uint32_t wprev[NC];
-#pragma unroll
-    for (int j = 0; j < NC; ++j) wprev[j] = 0;
-    static_for<NG>([&](auto gic) {
-      constexpr int gi = decltype(gic)::value;
-      static_for<8>([&](auto pc) {
-        constexpr int p = decltype(pc)::value;
-        uint32_t w1[NC], e1[NC], e2[NC];
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
-          e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+      // XS: lane 4 b + i = token 4 q + i's sums of 4 sub-blocks (hi or lo halves), block b = 2 (2 sb + half) + (lo)
+      auto load_xs = [&]() {
+  #pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int tok = 4 * q + qi, cb = qb & 7, lo = cb & 1, sh = cb >> 1;  // sh = 2 sb + half
+          uint64_t sv = 0;
+          if (XSUMS && tok < mt && qb < 4 * NSB) {
+            const int lc = (tc - (second ? cb0 : ca0) + KT) % KT;  // the column's slot
+            sv = xsb[(second ? xsb_b : 0) + ((size_t)lc * mt + tok) * (GPC * 2) + 2 * sh + lo];
+          }
+          xs[q] = __builtin_bit_cast(h4v, sv);
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-          P[j] = P[j] + e1[j] + e2[j];
-          const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
-          const bool slide = nslot != slot[j];
-          A[j] = slide ? B[j] : A[j];
-          B[j] = slide ? C[j] : B[j];
-          slot[j] = nslot;
-          C[j] = *(LdsU32*)(rlb + (nslot << 7));
-        }
-        static_for<NC>([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          if constexpr (SYMB == 4) {  // 4 codes as fp16 denormals q 2^-24, in weight order
-            const uint2 wv = make_uint2(__builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u),
-                                        __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u));
-            constexpr int g = NG * j + gi;           // 16-symbol group within the tile row
-            constexpr int pb = 8 * g + p;            // position block of the 4 weights within the tile row
-#pragma unroll
-            for (int q = 0; q < NQ; ++q)
-              acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[j][q]);
-          } else {  // 2 codes per pair (fp16(q) in the entries' upper halves), 4 per product
-            const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
-            if constexpr (p & 1) {
-              constexpr int pb = 4 * (NG * j + gi) + p / 2;
-#pragma unroll
+      };
+      if (!xs_late) load_xs();
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partials stored
+      if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (pend >= 0 && lane == 0)
+        pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t slot[NC], A[NC], B[NC], C[NC];
+  #pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        slot[j] = __builtin_amdgcn_ubfe(P[j], 5, 8);
+        A[j] = *(LdsU32*)(rlb + ((slot[j] - 2u) << 7));
+        B[j] = *(LdsU32*)(rlb + ((slot[j] - 1u) << 7));
+        C[j] = *(LdsU32*)(rlb + (slot[j] << 7));
+      }
+      // the lane's sub-block scales (bytes, low first) per super-block
+      uint64_t scq[NSB], scq2[NSB];  // scales of sub-blocks 0..7 and (Q6_K) 8..15
+      float dA[NSB], dB[NSB];
+  #pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) side_packed<KQ>(sw[sb], scq[sb], scq2[sb], dA[sb], dB[sb]);
+      // s_j of sub-block js of the tile row (a constant after unrolling), extracted where it is used: the scale words
+      // are opaque here, so the compiler does not hold every converted scale through the decode (8 tokens of IQ4_XS
+      // spilled)
+      auto scale_of = [&](int js) -> float {
+        const int jsb = js / NSUB, jj = js % NSUB;
+        uint32_t w = (uint32_t)((jj >= 8 ? scq2[jsb] : scq[jsb]) >> (32 * ((jj % 8) / 4)));
+        asm("" : "+v"(w));
+        const uint32_t b = (w >> (8 * (jj % 4))) & 255u;
+        return (KQ == KQ_Q6_K || KQ == KQ_IQ4_XS) ? (float)(int)(int8_t)(uint8_t)b : (float)b;
+      };
+      f4v acc[NC][NQ];  // per chain: its current sub-block's sums, 4 tokens per register quad
+      float fa[NQ][4];  // scaled sums of the finished sub-blocks
+  #pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) fa[q][i] = 0.f;
+  #pragma unroll
+        for (int j = 0; j < NC; ++j) acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
+      }
+      uint32_t wprev[NC];
+  #pragma unroll
+      for (int j = 0; j < NC; ++j) wprev[j] = 0;
+      static_for<NG>([&](auto gic) {
+        constexpr int gi = decltype(gic)::value;
+        static_for<8>([&](auto pc) {
+          constexpr int p = decltype(pc)::value;
+          uint32_t w1[NC], e1[NC], e2[NC];
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            w1[j] = __builtin_amdgcn_alignbit(B[j], A[j], P[j]);
+            e1[j] = *(LdsU32*)table_addr(w1[j], tsel, tmask);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) e2[j] = *(LdsU32*)table_addr(w1[j] >> (e1[j] & 31u), tsel, tmask);
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            P[j] = P[j] + e1[j] + e2[j];
+            const uint32_t nslot = __builtin_amdgcn_ubfe(P[j], 5, 8);
+            const bool slide = nslot != slot[j];
+            A[j] = slide ? B[j] : A[j];
+            B[j] = slide ? C[j] : B[j];
+            slot[j] = nslot;
+            C[j] = *(LdsU32*)(rlb + (nslot << 7));
+          }
+          static_for<NC>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if constexpr (SYMB == 4) {  // 4 codes as fp16 denormals q 2^-24, in weight order
+              const uint2 wv = make_uint2(__builtin_amdgcn_perm(e1[j], e1[j], 0x0C030C02u),
+                                          __builtin_amdgcn_perm(e2[j], e2[j], 0x0C030C02u));
+              constexpr int g = NG * j + gi;           // 16-symbol group within the tile row
+              constexpr int pb = 8 * g + p;            // position block of the 4 weights within the tile row
+  #pragma unroll
               for (int q = 0; q < NQ; ++q)
-                acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[j][q]);
-            } else {
-              wprev[j] = v;
+                acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, wv), acc[j][q]);
+            } else {  // 2 codes per pair (fp16(q) in the entries' upper halves), 4 per product
+              const uint32_t v = __builtin_amdgcn_perm(e2[j], e1[j], 0x07060302u);
+              if constexpr (p & 1) {
+                constexpr int pb = 4 * (NG * j + gi) + p / 2;
+  #pragma unroll
+                for (int q = 0; q < NQ; ++q)
+                  acc[j][q] = mfma4_from<pb & 15>(xa[q][pb >> 4], __builtin_bit_cast(h4v, make_uint2(wprev[j], v)), acc[j][q]);
+              } else {
+                wprev[j] = v;
+              }
             }
-          }
+          });
         });
+        // sub-blocks ending with this group: y += dA s_j acc (2^24 s_j for the denormal form), then acc = 0
+        if constexpr ((gi + 1) % GPSUB == 0) {
+          static_for<NC>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            constexpr int js = (NG * j + gi) / GPSUB;  // sub-block within the tile row
+            const float sa = dA[js / NSUB] * WSCALE * scale_of(js);
+  #pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+  #pragma unroll
+              for (int i = 0; i < 4; ++i) fa[q][i] = fmaf(acc[j][q][i], sa, fa[q][i]);
+              acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
+            }
+          });
+        }
       });
-      // sub-blocks ending with this group: y += dA s_j acc (2^24 s_j for the denormal form), then acc = 0
-      if constexpr ((gi + 1) % GPSUB == 0) {
-        static_for<NC>([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          constexpr int js = (NG * j + gi) / GPSUB;  // sub-block within the tile row
-          const float sa = dA[js / NSUB] * WSCALE * scale_of(js);
-#pragma unroll
-          for (int q = 0; q < NQ; ++q) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) fa[q][i] = fmaf(acc[j][q][i], sa, fa[q][i]);
-            acc[j][q] = f4v{0.f, 0.f, 0.f, 0.f};
-          }
-        });
+      // the products are formed here, not sunk past the claim and the copy below
+  #pragma unroll
+      for (int q = 0; q < NQ; ++q)
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[q][i]));
+      if (xs_late) {  // this tile's sums, now that every share is stored
+        while (__hip_atomic_load(xs_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)xnw)
+          __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");
+        load_xs();
+        xs_ready = true;
       }
-    });
-    // the products are formed here, not sunk past the claim and the copy below
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(fa[q][i]));
-    if (xs_late) {  // this tile's sums, now that every share is stored
-      while (__hip_atomic_load(xs_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)xnw)
-        __builtin_amdgcn_s_sleep(2);
-      asm volatile("" ::: "memory");
-      load_xs();
-      xs_ready = true;
-    }
-    // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
-    // so the buffer is free); the pending row's counter value arrived during the decode
-    {
-      uint32_t nx = 0;
-      if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      n = __builtin_amdgcn_readfirstlane((int)nx);
-    }
-    const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
-    have = n < per && T0 + n < plan.ntiles;
-    if (have) {
-      tile_of(n, sec, t);
-      uint32_t k = 0;
-      if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
-      copy_tile(sec ? eb : ea, t);
-    }
-    // offset terms: per super-block and token, sum_j c_j (sum x)_j from the hi and lo halves of the sums, c_j = the
-    // mins m_j (Q4_K / Q5_K) or the signed scales s_j (IQ4_XS)
-    f4v mac[NSB][NQ];
-#pragma unroll
-    for (int sb = 0; sb < NSB; ++sb) {
-      if constexpr (!XSUMS) break;
-      float mf[8];
-      if constexpr (KQ == KQ_IQ4_XS) {
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) mf[jj] = scale_of(8 * sb + jj);
-      } else {
-        side_mins(sw[sb], mf);
+      // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
+      // so the buffer is free); the pending row's counter value arrived during the decode
+      {
+        uint32_t nx = 0;
+        if (lane == 0) nx = __hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        n = __builtin_amdgcn_readfirstlane((int)nx);
       }
-      const h4v m0 = h4v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3]};
-      const h4v m1 = h4v{(_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        f4v r = {0.f, 0.f, 0.f, 0.f};
-        if (sb == 0) {
-          r = mfma4_from<0>(xs[q], m0, r);
-          r = mfma4_from<1>(xs[q], m0, r);
-          r = mfma4_from<2>(xs[q], m1, r);
-          r = mfma4_from<3>(xs[q], m1, r);
+      const uint32_t old = pend >= 0 ? (uint32_t)__builtin_amdgcn_readlane((int)pold, 0) : 0u;
+      have = n < per && T0 + n < plan.ntiles;
+      if (have) {
+        tile_of(n, sec, t);
+        uint32_t k = 0;
+        if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
+        copy_tile(sec ? eb : ea, t);
+      }
+      // offset terms: per super-block and token, sum_j c_j (sum x)_j from the hi and lo halves of the sums, c_j = the
+      // mins m_j (Q4_K / Q5_K) or the signed scales s_j (IQ4_XS)
+      f4v mac[NSB][NQ];
+  #pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) {
+        if constexpr (!XSUMS) break;
+        float mf[8];
+        if constexpr (KQ == KQ_IQ4_XS) {
+  #pragma unroll
+          for (int jj = 0; jj < 8; ++jj) mf[jj] = scale_of(8 * sb + jj);
         } else {
-          r = mfma4_from<4>(xs[q], m0, r);
-          r = mfma4_from<5>(xs[q], m0, r);
-          r = mfma4_from<6>(xs[q], m1, r);
-          r = mfma4_from<7>(xs[q], m1, r);
+          side_mins(sw[sb], mf);
         }
-        mac[sb][q] = r;
-      }
-    }
-    float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float tot = fa[q][i];
-        if constexpr (XSUMS) {
-#pragma unroll
-          for (int sb = 0; sb < NSB; ++sb)
-            tot = fmaf(KQ == KQ_IQ4_XS ? -128.f * dA[sb] : -dB[sb], mac[sb][q][i], tot);
+        const h4v m0 = h4v{(_Float16)mf[0], (_Float16)mf[1], (_Float16)mf[2], (_Float16)mf[3]};
+        const h4v m1 = h4v{(_Float16)mf[4], (_Float16)mf[5], (_Float16)mf[6], (_Float16)mf[7]};
+  #pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          f4v r = {0.f, 0.f, 0.f, 0.f};
+          if (sb == 0) {
+            r = mfma4_from<0>(xs[q], m0, r);
+            r = mfma4_from<1>(xs[q], m0, r);
+            r = mfma4_from<2>(xs[q], m1, r);
+            r = mfma4_from<3>(xs[q], m1, r);
+          } else {
+            r = mfma4_from<4>(xs[q], m0, r);
+            r = mfma4_from<5>(xs[q], m0, r);
+            r = mfma4_from<6>(xs[q], m1, r);
+            r = mfma4_from<7>(xs[q], m1, r);
+          }
+          mac[sb][q] = r;
         }
-        if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-    if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
-    pend = -1;
-    if (E.Y) {
-      pend = cur;
-      ptr = tr;
-      pKT = KT;
-      pN = N;
+      float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
+  #pragma unroll
+      for (int q = 0; q < NQ; ++q)
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float tot = fa[q][i];
+          if constexpr (XSUMS) {
+  #pragma unroll
+            for (int sb = 0; sb < NSB; ++sb)
+              tot = fmaf(KQ == KQ_IQ4_XS ? -128.f * dA[sb] : -dB[sb], mac[sb][q][i], tot);
+          }
+          if (4 * q + i < mt) __hip_atomic_store(out + (size_t)(4 * q + i) * N, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane, mt);
+      pend = -1;
+      if (E.Y) {
+        pend = cur;
+        ptr = tr;
+        pKT = KT;
+        pN = N;
+      }
+    };
+    if constexpr (KQB != KQA) {
+      if (__builtin_amdgcn_readfirstlane((sec ? mb : ma) >= plan.nfa ? 1 : 0)) tile(KqTag<KQB>{});
+      else tile(KqTag<KQA>{});
+    } else {
+      tile(KqTag<KQA>{});
     }
   }
   if (pend >= 0) {
@@ -2943,15 +2960,34 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
 }
 
-template <int KQ, int NTAB, int MT>
+template <int KQ, int NTAB, int MT, int KQB = KQ>
 static hipError_t tiles_mma_launch_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
   const size_t smem = (size_t)p.W * buf_rows * 128 + tiles_mma_xs_bytes(p, per);
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles_mma<KQ, NTAB, MT>),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fused_tiles_mma<KQ, NTAB, MT, KQB>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
   if (e != hipSuccess) return e;
   const int blocks = (p.ntiles + per - 1) / per;
-  hipLaunchKernelGGL((k_fused_tiles_mma<KQ, NTAB, MT>), dim3(blocks), dim3(p.W * 64), smem, s, p, per, buf_rows);
+  hipLaunchKernelGGL((k_fused_tiles_mma<KQ, NTAB, MT, KQB>), dim3(blocks), dim3(p.W * 64), smem, s, p, per,
+                     buf_rows);
   return hipGetLastError();
+}
+
+// two K-quant types in one launch: entries [0, nfa) of type KQA < KQB, the rest of KQB
+template <int KQA, int KQB>
+static hipError_t tiles_mma_launch_mixed_t(const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  return p.mt <= 4 ? tiles_mma_launch_t<KQA, 2, 4, KQB>(p, per, buf_rows, s)
+                   : tiles_mma_launch_t<KQA, 2, 8, KQB>(p, per, buf_rows, s);
+}
+static hipError_t tiles_mma_launch_mixed(int kqa, int kqb, const FlatPlan& p, int per, int buf_rows, hipStream_t s) {
+  switch (kqa * 8 + kqb) {
+    case KQ_Q4_K * 8 + KQ_Q5_K: return tiles_mma_launch_mixed_t<KQ_Q4_K, KQ_Q5_K>(p, per, buf_rows, s);
+    case KQ_Q4_K * 8 + KQ_Q6_K: return tiles_mma_launch_mixed_t<KQ_Q4_K, KQ_Q6_K>(p, per, buf_rows, s);
+    case KQ_Q4_K * 8 + KQ_IQ4_XS: return tiles_mma_launch_mixed_t<KQ_Q4_K, KQ_IQ4_XS>(p, per, buf_rows, s);
+    case KQ_Q5_K * 8 + KQ_Q6_K: return tiles_mma_launch_mixed_t<KQ_Q5_K, KQ_Q6_K>(p, per, buf_rows, s);
+    case KQ_Q5_K * 8 + KQ_IQ4_XS: return tiles_mma_launch_mixed_t<KQ_Q5_K, KQ_IQ4_XS>(p, per, buf_rows, s);
+    case KQ_Q6_K * 8 + KQ_IQ4_XS: return tiles_mma_launch_mixed_t<KQ_Q6_K, KQ_IQ4_XS>(p, per, buf_rows, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int KQ>
@@ -3444,7 +3480,9 @@ size_t tiles_mma_xs_bytes(const FlatPlan& p, int per) {
   // a block's tiles lie in at most per tile columns; per column and token 4 bytes per sub-block (int8 activations
   // bring their block sums: none)
   if (p.i8) return 0;
-  return (size_t)std::max(per, 0) * std::max(p.mt, 0) * (kq_symbits(p.e[0].M.kqt) == 4 ? 2 * TK : TK) / 32 * 4;
+  int tw = 0;
+  for (int i = 0; i < p.n; ++i) tw = std::max(tw, kq_symbits(p.e[i].M.kqt) == 4 ? 2 * TK : TK);
+  return (size_t)std::max(per, 0) * std::max(p.mt, 0) * tw / 32 * 4;
 }
 
 int tiles_mma_max_waves(int kqt, int mt) { return tiles_mma_waves(kqt, mt <= 4 ? 4 : 8); }
@@ -3475,14 +3513,17 @@ hipError_t launch_fused_tiles_mma8(const FlatPlan& p, int per, hipStream_t s) {
 }
 
 hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
-  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || per < p.W || p.ntiles < 1 || p.mt < 1 || p.mt > 8 || p.i8 ||
-      p.W > tiles_mma_max_waves(p.e[0].M.kqt, p.mt))
+  if (p.n < 1 || p.n > MAX_GROUP || p.W < 1 || per < p.W || p.ntiles < 1 || p.mt < 1 || p.mt > 8 || p.i8)
     return hipErrorInvalidValue;
-  const int kqt = p.e[0].M.kqt;
+  // two K-quant types: entries [0, nfa) of the first (the smaller type code), the rest of the second
+  const bool mixed = p.nfa > 0 && p.nfa < p.n;
+  const int kqt = p.e[0].M.kqt, kqb = mixed ? p.e[p.nfa].M.kqt : kqt;
+  if ((mixed && kqb <= kqt) || p.W > tiles_mma_max_waves(kqt, p.mt) || p.W > tiles_mma_max_waves(kqb, p.mt))
+    return hipErrorInvalidValue;
   for (int i = 0; i < p.n; ++i) {
     const FlatEntry& e = p.e[i];
     const int end = i + 1 < p.n ? p.e[i + 1].tile0 : p.ntiles;
-    if (e.M.kqt != kqt || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
+    if (e.M.kqt != (mixed && i >= p.nfa ? kqb : kqt) || !e.M.dsplit || !e.M.mid || !e.M.lut4 || !e.M.rows || e.M.packed || e.tile0 + e.ntile != end ||
         e.ntile < 1 || (p.n > 1 && e.ntile < per) || e.list || e.ntile != e.M.NT * e.M.KT ||
         (i == 0 && e.tile0 != 0))
       return hipErrorInvalidValue;
@@ -3491,6 +3532,7 @@ hipError_t launch_fused_tiles_mma(const FlatPlan& p, int per, hipStream_t s) {
   if (rows > 256 ||
       (size_t)p.W * rows * 128 + tiles_mma_xs_bytes(p, per) + (p.n > 1 ? 2 : 1) * 4 * LUTN + 16 > 160 * 1024)
     return hipErrorInvalidValue;
+  if (mixed) return tiles_mma_launch_mixed(kqt, kqb, p, per, rows, s);
   switch (kqt) {
     case KQ_Q4_K: return tiles_mma_launch<KQ_Q4_K>(p, per, rows, s);
     case KQ_Q5_K: return tiles_mma_launch<KQ_Q5_K>(p, per, rows, s);

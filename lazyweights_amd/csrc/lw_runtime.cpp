@@ -631,7 +631,9 @@ int tiles_mma_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   per = (fp.ntiles + cus - 1) / cus;
   if (fp.n > 1) per = std::min(per, mintiles);
   const long room = 160L * 1024 - tables - 16 - (long)lw::tiles_mma_xs_bytes(fp, per);
-  const int wmax = (int)std::min<long>(lw::tiles_mma_max_waves(fp.e[0].M.kqt, fp.mt), room / (rows * 128L));
+  int wcap = lw::tiles_mma_max_waves(fp.e[0].M.kqt, fp.mt);
+  for (int k = 1; k < fp.n; ++k) wcap = std::min(wcap, lw::tiles_mma_max_waves(fp.e[k].M.kqt, fp.mt));
+  const int wmax = (int)std::min<long>(wcap, room / (rows * 128L));
   if (wmax < 1) return 0;
   return std::min(wmax, per);
 }
@@ -674,7 +676,8 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
            dm.max_rows + 2 <= 256;
   };
   const bool mma = !x8 && per == 1 && mt >= 2 && mt <= 8 && g_kernel_mode == 0;
-  // its launches: matrices of one K-quant type, up to MAX_GROUP each
+  // its launches: matrices of one K-quant type, or of two (entries of the smaller type code first: one launch fewer),
+  // up to MAX_GROUP each
   struct MmaLaunch {
     lw::FlatPlan fp;
     int tpb;
@@ -683,6 +686,41 @@ int fused_group_dev(Model& M, Tensor* const* ts, const void* const* X16, int cou
   std::vector<MmaLaunch> mma_plans;
   if (mma) {
     std::vector<char> mdone(count, 0);
+    for (;;) {  // two types per launch while two are left
+      int ka = 0, kb = 0;
+      for (int i = 0; i < count; ++i) {
+        if (mdone[i] || !mma_ok(ts[i]->dm)) continue;
+        const int k = ts[i]->dm.kqt;
+        if (!ka) ka = k;
+        else if (k != ka && !kb) kb = k;
+      }
+      if (!kb) break;
+      if (kb < ka) std::swap(ka, kb);
+      MmaLaunch L{};
+      L.fp.mt = mt;
+      int mintiles = 1 << 30;
+      for (int pass = 0; pass < 2; ++pass)
+        for (int j = 0; j < count && L.fp.n < lw::MAX_GROUP; ++j) {
+          const lw::DevMat& dm = ts[j]->dm;
+          if (mdone[j] || !mma_ok(dm) || dm.kqt != (pass ? kb : ka)) continue;
+          if (!pass) ++L.fp.nfa;
+          lw::FlatEntry& e = L.fp.e[L.fp.n++];
+          e.M = dm;
+          e.X2 = static_cast<const uint32_t*>(X16[j]);
+          e.tile0 = L.fp.ntiles;
+          e.ntile = dm.NT * dm.KT;
+          e.Y = Y[j];
+          e.ldy = ldy[j];
+          L.fp.ntiles += e.ntile;
+          mintiles = std::min(mintiles, e.ntile);
+          L.sel.push_back(j);
+        }
+      if (L.fp.nfa == L.fp.n) break;  // the batch of MAX_GROUP holds one type only: the per-type launches take it
+      L.fp.W = tiles_mma_width(L.fp, mintiles, L.tpb);
+      if (L.fp.W < 1) break;
+      for (int j : L.sel) mdone[j] = 1;
+      mma_plans.push_back(std::move(L));
+    }
     for (int i = 0; i < count; ++i) {
       if (mdone[i] || !mma_ok(ts[i]->dm)) continue;
       MmaLaunch L{};

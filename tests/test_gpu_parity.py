@@ -861,23 +861,25 @@ def test_gpu_flat_kernel_spans_and_modes(fmt_rt, orc):
             check_err(a.cpu().numpy(), y64, "%s flat" % nm)
 
 
-def test_gpu_mixed_format_whole_tile_launch(fmt_rt, orc):
-    """m = 1 over matrices of several K-quant types in one grouped call: two types share a whole-tile launch
-    (FlatPlan::nfa: entries of the smaller type code first, blocks spanning a matrix of each type). The bits equal one
-    call per matrix (each its own single-type launch) and every result is within tolerance of fp64."""
+@pytest.mark.parametrize("m", [1, 5])
+def test_gpu_mixed_format_whole_tile_launch(fmt_rt, orc, m):
+    """m = 1 and m = 5 (the matrix-core kernel) over matrices of several K-quant types in one grouped call: two types
+    share a whole-tile launch (FlatPlan::nfa: entries of the smaller type code first, blocks spanning a matrix of each
+    type). The bits equal one call per matrix (each its own single-type launch) and every result is within tolerance
+    of fp64."""
     import ctypes
 
     import torch
     rt, mats = fmt_rt
     for names in (["Q4_K", "Q6_K_small", "IQ4_XS", "Q5_K", "Q6_K"], ["IQ4_XS", "Q6_K", "IQ4_XS_small"],
                   ["Q5_K_small", "Q4_K", "Q4_K_small", "Q5_K"]):
-        say("mixed-format launch", names)
-        X = [torch.randn(1, mats[nm][3]).half() for nm in names]
+        say("mixed-format launch m=%d" % m, names)
+        X = [torch.randn(m, mats[nm][3]).half() for nm in names]
         Xd = [x.cuda() for x in X]
-        Yg = [torch.zeros(1, mats[nm][2], device="cuda") for nm in names]
+        Yg = [torch.zeros(m, mats[nm][2], device="cuda") for nm in names]
         n = len(names)
         rc = rt.lib.lw_group_matmul_dev(rt.h, n, (ctypes.c_char_p * n)(*[nm.encode() for nm in names]),
-                                        (ctypes.c_void_p * n)(*[x.data_ptr() for x in Xd]), 1,
+                                        (ctypes.c_void_p * n)(*[x.data_ptr() for x in Xd]), m,
                                         (ctypes.c_void_p * n)(*[y.data_ptr() for y in Yg]), None)
         assert rc == 0, rt.lib.lw_last_error()
         Ys = [torch.zeros_like(y) for y in Yg]
@@ -887,7 +889,7 @@ def test_gpu_mixed_format_whole_tile_launch(fmt_rt, orc):
         for nm, x, a, c in zip(names, X, Yg, Ys):
             assert torch.equal(a, c), nm
             _, y64 = reference_y(orc, mats[nm], x.double().numpy())
-            check_err(a.cpu().numpy(), y64, "%s in a mixed launch" % nm)
+            check_err(a.cpu().numpy(), y64, "%s in a mixed launch, m=%d" % (nm, m))
 
 
 def test_gpu_model_shaped_bundle(gpu, tmp_path, orc):
