@@ -294,6 +294,9 @@ def main():
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection run: a few grouped passes over the layers plus a 256 MiB device copy "
                          "(the calibration for FETCH_SIZE / WRITE_SIZE), no timing, no JSON")
+    ap.add_argument("--profile-config3", action="store_true",
+                    help="with --profile: the passes over 4 config-3 layers (Q6_K down + IQ4_XS gate / up, one "
+                         "grouped call per layer) instead, at --m tokens")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the path has no multi-GPU leg); run with --gpus 1",
@@ -322,6 +325,34 @@ def main():
     if a.only_configs:
         try:
             print(json.dumps(further_configs(work)), flush=True)
+        finally:
+            if not a.workdir:
+                shutil.rmtree(work, ignore_errors=True)
+        return
+    if a.profile and a.profile_config3:
+        import ctypes
+        try:
+            lm = [("l%d.%s" % (l, nm), kqt, N, K, H, seed + 97 * l) for l in range(4)
+                  for nm, kqt, N, K, H, seed in CONFIG3]
+            bundle.write_synthetic_bundle(work, lm, threads=16)
+            rt = Runtime(work)
+            infos = [rt.info(mt[0]) for mt in lm]
+            g = torch.Generator().manual_seed(11)
+            X = [torch.randn(a.m, inf["K"], generator=g).half().cuda() for inf in infos]
+            Y = [torch.zeros(a.m, inf["N"], device="cuda") for inf in infos]
+            stream = torch.cuda.current_stream().cuda_stream
+            per = len(CONFIG3)
+            calls = [((ctypes.c_char_p * per)(*[mt[0].encode() for mt in lm[per * l:per * l + per]]),
+                      (ctypes.c_void_p * per)(*[x.data_ptr() for x in X[per * l:per * l + per]]),
+                      (ctypes.c_void_p * per)(*[y.data_ptr() for y in Y[per * l:per * l + per]])) for l in range(4)]
+            for _ in range(max(1, a.steps)):
+                for nm, xx, yy in calls:
+                    if lib.lw_group_matmul_dev(rt.h, per, nm, xx, a.m, yy, stream) != 0:
+                        raise RuntimeError(lib.lw_last_error().decode())
+            torch.cuda.synchronize()
+            log("bench --profile --profile-config3: %d passes over 4 config-3 layers at m = %d done"
+                % (max(1, a.steps), a.m))
+            rt.close()
         finally:
             if not a.workdir:
                 shutil.rmtree(work, ignore_errors=True)

@@ -1,6 +1,7 @@
 """Builds lazyweights_amd/liblazyweights_amd.so in-tree (HIP kernels for gfx950 + host C++ runtime).
 
-    python -m lazyweights_amd.build
+    python -m lazyweights_amd.build               # the library
+    python -m lazyweights_amd.build --timeline    # the diagnostic timestamp build (lazyweights_amd.timeline)
 
 Device code: hipcc --offload-arch=gfx950, with packed-fp32 instruction selection disabled. Pure host C++ (codec,
 layout, bundle writer) is compiled with g++; everything is linked into one shared library exposing the C-ABI of
@@ -17,6 +18,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "liblazyweights_amd.so")
+TIMELINE_LIB = os.path.join(PKG, "liblazyweights_amd_timeline.so")  # diagnostic build (build_timeline)
 ARCH = os.environ.get("LW_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -169,6 +171,30 @@ def build(verbose=False):
     return LIB
 
 
+def build_timeline(verbose=False):
+    """The diagnostic library (lazyweights_amd.timeline): the same sources, the device code compiled with
+    -DLW_TIMELINE (per-wave timestamps in the whole-tile kernel), beside the product library. Builds the product's
+    host objects first if they are missing."""
+    os.makedirs(BUILD, exist_ok=True)
+    objs = [os.path.join(BUILD, os.path.splitext(src)[0] + ".o") for src, kind in SOURCES if kind != "hip"]
+    if not all(os.path.exists(o) for o in objs):
+        build()
+    obj = os.path.join(BUILD, "lw_kernels_timeline.o")
+    _run([HIPCC, "-c", "-x", "hip", os.path.join(CSRC, "lw_kernels.hip"), "-o", obj] + COMMON + HIP_DEVICE +
+         ["-DLW_TIMELINE"])
+    tmp = TIMELINE_LIB + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp, obj] + objs +
+         ["-L" + ROCM_LIB, "-lrocblas", "-pthread", "-lm"])
+    check_dpp_hazards(tmp)
+    os.replace(tmp, TIMELINE_LIB)
+    if verbose:
+        print("built", TIMELINE_LIB)
+    return TIMELINE_LIB
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--timeline" in sys.argv[1:]:
+        build_timeline(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

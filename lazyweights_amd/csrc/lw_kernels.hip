@@ -802,10 +802,10 @@ __global__ void __launch_bounds__(WPB * 64, MT <= 2 ? 8 : (MT <= 8 ? 4 : 2)) k_f
 }
 
 // ── flat launches (m = 1): shared pieces ─────────────────────────────────────────────────────────────────
-// Reduction in the launch. A wave stores its tile's 64 partials (relaxed agent-scope atomic stores), waits for the
-// stores to complete (vmcnt(0)), and lane 0 counts the tile in its tile row with a relaxed agent-scope atomic; the
-// wave that counts the row's last tile resets the counter and sums the row's partials in tile-column order (the order
-// of k_reduce_group, so the bits are the same). No ordering between the partials and the counter is assumed (an
+// Reduction in the launch. A wave stores its tile's 64 partials (relaxed agent-scope atomic stores) and lane 0 counts
+// the tile in its tile row with a relaxed agent-scope atomic (no wait between the two); the wave that counts the
+// row's last tile resets the counter and sums the row's partials in tile-column order (the order of k_reduce_group,
+// so the bits are the same). No ordering between the partials and the counter is assumed (an
 // agent-scope release / acquire on gfx950 is a buffer_wbl2 / buffer_inv per wave, which measured 106-143 us per
 // config-2 layer against 45 us): a partial slot holds kNoPartial from the end of one reduction to the store of the
 // next partial, so the summing wave takes each slot by an atomic exchange with kNoPartial until what it takes is not
@@ -862,7 +862,6 @@ __device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int 
 template <class KEntryRef>
 __device__ __forceinline__ void row_reduce(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
   if (!E.Y) return;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   uint32_t old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(E.cnt + tr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   old = __builtin_amdgcn_readlane(old, 0);
@@ -1687,6 +1686,24 @@ constexpr int TILES_COPIES = LW_TILES_COPIES;
 // CANON (kernel mode 9, fp16 activations): codes are looked up by the comparator (canon_addr) in a 256-entry table
 // of entries in canonical order instead of the 2048-entry table; the same entries, so the same bits. Its blocks have
 // at most TILES_CANON_WAVES waves (3 per SIMD): the comparator's registers spill at 4.
+// Diagnostic build only (-DLW_TIMELINE, lazyweights_amd.timeline): per-wave timestamps of the whole-tile kernel
+// (s_memrealtime, 100 MHz) in g_timeline[block][wave][slot]: slot 0 the wave's start, 1 after the tables' barrier, 2
+// its HW_ID register (SIMD and CU), 3 its end, and for its tile i < 8: 4 + 3 i the tile in LDS, 5 + 3 i its decode
+// done, 6 + 3 i the next tile's copy issued. Lane 0 of each wave stores (vector stores); nothing else changes.
+#ifdef LW_TIMELINE
+constexpr int TL_BLOCKS = 1024, TL_WAVES = 16, TL_SLOTS = 32;
+__device__ uint64_t g_timeline[TL_BLOCKS * TL_WAVES * TL_SLOTS];
+__device__ __forceinline__ void tl_put(int k, uint64_t v) {
+  if ((threadIdx.x & 63) == 0 && blockIdx.x < TL_BLOCKS && k < TL_SLOTS)
+    g_timeline[((size_t)blockIdx.x * TL_WAVES + (threadIdx.x >> 6)) * TL_SLOTS + k] = v;
+}
+#define LW_TL(k) tl_put((k), __builtin_amdgcn_s_memrealtime())
+#define LW_TL_HWID() tl_put(2, __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11)))
+#else
+#define LW_TL(k) ((void)0)
+#define LW_TL_HWID() ((void)0)
+#endif
+
 template <int V>
 struct KqTag {
   static constexpr int value = V;
@@ -1719,6 +1736,10 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   KEntry* eb = (KEntry*)(kbase + offsetof(FlatPlan, e) + (size_t)mb * sizeof(FlatEntry));
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, s = lane & 31, f = lane >> 5;
+  LW_TL(0);
+  LW_TL_HWID();
+  int tl_i = 0;  // (the diagnostic timestamps' tile index)
+  (void)tl_i;
   if (CANON) {  // the comparator tables' 256 entries: one 1 KB direct-to-LDS load per table, at the tables' places
     const uint4* ta = reinterpret_cast<const uint4*>(ea->M.canon + 32);
     const uint4* tb = reinterpret_cast<const uint4*>(eb->M.canon + 32);
@@ -1804,6 +1825,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   // (a bare barrier: the copies stay in flight)
   wait_vmcnt_upto(ncopy);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  LW_TL(1);
   if (have && wave >= C) {
     ask((uint32_t)wave);
     copy_tile(sec ? eb : ea, t);
@@ -1878,6 +1900,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       }
       auto xw = [&](int c) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)xv[c >> 6], c & 63); };
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the tile is in LDS, the pending tile's partial stored
+      LW_TL(4 + 3 * tl_i);
       if (lane == 0) __hip_atomic_fetch_add(landed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       if (pend >= 0 && lane == 0)
         pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1983,6 +2006,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       // holding every table entry of the tile in scratch)
   #pragma unroll
       for (int k = 0; k < NSUBT; ++k) asm volatile("" : "+v"(sub[k]));
+      LW_TL(5 + 3 * tl_i);
       // the next tile: claimed and its copy issued now (the claim's wait also covers every LDS read of the decode,
       // so the buffer is free); the pending row first
       {
@@ -1999,6 +2023,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
         if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
         copy_tile(sec ? eb : ea, t);
+        LW_TL(6 + 3 * tl_i);
         ++tdone;  // the wave's priority falls with the tiles it has taken
         if (tdone == 1) __builtin_amdgcn_s_setprio(2);
         else if (tdone == 2) __builtin_amdgcn_s_setprio(1);
@@ -2067,6 +2092,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
         pKT = KT;
         pN = N;
       }
+      ++tl_i;
     };
     if constexpr (KQB != KQA) {
       if (__builtin_amdgcn_readfirstlane((sec ? mb : ma) >= plan.nfa ? 1 : 0)) tile(KqTag<KQB>{});
@@ -2076,11 +2102,11 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
     }
   }
   if (pend >= 0) {  // the last tile's reduction
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_pending();
   }
+  LW_TL(3);
 }
 
 // ── half-tile kernel for flat launches (m = 1, fp16 activations): a wave decodes half-tile units, two buffered ─────
@@ -2953,7 +2979,6 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     }
   }
   if (pend >= 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_pending();
@@ -3332,7 +3357,6 @@ k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
     }
   }
   if (pend >= 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0)
       pold = __hip_atomic_fetch_add((pend ? eb : ea)->cnt + ptr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     finish_pending();
@@ -4912,3 +4936,17 @@ hipError_t launch_stream_read(const void* src, size_t n16, float* out, int block
 }
 
 }  // namespace lw
+
+#ifdef LW_TIMELINE
+// the diagnostic build's timestamps (see g_timeline): copied out, or cleared
+extern "C" int lw_timeline_read(void* dst, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(lw::g_timeline), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int lw_timeline_clear() {
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(lw::g_timeline));
+  if (e == hipSuccess) e = hipMemset(p, 0, sizeof(lw::g_timeline));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  return (int)e;
+}
+#endif
