@@ -39,6 +39,7 @@ struct DevMat {
   int symbits;      // 4 (huf4p) or 8 (huf8)
   int KT, NT;       // tile columns, tile rows
   int max_rows;     // max over tiles of rows[t]
+  int tstride;      // > 0: tile t's words at words + 32 tstride t (= tbase[t]), tstride = max_rows; 0: read tbase
   int max_hrows;    // max over tiles and halves of a half-tile unit's rows
   int ring_rows;    // 16 / 32: ring kernel usable with that ring; 0: whole-tile kernel only
   // tiles the ring kernel skips (no schedule for ring_rows): the first nexc32 have a 32-row ring schedule (decoded
@@ -137,6 +138,9 @@ int split_stage_rows(const FlatPlan& plan);
 hipError_t launch_fused_tiles(const FlatPlan& plan, int per, hipStream_t s);
 // the most waves of a whole-tile block with the comparator lookup (FlatPlan::canon)
 constexpr int TILES_CANON_WAVES = 12;
+// LDS row counters of the whole-tile kernel (m = 1): a tile row that starts within this many tiles of a block's first
+// tile and ends among its tiles is counted in LDS; the static LDS is the tables plus 4 + TILES_ROWC words
+constexpr int TILES_ROWC = 64;
 // The half-tile kernel (m = 1, fp16 activations, no int8): as launch_fused_tiles, but a wave decodes half-tile units
 // (a tile's rows 32 f .. 32 f + 31) with two LDS buffers, the next unit's copy in flight while one decodes; the
 // in-launch reduction per tile row and half (each entry's cnt holds 2 NT counters). W waves per block, each with two

@@ -849,9 +849,11 @@ __device__ __forceinline__ float sum_partials(uint32_t* q, size_t cs, int KT) {
 }
 // The sums of tile row tr's partials, per token j < mt, by the wave that counted the row's last tile (it also resets
 // the counter). P is [KT][mt][N]: token j's partial of tile column c at P + (c mt + j) N.
+// (reset = false: the row was counted elsewhere, its counter is untouched)
 template <class KEntryRef>
-__device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1) {
-  if (lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void row_sum(const KEntryRef& E, int tr, int KT, int N, int lane, int mt = 1,
+                                        bool reset = true) {
+  if (reset && lane == 0) __hip_atomic_store(E.cnt + tr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   uint32_t* const q = reinterpret_cast<uint32_t*>(E.P + (size_t)tr * TN + (uint32_t)lane);
 #pragma unroll 1
   for (int j = 0; j < mt; ++j)
@@ -1720,8 +1722,8 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   typedef __attribute__((address_space(4))) const float KF32;
   typedef __attribute__((address_space(4))) const uint16_t KU16;
   // one static LDS object at address 0, so the tables sit at 0 and 8 KB (table_addr ORs its base into the index);
-  // the block's tile counter and copy counters after them
-  __shared__ uint32_t lut4[NTAB * LUTN + 4];
+  // the block's tile counter, copy counters and row counters after them
+  __shared__ uint32_t lut4[NTAB * LUTN + 4 + TILES_ROWC];
   extern __shared__ __align__(16) uint32_t tbuf[];  // W x buf_rows word rows of 32 words
 
   KChar* kbase = (KChar*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -1761,11 +1763,13 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   uint32_t* asked = next + 1;   // copies asked for (the first W: wave w's first tile is copy w)
   uint32_t* landed = next + 2;  // copies landed
   const int C = min(W, TILES_COPIES);
+  uint32_t* rowc = next + 4;   // tile rows in the block's tiles: counter of the row whose first tile is T0 + r
   if (threadIdx.x == 0) {
     next[0] = (uint32_t)W;
     asked[0] = (uint32_t)W;
     landed[0] = 0u;
   }
+  if (threadIdx.x < TILES_ROWC) rowc[threadIdx.x] = 0u;
   auto ask = [&](uint32_t k) {  // wait for copy k's turn
     while (k >= (uint32_t)C + __hip_atomic_load(landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
       __builtin_amdgcn_s_sleep(2);
@@ -1786,11 +1790,15 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   // the last one masked to the tile's own rows. The windows also read the 2 rows past the longest lane and the
   // table index takes up to 11 bits past a code's start: those rows keep whatever the buffer held, which no decoded
   // symbol depends on (every code lies within its lane's bits, a prefix code's entry ignores the bits after it).
-  // The per-tile words are read through the scalar cache (read-only during the launch). Returns the number of
-  // copy instructions.
-  auto copy_tile = [&](KEntry* e, int t) -> int {
-    const int nrow = (int)((KU16*)e->M.rows)[t];
-    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+  // The per-tile words are read through the scalar cache (read-only during the launch). A wave's first copy
+  // (slot) of a matrix whose tiles lie at a fixed stride copies the whole slot (max_rows rows: the rows past the
+  // tile's own are zeros) and reads no per-tile word, so it is issued as soon as the plan is read. Returns the
+  // number of copy instructions.
+  auto copy_tile = [&](KEntry* e, int t, bool slot) -> int {
+    const int ts = e->M.tstride;
+    const int nrow = (slot && ts > 0) ? ts : (int)((KU16*)e->M.rows)[t];
+    const uint32_t* wt = e->M.words + (ts > 0 ? (size_t)32 * ts * t : (size_t)((KU32*)e->M.tbase)[t]);
+    const uint4* src = reinterpret_cast<const uint4*>(wt) + lane;
     const int nc = (nrow + 7) / 8;
     for (int i = 0; i < nc; ++i)
       if (lane < 8 * (nrow - 8 * i))
@@ -1820,7 +1828,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   bool have = n < per && T0 + n < plan.ntiles;
   int sec = 0, t = 0, ncopy = 0;
   if (have) tile_of(n, sec, t);
-  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t, true);
   // this wave's table chunks, issued before its copy, are in LDS; the counters too; then every wave's
   // (a bare barrier: the copies stay in flight)
   wait_vmcnt_upto(ncopy);
@@ -1828,14 +1836,16 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
   LW_TL(1);
   if (have && wave >= C) {
     ask((uint32_t)wave);
-    copy_tile(sec ? eb : ea, t);
+    copy_tile(sec ? eb : ea, t, true);
   }
-  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+  if (wave == W - 1) {  // the block's row counts (and word offsets) into the scalar cache, read at each claim, by
+                        // the wave whose first tile comes last
     uint32_t warm = 0;
     auto touch = [&](KEntry* e, int u0, int u1) {
       if (e->list) return;
-      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
-      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+      const bool tb = e->M.tstride == 0;
+      for (int u = u0; u <= u1; u += 16) warm += (tb ? ((KU32*)e->M.tbase)[u] : 0u) + ((KU16*)e->M.rows)[u];
+      warm += (tb ? ((KU32*)e->M.tbase)[u1] : 0u) + ((KU16*)e->M.rows)[u1];
     };
     touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
     if (mb != ma) touch(eb, 0, Tl - eb->tile0);
@@ -2022,7 +2032,7 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
         uint32_t k = 0;
         if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
-        copy_tile(sec ? eb : ea, t);
+        copy_tile(sec ? eb : ea, t, false);
         LW_TL(6 + 3 * tl_i);
         ++tdone;  // the wave's priority falls with the tiles it has taken
         if (tdone == 1) __builtin_amdgcn_s_setprio(2);
@@ -2087,10 +2097,19 @@ k_fused_tiles(FlatPlan plan, int per, int buf_rows) {
       if (pend >= 0 && old == (uint32_t)(pKT - 1)) row_sum(*(pend ? eb : ea), ptr, pKT, pN, lane);
       pend = -1;
       if (E.Y) {
-        pend = cur;
-        ptr = tr;
-        pKT = KT;
-        pN = N;
+        // a tile row among the block's own tiles is counted in LDS at once (its global counter stays 0); a row
+        // shared with other blocks in the entry's counter, one tile later
+        const int r0 = E.tile0 + tr * KT - T0;
+        if (!E.list && r0 >= 0 && r0 < TILES_ROWC && T0 + r0 + KT - 1 <= Tl) {
+          uint32_t o = 0;
+          if (lane == 0) o = __hip_atomic_fetch_add(rowc + r0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if ((uint32_t)__builtin_amdgcn_readlane((int)o, 0) == (uint32_t)(KT - 1)) row_sum(E, tr, KT, N, lane, 1, false);
+        } else {
+          pend = cur;
+          ptr = tr;
+          pKT = KT;
+          pN = N;
+        }
       }
       ++tl_i;
     };
@@ -2623,9 +2642,11 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
     const int u = T - e->tile0;
     t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
   };
-  auto copy_tile = [&](KEntry* e, int t) -> int {  // as k_fused_tiles: the tile's own rows, the last copy masked
-    const int nrow = (int)((KU16*)e->M.rows)[t];
-    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+  auto copy_tile = [&](KEntry* e, int t, bool slot) -> int {  // as k_fused_tiles (a first copy takes the slot)
+    const int ts = e->M.tstride;
+    const int nrow = (slot && ts > 0) ? ts : (int)((KU16*)e->M.rows)[t];
+    const uint32_t* wt = e->M.words + (ts > 0 ? (size_t)32 * ts * t : (size_t)((KU32*)e->M.tbase)[t]);
+    const uint4* src = reinterpret_cast<const uint4*>(wt) + lane;
     const int nc = (nrow + 7) / 8;
     for (int i = 0; i < nc; ++i)
       if (lane < 8 * (nrow - 8 * i))
@@ -2645,7 +2666,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   bool have = n < per && T0 + n < plan.ntiles;
   int sec = 0, t = 0, ncopy = 0;
   if (have) tile_of(n, sec, t);
-  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t, true);
   // this wave's table chunks and the counters are in place; then every wave's (a bare barrier: copies stay in flight)
   wait_vmcnt_upto(ncopy);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -2703,14 +2724,16 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
   }
   if (have && wave >= C) {
     ask((uint32_t)wave);
-    copy_tile(sec ? eb : ea, t);
+    copy_tile(sec ? eb : ea, t, true);
   }
-  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+  if (wave == W - 1) {  // the block's row counts (and word offsets) into the scalar cache, read at each claim, by
+                        // the wave whose first tile comes last
     uint32_t warm = 0;
     auto touch = [&](KEntry* e, int u0, int u1) {
       if (e->list) return;
-      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
-      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+      const bool tb = e->M.tstride == 0;
+      for (int u = u0; u <= u1; u += 16) warm += (tb ? ((KU32*)e->M.tbase)[u] : 0u) + ((KU16*)e->M.rows)[u];
+      warm += (tb ? ((KU32*)e->M.tbase)[u1] : 0u) + ((KU16*)e->M.rows)[u1];
     };
     touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
     if (mb != ma) touch(eb, 0, Tl - eb->tile0);
@@ -2915,7 +2938,7 @@ k_fused_tiles_mma(FlatPlan plan, int per, int buf_rows) {
         uint32_t k = 0;
         if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
-        copy_tile(sec ? eb : ea, t);
+        copy_tile(sec ? eb : ea, t, false);
       }
       // offset terms: per super-block and token, sum_j c_j (sum x)_j from the hi and lo halves of the sums, c_j = the
       // mins m_j (Q4_K / Q5_K) or the signed scales s_j (IQ4_XS)
@@ -3102,9 +3125,11 @@ k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
     const int u = T - e->tile0;
     t = __builtin_amdgcn_readfirstlane(e->list ? (int)((KU32*)e->list)[u] : u);
   };
-  auto copy_tile = [&](KEntry* e, int t) -> int {  // as k_fused_tiles: the tile's own rows, the last copy masked
-    const int nrow = (int)((KU16*)e->M.rows)[t];
-    const uint4* src = reinterpret_cast<const uint4*>(e->M.words + ((KU32*)e->M.tbase)[t]) + lane;
+  auto copy_tile = [&](KEntry* e, int t, bool slot) -> int {  // as k_fused_tiles (a first copy takes the slot)
+    const int ts = e->M.tstride;
+    const int nrow = (slot && ts > 0) ? ts : (int)((KU16*)e->M.rows)[t];
+    const uint32_t* wt = e->M.words + (ts > 0 ? (size_t)32 * ts * t : (size_t)((KU32*)e->M.tbase)[t]);
+    const uint4* src = reinterpret_cast<const uint4*>(wt) + lane;
     const int nc = (nrow + 7) / 8;
     for (int i = 0; i < nc; ++i)
       if (lane < 8 * (nrow - 8 * i))
@@ -3124,19 +3149,21 @@ k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
   bool have = n < per && T0 + n < plan.ntiles;
   int sec = 0, t = 0, ncopy = 0;
   if (have) tile_of(n, sec, t);
-  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t);
+  if (have && wave < C) ncopy = copy_tile(sec ? eb : ea, t, true);
   wait_vmcnt_upto(ncopy);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (have && wave >= C) {
     ask((uint32_t)wave);
-    copy_tile(sec ? eb : ea, t);
+    copy_tile(sec ? eb : ea, t, true);
   }
-  if (wave == 0) {  // the block's row counts and word offsets into the scalar cache (read at each claim)
+  if (wave == W - 1) {  // the block's row counts (and word offsets) into the scalar cache, read at each claim, by
+                        // the wave whose first tile comes last
     uint32_t warm = 0;
     auto touch = [&](KEntry* e, int u0, int u1) {
       if (e->list) return;
-      for (int u = u0; u <= u1; u += 16) warm += ((KU32*)e->M.tbase)[u] + ((KU16*)e->M.rows)[u];
-      warm += ((KU32*)e->M.tbase)[u1] + ((KU16*)e->M.rows)[u1];
+      const bool tb = e->M.tstride == 0;
+      for (int u = u0; u <= u1; u += 16) warm += (tb ? ((KU32*)e->M.tbase)[u] : 0u) + ((KU16*)e->M.rows)[u];
+      warm += (tb ? ((KU32*)e->M.tbase)[u1] : 0u) + ((KU16*)e->M.rows)[u1];
     };
     touch(ea, T0 - ea->tile0, min(Tl, ea->tile0 + ea->ntile - 1) - ea->tile0);
     if (mb != ma) touch(eb, 0, Tl - eb->tile0);
@@ -3307,7 +3334,7 @@ k_fused_tiles_mma8(FlatPlan plan, int per, int buf_rows) {
       uint32_t k = 0;
       if (lane == 0) k = __hip_atomic_fetch_add(asked, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       ask((uint32_t)__builtin_amdgcn_readfirstlane((int)k));
-      copy_tile(sec ? eb : ea, t);
+      copy_tile(sec ? eb : ea, t, false);
     }
     float* out = E.P + (size_t)tc * mt * N + (size_t)tr * TN + (uint32_t)lane;
     f4v mac[NSB][NQ];
@@ -3442,7 +3469,8 @@ hipError_t launch_fused_tiles(const FlatPlan& p, int per, hipStream_t s) {
       return hipErrorInvalidValue;
   }
   const int rows = tiles_buf_rows(p);
-  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN > 160 * 1024) return hipErrorInvalidValue;
+  if (rows > 256 || (size_t)p.W * rows * 128 + (p.n > 1 ? 2 : 1) * 4 * LUTN + 4 * (4 + TILES_ROWC) > 160 * 1024)
+    return hipErrorInvalidValue;
   if (mixed) return tiles_launch_mixed(kqt, kqb, p, per, rows, s);
   switch (kqt) {
     case KQ_Q4_K: return tiles_launch<KQ_Q4_K>(p, per, rows, s);

@@ -251,7 +251,6 @@ void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits, B b
       r = std::max<uint32_t>(r, (uint32_t)((b + GUARD + 31) / 32));
     }
     L.rows[t] = (uint16_t)r;
-    L.tbase[t] = (uint32_t)nwords;
     nwords += (uint64_t)32 * r;
     L.max_rows = std::max<int>(L.max_rows, (int)r);
     // half-tile units: the first rows' bits end before each lane's mid (device bits, guard included); the second
@@ -266,6 +265,14 @@ void finish_layout(Layout& L, int T, const std::vector<uint64_t>& lane_bits, B b
     L.max_hrows = std::max<int>(L.max_hrows, (int)std::max<uint32_t>(r1, r - r0));
   }
   L.payload_bits = total;
+  // Tiles at a fixed stride of max_rows word rows when that pads the words by at most 1/8: a tile's place is then
+  // known without reading tbase (the whole-tile kernels' first copies); else back to back.
+  L.tstride = (uint64_t)T * L.max_rows * 32 <= nwords + nwords / 8 ? L.max_rows : 0;
+  if (L.tstride) nwords = (uint64_t)T * L.max_rows * 32;
+  for (uint64_t t = 0, o = 0; t < (uint64_t)T; ++t) {
+    L.tbase[t] = (uint32_t)(L.tstride ? 32 * L.tstride * t : o);
+    o += (uint64_t)32 * L.rows[t];
+  }
   L.words.assign(nwords + (uint64_t)32 * TAIL_ROWS, 0);
   parallel_for(T, threads, [&](int t0, int t1) {
     for (int t = t0; t < t1; ++t)

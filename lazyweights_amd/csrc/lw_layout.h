@@ -46,6 +46,9 @@ struct Layout {
   std::vector<uint32_t> exc;
   int nexc32 = 0;  // the first nexc32 exception tiles have a 32-row ring schedule (in sched)
   int max_rows = 0;
+  // > 0: tile t's rows start at word 32 tstride t (tstride = max_rows; tbase holds the same offsets); 0: tiles are
+  // back to back
+  int tstride = 0;
   int max_hrows = 0;  // max over tiles and halves of a half-tile unit's rows
   uint64_t payload_bits = 0;    // coded bits of all lanes
 };

@@ -360,6 +360,7 @@ bool make_resident(Model& M, Tensor& t, int threads) {
   dm.KT = t.KS() / lw::TK;
   dm.NT = (int)(t.N / lw::TN);
   dm.max_rows = L.max_rows;
+  dm.tstride = L.tstride;
   dm.max_hrows = L.max_hrows;
   if (t.kqt && !upload_side(M, t)) return false;
   t.resident = true;
@@ -609,7 +610,8 @@ int tiles_width(const lw::FlatPlan& fp, int mintiles, int& per) {
   const int cus = cu_count();
   const int rows = lw::tiles_buf_rows(fp), tables = (fp.n > 1 ? 2 : 1) * 4 * lw::LUTN;
   if (rows > 256) return 0;
-  const int wmax = std::min(fp.canon ? lw::TILES_CANON_WAVES : 16, (160 * 1024 - tables) / (rows * 128));
+  const int wmax = std::min(fp.canon ? lw::TILES_CANON_WAVES : 16,
+                            (160 * 1024 - tables - 4 * (4 + lw::TILES_ROWC)) / (rows * 128));
   if (wmax < 1) return 0;
   per = (fp.ntiles + cus - 1) / cus;
   if (fp.n > 1) per = std::min(per, mintiles);
