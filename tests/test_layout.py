@@ -329,6 +329,31 @@ def test_split_chain_emulation_exception_tiles(lib):
         assert np.array_equal(emulate_tiles(lut, tbase, split, rows, words, 128, 8192), sym)
 
 
+def test_tile_stride(lib):
+    """Tiles lie at a fixed stride of max(rows) word rows when that pads the words by at most 1/8, else back to back;
+    either way tbase holds the offsets, the words end 16 zero rows past the last slot, and the chains decode the same
+    symbols (a config-2-like matrix takes the stride; a matrix with one tile of twice the rows does not)."""
+    from lazyweights_amd import bundle
+    cases = [bundle.synth_matrix(1, 256, 2048, 2.3, 11)[0], skewed_tile_codes()[0]]
+    for kqt, codes in zip((1, 2), cases):
+        sym = bundle.form_symbols(kqt, codes)
+        blob, _ = bundle.encode_huf8(sym)
+        N, KS = sym.shape
+        tbase, split, rows, words = build_layout(lib, blob, N, KS, splits=True)
+        r = rows.astype(np.int64)
+        T = len(r)
+        fixed = T * r.max() * 32 <= r.sum() * 32 + (r.sum() * 32) // 8
+        want = 32 * r.max() * np.arange(T) if fixed else np.concatenate([[0], np.cumsum(32 * r)[:-1]])
+        assert np.array_equal(tbase.astype(np.int64), want)
+        assert len(words) == (T * r.max() if fixed else r.sum()) * 32 + 16 * 32
+        assert fixed == (kqt == 1)
+        if fixed:  # the rows past a tile's own are zeros
+            for t in range(T):
+                assert not words[int(tbase[t]) + 32 * int(r[t]):int(tbase[t]) + 32 * int(r.max())].any()
+        lut = np.frombuffer(blob, np.uint16, 2048, 0)
+        assert np.array_equal(emulate_tiles(lut, tbase, split, rows, words, N, KS), sym)
+
+
 @pytest.mark.parametrize("case", golden_cases())
 def test_ring_schedule_emulation(lib, case):
     g = load_golden(case)
