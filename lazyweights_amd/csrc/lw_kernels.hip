@@ -1674,12 +1674,13 @@ constexpr int TILES_COPIES = LW_TILES_COPIES;
 // ahead of the waves' first tile copies, so a wave waits only for those before the block's barrier; at most
 // TILES_COPIES copies are in flight per block. The next tile's copy is issued as soon as a decode ends, before
 // the row partial is formed; the tiles' row counts and word offsets, read at that point, were brought into the
-// scalar cache at the start.
+// scalar cache at the start (a wave's first copy of a fixed-stride matrix reads neither: it copies the tile's slot).
 // A tile's word rows are copied whole into the wave's LDS buffer with direct-to-LDS loads (1 KB per instruction);
 // lane l then decodes tile row l (lane stream l % 32, its row l / 32) as 8 chains of 32 symbols that start at the
 // load-time split offsets and run interleaved instruction by instruction, so their LDS round trips overlap. A
-// chain keeps its window rows in registers and reads one new row word per pair (LDS instruction issue, about 4
-// cycles per wave-wide read, is what a tile costs: 2 table gathers and 1 row read per pair).
+// chain keeps its window rows in registers and reads one new row word per pair (per pair of symbols 2 table
+// gathers, 1 row read and 14 VALU instructions; the gathers' bank conflicts and the VALU issue co-limit a tile).
+// A tile row whose tiles are all the block's own is counted in LDS; the others in the entry's counter.
 // There is no ring and no staging schedule: every tile of the matrices, exception tiles included, is decoded here.
 // The lane keeps its row's sub-block dot products in registers and forms the row partial in tile_gemv's order
 // (tile_gemv_i8's for int8 activations), the bits of the other kernels.
@@ -3964,36 +3965,50 @@ __global__ void __launch_bounds__(256) k_decode_split(DevMat M, uint8_t* __restr
   __syncthreads();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, l = lane & 31, f = lane >> 5;
+  // the lane decodes symbols 64 k .. 64 k + 63 of its lane stream as two chains of 32 from the split offsets
+  // 2 k and 2 k + 1, interleaved step by step so that their LDS round trips overlap
   const int k = 4 * f + wave;
-  uint32_t P = (uint32_t)M.split[((size_t)t * SPLITS + k * (SPLITS / 8)) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
   const uint32_t tsel = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint32_t*)lut4;
   uint32_t tmask = 0x1FFCu;
   asm volatile("" : "+v"(tmask));
   const uint32_t rlb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)(tw + l);
-  uint32_t slot = __builtin_amdgcn_ubfe(P, 5, 8);
-  uint32_t A = *(LdsU32*)(rlb + ((slot - 2u) << 7));
-  uint32_t B = *(LdsU32*)(rlb + ((slot - 1u) << 7));
-  uint32_t C = *(LdsU32*)(rlb + (slot << 7));
+  uint32_t P[2], slot[2], A[2], B[2], C[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    P[c] = (uint32_t)M.split[((size_t)t * SPLITS + 2 * k + c) * 32 + (uint32_t)l] - GUARD_BITS + 64u;
+    slot[c] = __builtin_amdgcn_ubfe(P[c], 5, 8);
+    A[c] = *(LdsU32*)(rlb + ((slot[c] - 2u) << 7));
+    B[c] = *(LdsU32*)(rlb + ((slot[c] - 1u) << 7));
+    C[c] = *(LdsU32*)(rlb + (slot[c] << 7));
+  }
   uint8_t* const wbuf = rowbuf + wave * 64 * RSTR;     // the wave's 64 code rows
   uint8_t* rb = wbuf + (f * 32 + l) * RSTR;              // the lane's row
 #pragma unroll 4
-  for (int p = 0; p < 32; ++p) {
-    const uint32_t w1 = __builtin_amdgcn_alignbit(B, A, P);
-    const uint32_t e1 = *(LdsU32*)table_addr(w1, tsel, tmask);
-    const uint32_t w2 = w1 >> (e1 & 31u);
-    const uint32_t e2 = *(LdsU32*)table_addr(w2, tsel, tmask);
-    P = P + e1 + e2;
-    const uint32_t nslot = __builtin_amdgcn_ubfe(P, 5, 8);
-    const bool slide = nslot != slot;
-    A = slide ? B : A;
-    B = slide ? C : B;
-    slot = nslot;
-    C = *(LdsU32*)(rlb + (nslot << 7));
-    const uint32_t s1 = e1 >> 16, s2 = e2 >> 16;
-    if (SYMB == 4)  // codes low nibble first: 4 bytes per pair
-      *reinterpret_cast<uint32_t*>(rb + 4 * p) = (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
-    else
-      *reinterpret_cast<uint16_t*>(rb + 2 * p) = (uint16_t)(s1 | s2 << 8);
+  for (int p = 0; p < 16; ++p) {
+    uint32_t w1[2], e1[2], e2[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      w1[c] = __builtin_amdgcn_alignbit(B[c], A[c], P[c]);
+      e1[c] = *(LdsU32*)table_addr(w1[c], tsel, tmask);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) e2[c] = *(LdsU32*)table_addr(w1[c] >> (e1[c] & 31u), tsel, tmask);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      P[c] = P[c] + e1[c] + e2[c];
+      const uint32_t nslot = __builtin_amdgcn_ubfe(P[c], 5, 8);
+      const bool slide = nslot != slot[c];
+      A[c] = slide ? B[c] : A[c];
+      B[c] = slide ? C[c] : B[c];
+      slot[c] = nslot;
+      C[c] = *(LdsU32*)(rlb + (nslot << 7));
+      const uint32_t s1 = e1[c] >> 16, s2 = e2[c] >> 16;
+      if (SYMB == 4)  // codes low nibble first: 4 bytes per pair
+        *reinterpret_cast<uint32_t*>(rb + 64 * c + 4 * p) =
+            (s1 & 15u) | (s1 >> 4) << 8 | (s2 & 15u) << 16 | (s2 >> 4) << 24;
+      else
+        *reinterpret_cast<uint16_t*>(rb + 32 * c + 2 * p) = (uint16_t)(s1 | s2 << 8);
+    }
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
